@@ -1,0 +1,209 @@
+/*
+ * mitten_kv.h — C ABI of the MI355X paged-KV library (libmitten_kv.so).
+ *
+ * The library owns the device KV pool (the inference backend's device-buffer
+ * type) and runs the four data-plane operations of the engine's paged-KV path
+ * as hand-written gfx950 HIP kernels:
+ *
+ *   append            scatter new K/V rows into block slots (slot mapping)
+ *   gather            block table -> contiguous per-sequence K/V
+ *   copy_blocks       copy-on-write block copies and batched block moves
+ *   decode_attention  GQA/MQA paged decode attention straight from the pool
+ *
+ * Pool layout in HBM (design/rust-inference-engine-design.md:1380-1387):
+ *   [num_layers][2 (K then V)][num_blocks][page_size][num_kv_heads][head_dim]
+ * A slot id is block * page_size + offset_in_block.
+ *
+ * Conventions
+ *   - Every function returns an mkv_status (0 = MKV_OK). On failure a message
+ *     is available from mkv_last_error() (thread-local). No C++ exception and
+ *     no abort crosses this boundary.
+ *   - Pointers named d_* are device pointers (HBM), 16-byte aligned. Metadata
+ *     arrays (slot mappings, block tables, context lengths) are device int32.
+ *     The mkv_validate_* functions check the same arrays on the host.
+ *   - Kernels bound-check every slot and block id they dereference against
+ *     the pool; an out-of-range id is skipped (never dereferenced) and
+ *     recorded in the pool's device error word, read by mkv_pool_check().
+ *   - `stream` is a hipStream_t (NULL = the null stream). Operations are
+ *     asynchronous on that stream. A pool is not thread-safe: one caller
+ *     thread at a time (the engine drives it from its single GPU thread,
+ *     inference-api/src/main.rs:84-91).
+ */
+#ifndef MITTEN_KV_H
+#define MITTEN_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifndef MKV_API
+#define MKV_API __attribute__((visibility("default")))
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. Mapping onto the engine's error type
+ * (inference-backend/src/error.rs:3-13):
+ *   MKV_ERR_OUT_OF_MEMORY -> EngineError::OutOfKvPages
+ *   everything else       -> EngineError::Backend(mkv_last_error()) */
+typedef enum {
+  MKV_OK = 0,
+  MKV_ERR_INVALID_ARGUMENT = 1,
+  MKV_ERR_OUT_OF_MEMORY = 2,
+  MKV_ERR_HIP = 3,
+  MKV_ERR_DEVICE_INDEX = 4, /* a kernel met an out-of-range id (mkv_pool_check) */
+  MKV_ERR_NO_DEVICE = 5
+} mkv_status;
+
+typedef enum { MKV_DTYPE_F32 = 0, MKV_DTYPE_BF16 = 1 } mkv_dtype;
+
+/* Bits of the device error word (mkv_pool_check). */
+enum {
+  MKV_DEVERR_SLOT = 1u << 0,        /* append: slot id outside the pool */
+  MKV_DEVERR_BLOCK = 1u << 1,       /* gather/attention: block id outside the pool */
+  MKV_DEVERR_TABLE = 1u << 2,       /* block table shorter than ceil(ctx/page_size) */
+  MKV_DEVERR_COPY = 1u << 3,        /* copy_blocks: src or dst outside the pool */
+  MKV_DEVERR_CTX = 1u << 4          /* context length < 1 or > the max_ctx_len given */
+};
+
+/* decode_attention flags. */
+enum {
+  MKV_ATTN_ZERO_SINK = 1u << 0,  /* add the reference's phantom zero key/value:
+                                    inference-model-qwen/src/model.rs:210-213 */
+  MKV_ATTN_FORCE_VALU = 1u << 1, /* use the VALU kernel even where MFMA applies */
+  MKV_ATTN_FORCE_MFMA = 1u << 2  /* fail unless the MFMA kernel applies */
+};
+
+typedef struct mkv_pool mkv_pool;
+
+/* Pool descriptor. Extends the engine's ModelConfig
+ * (inference-backend/src/config.rs:1-11: num_layers, num_kv_heads, head_dim)
+ * with num_q_heads, which ModelConfig lacks, and the pool sizing of
+ * EngineConfig (inference-engine/src/config.rs:3-17: num_kv_pages, page_size). */
+typedef struct {
+  int32_t num_layers;
+  int32_t num_kv_heads;
+  int32_t num_q_heads;  /* multiple of num_kv_heads */
+  int32_t head_dim;     /* multiple of 8, at most 512 */
+  int32_t page_size;    /* tokens per block; must be 16 */
+  int32_t dtype;        /* mkv_dtype */
+  int64_t num_blocks;   /* pages in the pool */
+} mkv_pool_desc;
+
+/* ---- pool lifecycle ------------------------------------------------------ */
+
+/* Bytes of the pool: 2*L*blocks*page_size*Hkv*D*dtype_bytes.
+ * Replaces KvCachePool::required_bytes (inference-engine/src/kv_pool.rs:58-68). */
+MKV_API int mkv_pool_required_bytes(const mkv_pool_desc *desc, uint64_t *out_bytes);
+
+/* Allocate the device pool on `device` (hipMalloc; contents uninitialised).
+ * Replaces the device half of KvCachePool::new (kv_pool.rs:18-27) and the
+ * design's KvBufferHandle (design/phase0-deliverable.md:1320-1332).
+ * MKV_ERR_OUT_OF_MEMORY if HBM cannot hold it. */
+MKV_API int mkv_pool_create(const mkv_pool_desc *desc, int device, mkv_pool **out_pool);
+MKV_API int mkv_pool_destroy(mkv_pool *pool);
+MKV_API int mkv_pool_get_desc(const mkv_pool *pool, mkv_pool_desc *out_desc);
+/* Device base address and size of the pool buffer (for host read-back). */
+MKV_API int mkv_pool_buffer(const mkv_pool *pool, void **out_dev_ptr, uint64_t *out_bytes);
+
+/* Synchronise `stream`, then read and clear the device error word.
+ * Returns MKV_ERR_DEVICE_INDEX if any bit was set (bits in *out_bits). */
+MKV_API int mkv_pool_check(mkv_pool *pool, void *stream, uint32_t *out_bits);
+
+/* ---- data-plane operations ----------------------------------------------- */
+
+/* Append num_tokens K/V rows into `layer`:
+ *   pool[layer][K][s/ps][s%ps] = d_k[t],  pool[layer][V][s/ps][s%ps] = d_v[t],
+ *   s = d_slot_mapping[t].
+ * d_k, d_v: [num_tokens][num_kv_heads][head_dim] in the pool dtype.
+ * Replaces the per-layer Tensor::cat append
+ * (inference-model-qwen/src/model.rs:390-392). */
+MKV_API int mkv_append(mkv_pool *pool, int32_t layer, const void *d_k, const void *d_v,
+               const int32_t *d_slot_mapping, int32_t num_tokens, void *stream);
+
+/* All layers in one launch: d_k, d_v are [num_layers][num_tokens][Hkv][D];
+ * the same slot mapping applies to every layer. */
+MKV_API int mkv_append_all_layers(mkv_pool *pool, const void *d_k, const void *d_v,
+                          const int32_t *d_slot_mapping, int32_t num_tokens, void *stream);
+
+/* Gather: for each sequence b, its first n_b = d_ctx_indptr[b+1]-d_ctx_indptr[b]
+ * tokens, found through the block table
+ * d_block_ids[d_block_indptr[b] .. d_block_indptr[b+1]), are written as
+ * [num_kv_heads][n_b][head_dim] at element offset d_ctx_indptr[b]*Hkv*D of
+ * d_out_k / d_out_v (the KVCacheState layout [batch, heads, seq, head_dim],
+ * inference-model-common/src/lib.rs:5-8). max_ctx_len bounds every n_b;
+ * out_capacity_tokens (tokens the outputs hold) bounds d_ctx_indptr[b+1]:
+ * a sequence that would overflow is skipped and reported (MKV_DEVERR_CTX).
+ * Implements the design's gather-then-attend copy
+ * (design/phase0-deliverable.md:278; CSR kv_indptr/kv_indices,
+ * design/rust-inference-engine-design.md:1505-1534). */
+MKV_API int mkv_gather(mkv_pool *pool, int32_t layer, const int32_t *d_block_indptr,
+                       const int32_t *d_block_ids, const int32_t *d_ctx_indptr, int32_t num_seqs,
+                       int32_t max_ctx_len, void *d_out_k, void *d_out_v,
+                       int64_t out_capacity_tokens, void *stream);
+
+/* Copy whole blocks, all layers, K and V: pool[*][*][dst[i]] = pool[*][*][src[i]].
+ * The result is defined when no block id is both a source and a destination
+ * and destinations are distinct (mkv_validate_copy_pairs). Serves copy-on-write
+ * of a shared partial block and the batched moves of pool compaction; the
+ * reference has no counterpart (it aliases shared pages, prefill.rs:60-71). */
+MKV_API int mkv_copy_blocks(mkv_pool *pool, const int32_t *d_src_blocks, const int32_t *d_dst_blocks,
+                    int32_t num_pairs, void *stream);
+
+/* Paged decode attention for one layer, one query row per sequence:
+ *   O[b][h] = softmax(scale * Q[b][h] . K_b^T) . V_b
+ * over the first d_ctx_lens[b] tokens of sequence b (block table CSR as in
+ * mkv_gather), query head h reading KV head h / (num_q_heads/num_kv_heads).
+ * d_q, d_o: [num_seqs][num_q_heads][head_dim] in the pool dtype; accumulation
+ * is f32. max_ctx_len >= every d_ctx_lens[b] >= 1 sizes the launch.
+ * split_tokens: context tokens per split-K partition (multiple of page_size),
+ * 0 = chosen by the library. Workspace: device scratch of at least
+ * mkv_decode_attention_workspace_size() bytes, or NULL to use a pool-owned
+ * buffer (grown on demand). Replaces model.rs:394-416 (repeat_kv, q.k^T*scaling,
+ * mask, softmax, .v). */
+MKV_API int mkv_decode_attention(mkv_pool *pool, int32_t layer, const void *d_q, void *d_o,
+                         const int32_t *d_block_indptr, const int32_t *d_block_ids,
+                         const int32_t *d_ctx_lens, int32_t num_seqs, int32_t max_ctx_len,
+                         float scale, uint32_t flags, int32_t split_tokens, void *d_workspace,
+                         uint64_t workspace_bytes, void *stream);
+
+MKV_API int mkv_decode_attention_workspace_size(const mkv_pool *pool, int32_t num_seqs,
+                                        int32_t max_ctx_len, int32_t split_tokens,
+                                        uint64_t *out_bytes);
+
+/* ---- host-side validation (pure CPU; no device access) ------------------- */
+
+/* 0 <= slot < num_blocks*page_size for every slot. */
+MKV_API int mkv_validate_slots(const mkv_pool_desc *desc, const int32_t *slots, int32_t n);
+/* indptr monotone, ids in range, table b holds >= ceil(ctx_b/page_size) ids,
+ * 1 <= ctx_b <= max_ctx_len. ctx_lens may be NULL (tables only). */
+MKV_API int mkv_validate_block_tables(const mkv_pool_desc *desc, const int32_t *indptr,
+                              const int32_t *ids, const int32_t *ctx_lens, int32_t num_seqs,
+                              int32_t max_ctx_len);
+/* ids in range, destinations distinct, no id both source and destination. */
+MKV_API int mkv_validate_copy_pairs(const mkv_pool_desc *desc, const int32_t *src, const int32_t *dst,
+                            int32_t n);
+
+/* ---- device buffers (the backend's device-buffer type) ------------------- */
+
+MKV_API int mkv_buffer_alloc(int device, uint64_t bytes, void **out_dev_ptr);
+MKV_API int mkv_buffer_free(void *dev_ptr);
+/* Host -> device on `stream`; the host buffer must stay valid until the
+ * stream reaches this point. */
+MKV_API int mkv_memcpy_h2d(void *d_dst, const void *h_src, uint64_t bytes, void *stream);
+/* Device -> host on `stream`, synchronous on return. */
+MKV_API int mkv_memcpy_d2h(void *h_dst, const void *d_src, uint64_t bytes, void *stream);
+MKV_API int mkv_stream_synchronize(void *stream);
+
+/* ---- diagnostics --------------------------------------------------------- */
+
+MKV_API const char *mkv_last_error(void);
+/* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
+MKV_API int mkv_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MITTEN_KV_H */

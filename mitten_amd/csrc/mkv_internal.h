@@ -1,0 +1,92 @@
+// Internal definitions shared by the libmitten_kv translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/mitten_kv.h"
+
+namespace mkv {
+
+constexpr int kPageSize = 16;
+constexpr int kWave = 64;
+
+// Pool geometry in bytes. Layout: [L][2][blocks][page][Hkv][D].
+struct Geom {
+  int32_t L, Hkv, Hq, D, ps, dtype;
+  int64_t nblocks;
+  int32_t es;          // element bytes
+  int64_t row_bytes;   // one token, all KV heads: Hkv*D*es
+  int64_t block_bytes; // ps * row_bytes
+  int64_t plane_bytes; // nblocks * block_bytes (one layer, K or V)
+};
+
+struct Pool {
+  mkv_pool_desc desc;
+  Geom g;
+  int device = 0;
+  uint8_t *data = nullptr;   // pool buffer
+  uint64_t bytes = 0;
+  uint32_t *d_err = nullptr; // device error word
+  void *ws = nullptr;        // pool-owned attention workspace
+  uint64_t ws_bytes = 0;
+};
+
+// Thread-local last-error message and status helpers.
+int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int hip_fail(hipError_t e, const char *what);
+
+// Sets the pool's device current for the lifetime of the guard.
+struct DeviceGuard {
+  int prev = -1;
+  bool ok = true;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != dev) ok = hipSetDevice(dev) == hipSuccess;
+  }
+  ~DeviceGuard() {
+    int cur = -1;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+  }
+};
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+#define MKV_CHECK_HIP(expr)                      \
+  do {                                           \
+    hipError_t e_ = (expr);                      \
+    if (e_ != hipSuccess) return ::mkv::hip_fail(e_, #expr); \
+  } while (0)
+
+// After a kernel launch.
+#define MKV_CHECK_LAUNCH(name)                   \
+  do {                                           \
+    hipError_t e_ = hipGetLastError();           \
+    if (e_ != hipSuccess) return ::mkv::hip_fail(e_, name); \
+  } while (0)
+
+// ---- device helpers -------------------------------------------------------
+
+__device__ __forceinline__ void record_error(uint32_t *d_err, uint32_t bit) {
+  atomicOr(d_err, bit);
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// f32 -> bf16 bits, round to nearest even (NaN kept NaN).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+}
+
+}  // namespace mkv

@@ -1,0 +1,453 @@
+// Device KV pool, KV data movement kernels (append, gather, copy_blocks),
+// host-side validators, device buffers and the error API of libmitten_kv.
+//
+// All three movement kernels are pure HBM streams: every thread moves whole
+// 16-byte chunks (global_load_dwordx4 / global_store_dwordx4), consecutive
+// lanes touch consecutive chunks of one contiguous row or block, and every
+// slot / block id is range-checked before it is dereferenced.
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "mkv_internal.h"
+
+namespace mkv {
+
+static thread_local std::string g_last_error;
+
+int set_error(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+  int code = (e == hipErrorOutOfMemory) ? MKV_ERR_OUT_OF_MEMORY : MKV_ERR_HIP;
+  return set_error(code, "%s failed: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+static int validate_desc(const mkv_pool_desc *d) {
+  if (!d) return set_error(MKV_ERR_INVALID_ARGUMENT, "desc is NULL");
+  if (d->num_layers < 1 || d->num_kv_heads < 1 || d->num_q_heads < 1 || d->num_blocks < 1)
+    return set_error(MKV_ERR_INVALID_ARGUMENT,
+                     "num_layers, num_kv_heads, num_q_heads and num_blocks must be >= 1");
+  if (d->num_q_heads % d->num_kv_heads)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "num_q_heads (%d) is not a multiple of num_kv_heads (%d)",
+                     d->num_q_heads, d->num_kv_heads);
+  if (d->head_dim < 8 || d->head_dim > 512 || d->head_dim % 8)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "head_dim (%d) must be a multiple of 8 in [8, 512]",
+                     d->head_dim);
+  if (d->page_size != kPageSize)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "page_size must be %d (got %d)", kPageSize,
+                     d->page_size);
+  if (d->dtype != MKV_DTYPE_F32 && d->dtype != MKV_DTYPE_BF16)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "unknown dtype %d", d->dtype);
+  if (d->num_blocks > (int64_t)INT32_MAX / kPageSize)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "num_blocks too large for int32 slot ids");
+  return MKV_OK;
+}
+
+static Geom make_geom(const mkv_pool_desc *d) {
+  Geom g;
+  g.L = d->num_layers;
+  g.Hkv = d->num_kv_heads;
+  g.Hq = d->num_q_heads;
+  g.D = d->head_dim;
+  g.ps = d->page_size;
+  g.dtype = d->dtype;
+  g.nblocks = d->num_blocks;
+  g.es = d->dtype == MKV_DTYPE_F32 ? 4 : 2;
+  g.row_bytes = (int64_t)g.Hkv * g.D * g.es;
+  g.block_bytes = g.ps * g.row_bytes;
+  g.plane_bytes = g.nblocks * g.block_bytes;
+  return g;
+}
+
+// ---- kernels ------------------------------------------------------------------
+
+// grid.x covers num_tokens * 2 * chunks_per_row 16-byte chunks; grid.y = layers.
+__global__ void __launch_bounds__(256)
+append_kernel(uint8_t *__restrict__ pool, int32_t layer0, const uint4 *__restrict__ k,
+              const uint4 *__restrict__ v, const int32_t *__restrict__ slots, int32_t n_tok,
+              int64_t src_layer_stride, Geom g, uint32_t *__restrict__ d_err) {
+  const int cpr = (int)(g.row_bytes >> 4);
+  const int64_t total = (int64_t)n_tok * 2 * cpr;
+  const int64_t nslots = g.nblocks * g.ps;
+  const int layer = layer0 + (int)blockIdx.y;
+  uint8_t *layer_base = pool + (int64_t)layer * 2 * g.plane_bytes;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = i / (2 * cpr);
+    const int rem = (int)(i - t * 2 * cpr);
+    const int kv = rem >= cpr;
+    const int c = rem - kv * cpr;
+    const int32_t s = slots[t];
+    if (s < 0 || s >= nslots) {
+      if (c == 0 && kv == 0) record_error(d_err, MKV_DEVERR_SLOT);
+      continue;
+    }
+    const uint4 *src = (kv ? v : k) + (int64_t)blockIdx.y * src_layer_stride + t * cpr + c;
+    uint8_t *dst = layer_base + kv * g.plane_bytes + (int64_t)(s / kPageSize) * g.block_bytes +
+                   (int64_t)(s % kPageSize) * g.row_bytes;
+    reinterpret_cast<uint4 *>(dst)[c] = *src;
+  }
+}
+
+// grid.x = block index within a sequence, grid.y = sequence.
+__global__ void __launch_bounds__(256)
+gather_kernel(const uint8_t *__restrict__ pool, int32_t layer, const int32_t *__restrict__ indptr,
+              const int32_t *__restrict__ ids, const int32_t *__restrict__ ctx_indptr,
+              int32_t max_ctx, uint8_t *__restrict__ out_k, uint8_t *__restrict__ out_v,
+              int64_t out_cap, Geom g, uint32_t *__restrict__ d_err) {
+  const int b = blockIdx.y, j = blockIdx.x, tid = threadIdx.x;
+  const int64_t c0 = ctx_indptr[b];
+  const int64_t n = (int64_t)ctx_indptr[b + 1] - c0;
+  if (n < 0 || n > max_ctx || c0 < 0 || c0 + n > out_cap) {
+    if (j == 0 && tid == 0) record_error(d_err, MKV_DEVERR_CTX);
+    return;
+  }
+  const int64_t t0 = (int64_t)j * kPageSize;
+  if (t0 >= n) return;
+  const int64_t tab0 = indptr[b];
+  const int64_t tabn = (int64_t)indptr[b + 1] - tab0;
+  if (tabn < (n + kPageSize - 1) / kPageSize || tab0 < 0) {
+    if (j == 0 && tid == 0) record_error(d_err, MKV_DEVERR_TABLE);
+    return;
+  }
+  const int32_t blk = ids[tab0 + j];
+  if (blk < 0 || blk >= g.nblocks) {
+    if (tid == 0) record_error(d_err, MKV_DEVERR_BLOCK);
+    return;
+  }
+  const int nt = (int)min<int64_t>(kPageSize, n - t0);
+  const int cph = (g.D * g.es) >> 4;  // 16-byte chunks per head row
+  const int total = nt * g.Hkv * cph;
+  for (int kv = 0; kv < 2; kv++) {
+    const uint4 *src = reinterpret_cast<const uint4 *>(
+        pool + ((int64_t)layer * 2 + kv) * g.plane_bytes + (int64_t)blk * g.block_bytes);
+    uint8_t *out = kv ? out_v : out_k;
+    for (int c = tid; c < total; c += blockDim.x) {
+      const int t = c / (g.Hkv * cph);
+      const int h = (c / cph) % g.Hkv;
+      const int cc = c % cph;
+      const int64_t elem = (c0 * g.Hkv + (int64_t)h * n + t0 + t) * g.D;
+      reinterpret_cast<uint4 *>(out + elem * g.es)[cc] = src[c];
+    }
+  }
+}
+
+// grid.x = pair, grid.y = plane (layer * 2 + kv).
+__global__ void __launch_bounds__(256)
+copy_blocks_kernel(uint8_t *__restrict__ pool, const int32_t *__restrict__ src,
+                   const int32_t *__restrict__ dst, Geom g, uint32_t *__restrict__ d_err) {
+  const int i = blockIdx.x, plane = blockIdx.y, tid = threadIdx.x;
+  const int32_t s = src[i], d = dst[i];
+  if (s < 0 || s >= g.nblocks || d < 0 || d >= g.nblocks) {
+    if (plane == 0 && tid == 0) record_error(d_err, MKV_DEVERR_COPY);
+    return;
+  }
+  const uint4 *sp = reinterpret_cast<const uint4 *>(pool + plane * g.plane_bytes + s * g.block_bytes);
+  uint4 *dp = reinterpret_cast<uint4 *>(pool + plane * g.plane_bytes + d * g.block_bytes);
+  const int n = (int)(g.block_bytes >> 4);
+  const int bd = blockDim.x;
+  // Issue four loads before the four stores so each lane keeps 64 B in flight.
+  for (int base = tid; base < n; base += 4 * bd) {
+    uint4 r[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+      if (base + u * bd < n) r[u] = sp[base + u * bd];
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+      if (base + u * bd < n) dp[base + u * bd] = r[u];
+  }
+}
+
+}  // namespace mkv
+
+using namespace mkv;
+
+// ---- C ABI: pool lifecycle -------------------------------------------------------
+
+extern "C" int mkv_pool_required_bytes(const mkv_pool_desc *desc, uint64_t *out_bytes) {
+  int rc = validate_desc(desc);
+  if (rc) return rc;
+  if (!out_bytes) return set_error(MKV_ERR_INVALID_ARGUMENT, "out_bytes is NULL");
+  Geom g = make_geom(desc);
+  *out_bytes = (uint64_t)2 * g.L * (uint64_t)g.plane_bytes;
+  return MKV_OK;
+}
+
+extern "C" int mkv_pool_create(const mkv_pool_desc *desc, int device, mkv_pool **out_pool) {
+  int rc = validate_desc(desc);
+  if (rc) return rc;
+  if (!out_pool) return set_error(MKV_ERR_INVALID_ARGUMENT, "out_pool is NULL");
+  *out_pool = nullptr;
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0)
+    return set_error(MKV_ERR_NO_DEVICE, "no HIP device available");
+  if (device < 0 || device >= ndev)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "device %d out of range (%d devices)", device, ndev);
+  DeviceGuard guard(device);
+  if (!guard.ok) return set_error(MKV_ERR_HIP, "hipSetDevice(%d) failed", device);
+  Pool *p = new (std::nothrow) Pool();
+  if (!p) return set_error(MKV_ERR_OUT_OF_MEMORY, "host allocation failed");
+  p->desc = *desc;
+  p->g = make_geom(desc);
+  p->device = device;
+  p->bytes = (uint64_t)2 * p->g.L * (uint64_t)p->g.plane_bytes;
+  hipError_t e = hipMalloc(reinterpret_cast<void **>(&p->data), p->bytes);
+  if (e != hipSuccess) {
+    delete p;
+    (void)hipGetLastError();
+    return set_error(e == hipErrorOutOfMemory ? MKV_ERR_OUT_OF_MEMORY : MKV_ERR_HIP,
+                     "pool allocation of %llu bytes failed: %s", (unsigned long long)p->bytes,
+                     hipGetErrorString(e));
+  }
+  e = hipMalloc(reinterpret_cast<void **>(&p->d_err), 256);
+  if (e == hipSuccess) e = hipMemset(p->d_err, 0, 256);
+  if (e != hipSuccess) {
+    (void)hipFree(p->data);
+    if (p->d_err) (void)hipFree(p->d_err);
+    delete p;
+    return hip_fail(e, "error word allocation");
+  }
+  *out_pool = reinterpret_cast<mkv_pool *>(p);
+  return MKV_OK;
+}
+
+extern "C" int mkv_pool_destroy(mkv_pool *pool) {
+  if (!pool) return MKV_OK;
+  Pool *p = reinterpret_cast<Pool *>(pool);
+  DeviceGuard guard(p->device);
+  (void)hipDeviceSynchronize();
+  if (p->ws) (void)hipFree(p->ws);
+  (void)hipFree(p->d_err);
+  (void)hipFree(p->data);
+  delete p;
+  return MKV_OK;
+}
+
+extern "C" int mkv_pool_get_desc(const mkv_pool *pool, mkv_pool_desc *out_desc) {
+  if (!pool || !out_desc) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL argument");
+  *out_desc = reinterpret_cast<const Pool *>(pool)->desc;
+  return MKV_OK;
+}
+
+extern "C" int mkv_pool_buffer(const mkv_pool *pool, void **out_dev_ptr, uint64_t *out_bytes) {
+  if (!pool) return set_error(MKV_ERR_INVALID_ARGUMENT, "pool is NULL");
+  const Pool *p = reinterpret_cast<const Pool *>(pool);
+  if (out_dev_ptr) *out_dev_ptr = p->data;
+  if (out_bytes) *out_bytes = p->bytes;
+  return MKV_OK;
+}
+
+extern "C" int mkv_pool_check(mkv_pool *pool, void *stream, uint32_t *out_bits) {
+  if (!pool) return set_error(MKV_ERR_INVALID_ARGUMENT, "pool is NULL");
+  Pool *p = reinterpret_cast<Pool *>(pool);
+  DeviceGuard guard(p->device);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  uint32_t bits = 0;
+  MKV_CHECK_HIP(hipStreamSynchronize(s));
+  MKV_CHECK_HIP(hipMemcpy(&bits, p->d_err, sizeof(bits), hipMemcpyDeviceToHost));
+  if (bits) MKV_CHECK_HIP(hipMemset(p->d_err, 0, sizeof(bits)));
+  if (out_bits) *out_bits = bits;
+  if (bits)
+    return set_error(MKV_ERR_DEVICE_INDEX, "kernel met out-of-range ids (error bits 0x%x)", bits);
+  return MKV_OK;
+}
+
+// ---- C ABI: data movement -----------------------------------------------------------
+
+static int check_layer(const Pool *p, int32_t layer) {
+  if (layer < 0 || layer >= p->g.L)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "layer %d out of range [0, %d)", layer, p->g.L);
+  return MKV_OK;
+}
+
+static int launch_append(Pool *p, int32_t layer0, int32_t nlayers, const void *d_k,
+                         const void *d_v, const int32_t *d_slots, int32_t n, void *stream) {
+  if (n < 0) return set_error(MKV_ERR_INVALID_ARGUMENT, "num_tokens < 0");
+  if (n == 0) return MKV_OK;
+  if (!d_k || !d_v || !d_slots) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL device pointer");
+  if (!aligned16(d_k) || !aligned16(d_v))
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "K/V source must be 16-byte aligned");
+  DeviceGuard guard(p->device);
+  const int64_t cpr = p->g.row_bytes >> 4;
+  const int64_t total = (int64_t)n * 2 * cpr;
+  const int threads = 256;
+  const int64_t blocks = std::min<int64_t>((total + threads - 1) / threads, 65536);
+  hipLaunchKernelGGL(append_kernel, dim3((unsigned)blocks, (unsigned)nlayers), dim3(threads), 0,
+                     reinterpret_cast<hipStream_t>(stream), p->data, layer0,
+                     reinterpret_cast<const uint4 *>(d_k), reinterpret_cast<const uint4 *>(d_v),
+                     d_slots, n, (int64_t)n * cpr, p->g, p->d_err);
+  MKV_CHECK_LAUNCH("append_kernel");
+  return MKV_OK;
+}
+
+extern "C" int mkv_append(mkv_pool *pool, int32_t layer, const void *d_k, const void *d_v,
+                          const int32_t *d_slot_mapping, int32_t num_tokens, void *stream) {
+  if (!pool) return set_error(MKV_ERR_INVALID_ARGUMENT, "pool is NULL");
+  Pool *p = reinterpret_cast<Pool *>(pool);
+  int rc = check_layer(p, layer);
+  if (rc) return rc;
+  return launch_append(p, layer, 1, d_k, d_v, d_slot_mapping, num_tokens, stream);
+}
+
+extern "C" int mkv_append_all_layers(mkv_pool *pool, const void *d_k, const void *d_v,
+                                     const int32_t *d_slot_mapping, int32_t num_tokens,
+                                     void *stream) {
+  if (!pool) return set_error(MKV_ERR_INVALID_ARGUMENT, "pool is NULL");
+  Pool *p = reinterpret_cast<Pool *>(pool);
+  return launch_append(p, 0, p->g.L, d_k, d_v, d_slot_mapping, num_tokens, stream);
+}
+
+extern "C" int mkv_gather(mkv_pool *pool, int32_t layer, const int32_t *d_block_indptr,
+                          const int32_t *d_block_ids, const int32_t *d_ctx_indptr,
+                          int32_t num_seqs, int32_t max_ctx_len, void *d_out_k, void *d_out_v,
+                          int64_t out_capacity_tokens, void *stream) {
+  if (!pool) return set_error(MKV_ERR_INVALID_ARGUMENT, "pool is NULL");
+  Pool *p = reinterpret_cast<Pool *>(pool);
+  int rc = check_layer(p, layer);
+  if (rc) return rc;
+  if (num_seqs < 0 || max_ctx_len < 0 || out_capacity_tokens < 0)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "num_seqs, max_ctx_len and out_capacity_tokens must be >= 0");
+  if (num_seqs == 0 || max_ctx_len == 0) return MKV_OK;
+  if (num_seqs > 65535) return set_error(MKV_ERR_INVALID_ARGUMENT, "num_seqs > 65535");
+  if (!d_block_indptr || !d_block_ids || !d_ctx_indptr || !d_out_k || !d_out_v)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL device pointer");
+  if (!aligned16(d_out_k) || !aligned16(d_out_v))
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "gather outputs must be 16-byte aligned");
+  DeviceGuard guard(p->device);
+  const int nblk = (max_ctx_len + kPageSize - 1) / kPageSize;
+  hipLaunchKernelGGL(gather_kernel, dim3(nblk, num_seqs), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), p->data, layer, d_block_indptr,
+                     d_block_ids, d_ctx_indptr, max_ctx_len,
+                     reinterpret_cast<uint8_t *>(d_out_k), reinterpret_cast<uint8_t *>(d_out_v),
+                     (int64_t)out_capacity_tokens, p->g, p->d_err);
+  MKV_CHECK_LAUNCH("gather_kernel");
+  return MKV_OK;
+}
+
+extern "C" int mkv_copy_blocks(mkv_pool *pool, const int32_t *d_src_blocks,
+                               const int32_t *d_dst_blocks, int32_t num_pairs, void *stream) {
+  if (!pool) return set_error(MKV_ERR_INVALID_ARGUMENT, "pool is NULL");
+  Pool *p = reinterpret_cast<Pool *>(pool);
+  if (num_pairs < 0) return set_error(MKV_ERR_INVALID_ARGUMENT, "num_pairs < 0");
+  if (num_pairs == 0) return MKV_OK;
+  if (!d_src_blocks || !d_dst_blocks)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL device pointer");
+  if (2 * p->g.L > 65535) return set_error(MKV_ERR_INVALID_ARGUMENT, "too many layers");
+  DeviceGuard guard(p->device);
+  hipLaunchKernelGGL(copy_blocks_kernel, dim3(num_pairs, 2 * p->g.L), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), p->data, d_src_blocks, d_dst_blocks,
+                     p->g, p->d_err);
+  MKV_CHECK_LAUNCH("copy_blocks_kernel");
+  return MKV_OK;
+}
+
+// ---- C ABI: host validation ------------------------------------------------------------
+
+extern "C" int mkv_validate_slots(const mkv_pool_desc *desc, const int32_t *slots, int32_t n) {
+  int rc = validate_desc(desc);
+  if (rc) return rc;
+  if (n < 0 || (n > 0 && !slots)) return set_error(MKV_ERR_INVALID_ARGUMENT, "bad slot array");
+  const int64_t nslots = desc->num_blocks * desc->page_size;
+  for (int32_t i = 0; i < n; i++)
+    if (slots[i] < 0 || slots[i] >= nslots)
+      return set_error(MKV_ERR_INVALID_ARGUMENT, "slot[%d] = %d outside [0, %lld)", i, slots[i],
+                       (long long)nslots);
+  return MKV_OK;
+}
+
+extern "C" int mkv_validate_block_tables(const mkv_pool_desc *desc, const int32_t *indptr,
+                                         const int32_t *ids, const int32_t *ctx_lens,
+                                         int32_t num_seqs, int32_t max_ctx_len) {
+  int rc = validate_desc(desc);
+  if (rc) return rc;
+  if (num_seqs < 0 || !indptr) return set_error(MKV_ERR_INVALID_ARGUMENT, "bad indptr");
+  if (indptr[0] < 0) return set_error(MKV_ERR_INVALID_ARGUMENT, "indptr[0] < 0");
+  for (int32_t b = 0; b < num_seqs; b++) {
+    if (indptr[b + 1] < indptr[b])
+      return set_error(MKV_ERR_INVALID_ARGUMENT, "indptr not monotone at %d", b);
+    for (int32_t i = indptr[b]; i < indptr[b + 1]; i++)
+      if (!ids || ids[i] < 0 || ids[i] >= desc->num_blocks)
+        return set_error(MKV_ERR_INVALID_ARGUMENT, "block id at %d (sequence %d) out of range", i, b);
+    if (ctx_lens) {
+      const int32_t n = ctx_lens[b];
+      if (n < 1 || n > max_ctx_len)
+        return set_error(MKV_ERR_INVALID_ARGUMENT, "ctx_len[%d] = %d outside [1, %d]", b, n,
+                         max_ctx_len);
+      if ((int64_t)(n + desc->page_size - 1) / desc->page_size > indptr[b + 1] - indptr[b])
+        return set_error(MKV_ERR_INVALID_ARGUMENT,
+                         "sequence %d: %d blocks cannot hold %d tokens", b,
+                         indptr[b + 1] - indptr[b], n);
+    }
+  }
+  return MKV_OK;
+}
+
+extern "C" int mkv_validate_copy_pairs(const mkv_pool_desc *desc, const int32_t *src,
+                                       const int32_t *dst, int32_t n) {
+  int rc = validate_desc(desc);
+  if (rc) return rc;
+  if (n < 0 || (n > 0 && (!src || !dst))) return set_error(MKV_ERR_INVALID_ARGUMENT, "bad pairs");
+  std::vector<uint8_t> role((size_t)desc->num_blocks, 0);  // bit0 = source, bit1 = destination
+  for (int32_t i = 0; i < n; i++) {
+    if (src[i] < 0 || src[i] >= desc->num_blocks || dst[i] < 0 || dst[i] >= desc->num_blocks)
+      return set_error(MKV_ERR_INVALID_ARGUMENT, "pair %d (%d -> %d) out of range", i, src[i], dst[i]);
+    if (role[dst[i]] & 2) return set_error(MKV_ERR_INVALID_ARGUMENT, "destination %d repeats", dst[i]);
+    role[src[i]] |= 1;
+    role[dst[i]] |= 2;
+  }
+  for (int32_t i = 0; i < n; i++)
+    if (role[src[i]] == 3 || role[dst[i]] == 3)
+      return set_error(MKV_ERR_INVALID_ARGUMENT, "block %d is both a source and a destination",
+                       role[src[i]] == 3 ? src[i] : dst[i]);
+  return MKV_OK;
+}
+
+// ---- C ABI: device buffers ------------------------------------------------------------
+
+extern "C" int mkv_buffer_alloc(int device, uint64_t bytes, void **out_dev_ptr) {
+  if (!out_dev_ptr) return set_error(MKV_ERR_INVALID_ARGUMENT, "out pointer is NULL");
+  *out_dev_ptr = nullptr;
+  DeviceGuard guard(device);
+  if (!guard.ok) return set_error(MKV_ERR_NO_DEVICE, "cannot select device %d", device);
+  MKV_CHECK_HIP(hipMalloc(out_dev_ptr, bytes ? bytes : 1));
+  return MKV_OK;
+}
+
+extern "C" int mkv_buffer_free(void *dev_ptr) {
+  if (dev_ptr) MKV_CHECK_HIP(hipFree(dev_ptr));
+  return MKV_OK;
+}
+
+extern "C" int mkv_memcpy_h2d(void *d_dst, const void *h_src, uint64_t bytes, void *stream) {
+  if (!bytes) return MKV_OK;
+  if (!d_dst || !h_src) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL pointer");
+  MKV_CHECK_HIP(hipMemcpyAsync(d_dst, h_src, bytes, hipMemcpyHostToDevice,
+                               reinterpret_cast<hipStream_t>(stream)));
+  return MKV_OK;
+}
+
+extern "C" int mkv_memcpy_d2h(void *h_dst, const void *d_src, uint64_t bytes, void *stream) {
+  if (!bytes) return MKV_OK;
+  if (!h_dst || !d_src) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL pointer");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  MKV_CHECK_HIP(hipMemcpyAsync(h_dst, d_src, bytes, hipMemcpyDeviceToHost, s));
+  MKV_CHECK_HIP(hipStreamSynchronize(s));
+  return MKV_OK;
+}
+
+extern "C" int mkv_stream_synchronize(void *stream) {
+  MKV_CHECK_HIP(hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream)));
+  return MKV_OK;
+}
+
+extern "C" const char *mkv_last_error(void) { return g_last_error.c_str(); }
+
+extern "C" int mkv_version(void) { return 100; }

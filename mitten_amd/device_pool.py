@@ -1,0 +1,352 @@
+"""Device KV pool: the inference backend's device-buffer type, in Python.
+
+`DeviceKvPool` owns one libmitten_kv pool (HBM, layout
+[num_layers][2][num_blocks][page_size][num_kv_heads][head_dim]) and exposes the
+four hot-path operations on torch device tensors:
+
+    append(layer, k, v, slot_mapping)              model.rs:390-392 (Tensor::cat)
+    gather(layer, block_indptr, block_ids, ctx_indptr, max_ctx_len)
+                                                   design/phase0-deliverable.md:278
+    copy_blocks(src, dst)                          (COW / compaction; no reference
+                                                    counterpart)
+    decode_attention(layer, q, block_indptr, block_ids, ctx_lens, max_ctx_len)
+                                                   model.rs:394-416
+
+torch is used only for device memory and streams; every operation runs in
+the HIP library. Errors map onto the engine's error type
+(inference-backend/src/error.rs:3-13): pool exhaustion -> OutOfKvPages,
+everything else -> BackendError.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+
+MKV_OK = 0
+MKV_ERR_INVALID_ARGUMENT = 1
+MKV_ERR_OUT_OF_MEMORY = 2
+MKV_ERR_HIP = 3
+MKV_ERR_DEVICE_INDEX = 4
+MKV_ERR_NO_DEVICE = 5
+
+DEVERR_SLOT, DEVERR_BLOCK, DEVERR_TABLE, DEVERR_COPY, DEVERR_CTX = 1, 2, 4, 8, 16
+
+ATTN_ZERO_SINK, ATTN_FORCE_VALU, ATTN_FORCE_MFMA = 1, 2, 4
+
+DTYPES = {"f32": 0, "bf16": 1}
+PAGE_SIZE = 16
+
+
+class EngineError(RuntimeError):
+    """Mirror of inference-backend/src/error.rs EngineError."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(message)
+        self.status = status
+
+
+class OutOfKvPages(EngineError):
+    """EngineError::OutOfKvPages (error.rs:7-8)."""
+
+
+class BackendError(EngineError):
+    """EngineError::Backend(String) (error.rs:5-6)."""
+
+
+class DeviceIndexError(BackendError):
+    """A kernel met an out-of-range slot/block id (skipped, never dereferenced)."""
+
+    def __init__(self, status: int, message: str, bits: int):
+        super().__init__(status, message)
+        self.bits = bits
+
+
+def _raise(status: int) -> None:
+    if status == MKV_OK:
+        return
+    msg = (_lib.device_lib().mkv_last_error() or b"").decode(errors="replace")
+    if status == MKV_ERR_OUT_OF_MEMORY:
+        raise OutOfKvPages(status, msg)
+    raise BackendError(status, msg)
+
+
+@dataclass(frozen=True)
+class PoolDesc:
+    """Pool geometry: the engine's ModelConfig (num_layers, num_kv_heads,
+    head_dim; inference-backend/src/config.rs:1-11) plus num_q_heads and the
+    EngineConfig pool size (num_kv_pages, page_size; inference-engine/src/config.rs:3-17)."""
+
+    num_layers: int
+    num_kv_heads: int
+    num_q_heads: int
+    head_dim: int
+    num_blocks: int
+    dtype: str = "bf16"
+    page_size: int = PAGE_SIZE
+
+    def c(self) -> _lib.PoolDescC:
+        return _lib.PoolDescC(self.num_layers, self.num_kv_heads, self.num_q_heads, self.head_dim,
+                              self.page_size, DTYPES[self.dtype], self.num_blocks)
+
+    @property
+    def elem_bytes(self) -> int:
+        return 4 if self.dtype == "f32" else 2
+
+    @property
+    def block_bytes(self) -> int:
+        """Bytes of one block of one layer, K or V."""
+        return self.page_size * self.num_kv_heads * self.head_dim * self.elem_bytes
+
+    @property
+    def shape(self):
+        return (self.num_layers, 2, self.num_blocks, self.page_size, self.num_kv_heads, self.head_dim)
+
+
+def required_bytes(desc: PoolDesc) -> int:
+    """KvCachePool::required_bytes (inference-engine/src/kv_pool.rs:58-68)."""
+    out = ctypes.c_uint64()
+    _raise(_lib.device_lib().mkv_pool_required_bytes(ctypes.byref(desc.c()), ctypes.byref(out)))
+    return out.value
+
+
+def _i32p(a: np.ndarray):
+    return a.ctypes.data_as(_lib.I32P)
+
+
+def validate_slots(desc: PoolDesc, slots) -> None:
+    s = np.ascontiguousarray(slots, np.int32)
+    _raise(_lib.device_lib().mkv_validate_slots(ctypes.byref(desc.c()), _i32p(s), s.size))
+
+
+def validate_block_tables(desc: PoolDesc, indptr, ids, ctx_lens, max_ctx_len: int) -> None:
+    ip = np.ascontiguousarray(indptr, np.int32)
+    ix = np.ascontiguousarray(ids, np.int32)
+    cl = None if ctx_lens is None else np.ascontiguousarray(ctx_lens, np.int32)
+    _raise(_lib.device_lib().mkv_validate_block_tables(
+        ctypes.byref(desc.c()), _i32p(ip), _i32p(ix) if ix.size else None,
+        _i32p(cl) if cl is not None else None, ip.size - 1, max_ctx_len))
+
+
+def validate_copy_pairs(desc: PoolDesc, src, dst) -> None:
+    s = np.ascontiguousarray(src, np.int32)
+    d = np.ascontiguousarray(dst, np.int32)
+    if s.size != d.size:
+        raise BackendError(MKV_ERR_INVALID_ARGUMENT, "src and dst differ in length")
+    _raise(_lib.device_lib().mkv_validate_copy_pairs(ctypes.byref(desc.c()), _i32p(s), _i32p(d), s.size))
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+def _stream_handle(stream) -> ctypes.c_void_p:
+    torch = _torch()
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def _dptr(t) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr())
+
+
+class DeviceKvPool:
+    """The device KV pool (design's KvBufferHandle, design/phase0-deliverable.md:1320-1332)."""
+
+    def __init__(self, desc: PoolDesc, device: int = 0):
+        self.desc = desc
+        self.device = device
+        self._lib = _lib.device_lib()
+        h = ctypes.c_void_p()
+        _raise(self._lib.mkv_pool_create(ctypes.byref(desc.c()), device, ctypes.byref(h)))
+        self._h = h
+        ptr, nbytes = ctypes.c_void_p(), ctypes.c_uint64()
+        _raise(self._lib.mkv_pool_buffer(self._h, ctypes.byref(ptr), ctypes.byref(nbytes)))
+        self.data_ptr = ptr.value
+        self.nbytes = nbytes.value
+
+    # -- lifecycle -------------------------------------------------------------------
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._lib.mkv_pool_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @property
+    def torch_dtype(self):
+        torch = _torch()
+        return torch.float32 if self.desc.dtype == "f32" else torch.bfloat16
+
+    def _check_tensor(self, t, shape, name, dtype=None):
+        torch = _torch()
+        if not isinstance(t, torch.Tensor) or not t.is_cuda:
+            raise BackendError(MKV_ERR_INVALID_ARGUMENT, f"{name} must be a device tensor")
+        want = dtype or self.torch_dtype
+        if t.dtype != want:
+            raise BackendError(MKV_ERR_INVALID_ARGUMENT, f"{name} has dtype {t.dtype}, expected {want}")
+        if shape is not None and tuple(t.shape) != tuple(shape):
+            raise BackendError(MKV_ERR_INVALID_ARGUMENT, f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+        if not t.is_contiguous():
+            raise BackendError(MKV_ERR_INVALID_ARGUMENT, f"{name} must be contiguous")
+
+    def _i32(self, t, name, n=None):
+        torch = _torch()
+        self._check_tensor(t, (n,) if n is not None else None, name, dtype=torch.int32)
+
+    # -- error word ---------------------------------------------------------------------
+    def check(self, stream=None) -> None:
+        """Synchronise and raise DeviceIndexError if a kernel met a bad id."""
+        bits = ctypes.c_uint32()
+        st = self._lib.mkv_pool_check(self._h, _stream_handle(stream), ctypes.byref(bits))
+        if st == MKV_ERR_DEVICE_INDEX:
+            raise DeviceIndexError(st, self._lib.mkv_last_error().decode(), bits.value)
+        _raise(st)
+
+    # -- operations -----------------------------------------------------------------------
+    def append(self, layer: int, k, v, slot_mapping, stream=None) -> None:
+        d = self.desc
+        n = slot_mapping.shape[0]
+        self._i32(slot_mapping, "slot_mapping", n)
+        self._check_tensor(k, (n, d.num_kv_heads, d.head_dim), "k")
+        self._check_tensor(v, (n, d.num_kv_heads, d.head_dim), "v")
+        _raise(self._lib.mkv_append(self._h, layer, _dptr(k), _dptr(v), _dptr(slot_mapping), n,
+                                    _stream_handle(stream)))
+
+    def append_all_layers(self, k, v, slot_mapping, stream=None) -> None:
+        d = self.desc
+        n = slot_mapping.shape[0]
+        self._i32(slot_mapping, "slot_mapping", n)
+        self._check_tensor(k, (d.num_layers, n, d.num_kv_heads, d.head_dim), "k")
+        self._check_tensor(v, (d.num_layers, n, d.num_kv_heads, d.head_dim), "v")
+        _raise(self._lib.mkv_append_all_layers(self._h, _dptr(k), _dptr(v), _dptr(slot_mapping), n,
+                                               _stream_handle(stream)))
+
+    def gather(self, layer: int, block_indptr, block_ids, ctx_indptr, max_ctx_len: int,
+               out_k=None, out_v=None, total_tokens: int | None = None, stream=None):
+        """Returns (k, v), each flat [sum(ctx) * Hkv * D]: sequence b occupies
+        [Hkv][ctx_b][D] starting at element ctx_indptr[b]*Hkv*D."""
+        torch = _torch()
+        d = self.desc
+        B = ctx_indptr.shape[0] - 1
+        self._i32(block_indptr, "block_indptr", B + 1)
+        self._i32(block_ids, "block_ids")
+        self._i32(ctx_indptr, "ctx_indptr", B + 1)
+        if total_tokens is None:
+            total_tokens = int(ctx_indptr[-1].item())
+        n = total_tokens * d.num_kv_heads * d.head_dim
+        if out_k is None:
+            out_k = torch.empty(n, dtype=self.torch_dtype, device=ctx_indptr.device)
+        if out_v is None:
+            out_v = torch.empty(n, dtype=self.torch_dtype, device=ctx_indptr.device)
+        self._check_tensor(out_k, None, "out_k")
+        self._check_tensor(out_v, None, "out_v")
+        if out_k.numel() < n or out_v.numel() < n:
+            raise BackendError(MKV_ERR_INVALID_ARGUMENT, "gather outputs too small")
+        row = d.num_kv_heads * d.head_dim
+        cap = min(out_k.numel(), out_v.numel()) // row
+        _raise(self._lib.mkv_gather(self._h, layer, _dptr(block_indptr), _dptr(block_ids),
+                                    _dptr(ctx_indptr), B, max_ctx_len, _dptr(out_k), _dptr(out_v),
+                                    cap, _stream_handle(stream)))
+        return out_k, out_v
+
+    def copy_blocks(self, src, dst, stream=None) -> None:
+        n = src.shape[0]
+        self._i32(src, "src", n)
+        self._i32(dst, "dst", n)
+        _raise(self._lib.mkv_copy_blocks(self._h, _dptr(src), _dptr(dst), n, _stream_handle(stream)))
+
+    def workspace_size(self, num_seqs: int, max_ctx_len: int, split_tokens: int = 0) -> int:
+        out = ctypes.c_uint64()
+        _raise(self._lib.mkv_decode_attention_workspace_size(self._h, num_seqs, max_ctx_len,
+                                                             split_tokens, ctypes.byref(out)))
+        return out.value
+
+    def decode_attention(self, layer: int, q, block_indptr, block_ids, ctx_lens, max_ctx_len: int,
+                         scale: float | None = None, zero_sink: bool = False, out=None,
+                         split_tokens: int = 0, workspace=None, kernel: str | None = None,
+                         stream=None):
+        """q: [B, Hq, D] in the pool dtype. Returns o: [B, Hq, D]."""
+        torch = _torch()
+        d = self.desc
+        B = q.shape[0]
+        self._check_tensor(q, (B, d.num_q_heads, d.head_dim), "q")
+        self._i32(block_indptr, "block_indptr", B + 1)
+        self._i32(block_ids, "block_ids")
+        self._i32(ctx_lens, "ctx_lens", B)
+        if out is None:
+            out = torch.empty_like(q)
+        self._check_tensor(out, (B, d.num_q_heads, d.head_dim), "out")
+        if scale is None:
+            scale = float(np.float32(d.head_dim ** -0.5))
+        flags = ATTN_ZERO_SINK if zero_sink else 0
+        if kernel == "valu":
+            flags |= ATTN_FORCE_VALU
+        elif kernel == "mfma":
+            flags |= ATTN_FORCE_MFMA
+        elif kernel is not None:
+            raise ValueError(f"unknown kernel {kernel!r}")
+        ws_ptr, ws_bytes = None, 0
+        if workspace is not None:
+            self._check_tensor(workspace, None, "workspace", dtype=workspace.dtype)
+            ws_ptr, ws_bytes = _dptr(workspace), workspace.numel() * workspace.element_size()
+        _raise(self._lib.mkv_decode_attention(
+            self._h, layer, _dptr(q), _dptr(out), _dptr(block_indptr), _dptr(block_ids),
+            _dptr(ctx_lens), B, max_ctx_len, scale, flags, split_tokens, ws_ptr, ws_bytes,
+            _stream_handle(stream)))
+        return out
+
+    # -- host read-back / upload (tests) ------------------------------------------------------
+    def read(self) -> np.ndarray:
+        """Copy of the whole pool as numpy (uint16 bit patterns for bf16)."""
+        dt = np.float32 if self.desc.dtype == "f32" else np.uint16
+        host = np.empty(self.desc.shape, dt)
+        _raise(self._lib.mkv_memcpy_d2h(ctypes.c_void_p(host.ctypes.data), ctypes.c_void_p(self.data_ptr),
+                                        self.nbytes, _stream_handle(None)))
+        return host
+
+    def write(self, host: np.ndarray) -> None:
+        """Upload a whole-pool numpy array (same layout/bytes) and synchronise."""
+        host = np.ascontiguousarray(host)
+        if host.nbytes != self.nbytes:
+            raise BackendError(MKV_ERR_INVALID_ARGUMENT, "host array size differs from the pool")
+        s = _stream_handle(None)
+        _raise(self._lib.mkv_memcpy_h2d(ctypes.c_void_p(self.data_ptr), ctypes.c_void_p(host.ctypes.data),
+                                        self.nbytes, s))
+        _raise(self._lib.mkv_stream_synchronize(s))
+
+    def tensor(self):
+        """Zero-copy torch view of the pool buffer, shape `desc.shape`."""
+        torch = _torch()
+        dt = self.torch_dtype
+
+        class _View:
+            pass
+
+        view = _View()
+        typestr = "<f4" if self.desc.dtype == "f32" else "<i2"
+        view.__cuda_array_interface__ = {
+            "shape": tuple(int(x) for x in self.desc.shape),
+            "typestr": typestr,
+            "data": (self.data_ptr, False),
+            "version": 3,
+            "strides": None,
+        }
+        t = torch.as_tensor(view, device=f"cuda:{self.device}")
+        return t if self.desc.dtype == "f32" else t.view(dt)

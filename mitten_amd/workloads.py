@@ -1,0 +1,146 @@
+"""Seeded synthetic decode batches at the shapes of the benchmark configurations.
+
+Integers come from SplitMix64 with Lemire's bounded draw, so every length,
+permutation and slot below is a pure function of the seed. A decode batch is
+what one engine step hands the device: per sequence a block table (CSR), the
+number of tokens to attend (context + the token appended this step) and the
+slot of the appended token, slot = table[pos // 16] * 16 + pos % 16
+(inference-engine/src/prefill.rs:72-81, scheduler.rs:56-57).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+PAGE = 16
+MASK64 = (1 << 64) - 1
+BASE_SEED = 20261201
+
+
+class SplitMix64:
+    def __init__(self, seed: int):
+        self.s = seed & MASK64
+
+    def next(self) -> int:
+        self.s = (self.s + 0x9E3779B97F4A7C15) & MASK64
+        z = self.s
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & MASK64
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & MASK64
+        return z ^ (z >> 31)
+
+    def bounded(self, n: int) -> int:
+        """Uniform in [0, n), Lemire's multiply-shift with rejection."""
+        x = self.next() >> 32
+        m = x * n
+        lo = m & 0xFFFFFFFF
+        if lo < n:
+            t = (-n & 0xFFFFFFFF) % n
+            while lo < t:
+                x = self.next() >> 32
+                m = x * n
+                lo = m & 0xFFFFFFFF
+        return m >> 32
+
+    def uniform_int(self, lo: int, hi: int) -> int:
+        return lo + self.bounded(hi - lo + 1)
+
+    def uniform01(self) -> float:
+        return ((self.next() >> 11) + 1) * (1.0 / 9007199254740992.0)
+
+
+def permutation(n: int, rng: SplitMix64) -> np.ndarray:
+    """Fisher-Yates shuffle of 0..n-1."""
+    p = np.arange(n, dtype=np.int32)
+    for i in range(n - 1, 0, -1):
+        j = rng.bounded(i + 1)
+        p[i], p[j] = p[j], p[i]
+    return p
+
+
+@dataclass
+class DecodeBatch:
+    ctx_lens: np.ndarray       # int32 [B]: tokens attended (existing context + 1)
+    block_indptr: np.ndarray   # int32 [B+1]
+    block_ids: np.ndarray      # int32 [nnz]
+    slot_mapping: np.ndarray   # int32 [B]: slot of the appended token
+    num_blocks: int            # pool blocks covering every table
+    seed: int = 0
+    meta: dict = field(default_factory=dict)
+
+    @property
+    def num_seqs(self) -> int:
+        return int(self.ctx_lens.size)
+
+    @property
+    def max_ctx(self) -> int:
+        return int(self.ctx_lens.max())
+
+    @property
+    def total_tokens(self) -> int:
+        return int(self.ctx_lens.sum())
+
+    @property
+    def ctx_indptr(self) -> np.ndarray:
+        out = np.zeros(self.num_seqs + 1, np.int32)
+        np.cumsum(self.ctx_lens, out=out[1:])
+        return out
+
+
+def decode_batch_from_contexts(contexts, rng: SplitMix64, extra_blocks: int = 0,
+                               shuffle: bool = True) -> DecodeBatch:
+    """Each sequence holds `contexts[b]` tokens and appends one at position
+    contexts[b]; its table covers ceil((ctx+1)/16) blocks. Tables are slices of
+    a seeded permutation of the pool ids (or of 0..n-1 when shuffle=False)."""
+    ctx = np.asarray(contexts, np.int64)
+    attend = ctx + 1
+    nblk = (attend + PAGE - 1) // PAGE
+    total = int(nblk.sum())
+    num_blocks = total + extra_blocks
+    perm = permutation(num_blocks, rng) if shuffle else np.arange(num_blocks, dtype=np.int32)
+    indptr = np.zeros(ctx.size + 1, np.int32)
+    np.cumsum(nblk, out=indptr[1:])
+    ids = perm[:total].astype(np.int32)
+    pos = ctx
+    slots = ids[indptr[:-1] + pos // PAGE].astype(np.int64) * PAGE + pos % PAGE
+    return DecodeBatch(attend.astype(np.int32), indptr, ids, slots.astype(np.int32), num_blocks)
+
+
+def uniform_contexts(B: int, lo: int, hi: int, rng: SplitMix64):
+    return [rng.uniform_int(lo, hi) for _ in range(B)]
+
+
+# Benchmark configurations (shapes of the BASELINE configurations).
+CONFIGS = {
+    "qwen2.5-0.5b": dict(num_layers=24, num_q_heads=14, num_kv_heads=2, head_dim=64, dtype="f32",
+                         batch=8, ctx_lo=32, ctx_hi=512, index=0),
+    "qwen2.5-7b": dict(num_layers=28, num_q_heads=28, num_kv_heads=4, head_dim=128, dtype="bf16",
+                       batch=64, ctx_lo=1024, ctx_hi=8192, index=1),
+    "gemma-2b-mqa": dict(num_layers=18, num_q_heads=8, num_kv_heads=1, head_dim=256, dtype="bf16",
+                         batch=128, ctx_lo=2048, ctx_hi=8192, index=2),
+}
+
+
+def config_batch(name: str, seed: int | None = None) -> DecodeBatch:
+    c = CONFIGS[name]
+    s = BASE_SEED + c["index"] if seed is None else seed
+    rng = SplitMix64(s)
+    ctx = uniform_contexts(c["batch"], c["ctx_lo"], c["ctx_hi"], rng)
+    b = decode_batch_from_contexts(ctx, rng)
+    b.seed = s
+    return b
+
+
+def algorithmic_bytes_attention(batch: DecodeBatch, num_q_heads: int, num_kv_heads: int,
+                                head_dim: int, elem_bytes: int) -> int:
+    """K+V read once + Q read + O written + block ids + context lengths."""
+    kv = batch.total_tokens * 2 * num_kv_heads * head_dim * elem_bytes
+    qo = 2 * batch.num_seqs * num_q_heads * head_dim * elem_bytes
+    meta = 4 * int(batch.block_ids.size) + 4 * (batch.num_seqs + 1) + 4 * batch.num_seqs
+    return kv + qo + meta
+
+
+def algorithmic_bytes_append(num_tokens: int, num_kv_heads: int, head_dim: int,
+                             elem_bytes: int) -> int:
+    """K and V rows read and written + slot ids."""
+    return 4 * num_tokens * num_kv_heads * head_dim * elem_bytes + 4 * num_tokens

@@ -1,0 +1,194 @@
+"""ctypes front-end of the CPU oracle (oracle/mkv_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, ``__graft_entry__.smoke()`` and
+bench.py's CPU-baseline leg, always as the checker or the timed CPU baseline,
+never as the product path.  The HIP library (mitten_amd) does not import this.
+
+Arrays are numpy; bf16 data is carried as ``np.uint16`` bit patterns.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "build", "libmkv_oracle.so")
+
+_lib = None
+
+
+def build(force: bool = False) -> str:
+    """Compile the oracle with its Makefile (gcc); returns the library path."""
+    if force or not os.path.exists(LIB_PATH):
+        subprocess.run(["make", "-C", HERE, "-B" if force else "-s"], check=True,
+                       stdout=subprocess.DEVNULL)
+    return LIB_PATH
+
+
+class PoolDesc(ctypes.Structure):
+    _fields_ = [
+        ("num_layers", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("page_size", ctypes.c_int32),
+        ("num_blocks", ctypes.c_int64),
+        ("elem_bytes", ctypes.c_int32),
+    ]
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        P = ctypes.c_void_p
+        i32, i64, f32, f64 = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_double
+        dp = ctypes.POINTER(PoolDesc)
+        sig = {
+            "orc_splitmix64": (ctypes.c_uint64, [P]),
+            "orc_fill_normal_f32": (None, [ctypes.c_uint64, i64, P]),
+            "orc_bounded": (ctypes.c_uint32, [P, ctypes.c_uint32]),
+            "orc_f32_to_bf16": (None, [P, P, i64]),
+            "orc_bf16_to_f32": (None, [P, P, i64]),
+            "orc_pool_bytes": (i64, [dp]),
+            "orc_append": (i64, [dp, P, ctypes.c_int, P, P, P, i64]),
+            "orc_gather": (ctypes.c_int, [dp, P, ctypes.c_int, P, P, P, i32, P, P]),
+            "orc_copy_blocks": (ctypes.c_int, [dp, P, P, P, i64]),
+            "orc_decode_attention_f32": (ctypes.c_int, [dp, P, ctypes.c_int, P, i32, i32, P, P, P,
+                                                        f32, ctypes.c_int, P]),
+            "orc_decode_attention_f64": (ctypes.c_int, [dp, P, ctypes.c_int, P, i32, i32, P, P, P,
+                                                        f64, ctypes.c_int, P]),
+            "orc_ref_faithful_decode": (ctypes.c_int, [P, P, i64, i32, i32, i32, P, P, P, f32, P]),
+            "orc_num_threads": (ctypes.c_int, []),
+            "orc_set_num_threads": (None, [ctypes.c_int]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+# ---------------------------------------------------------------- data ----
+
+def fill_normal(seed: int, n: int) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().orc_fill_normal_f32(ctypes.c_uint64(seed), n, _p(out))
+    return out
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_f32_to_bf16(_p(x), _p(out), x.size)
+    return out
+
+
+def bf16_to_f32(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.uint16)
+    out = np.empty(x.shape, np.float32)
+    lib().orc_bf16_to_f32(_p(x), _p(out), x.size)
+    return out
+
+
+class SplitMix64:
+    """Seeded integer stream shared with the C oracle (SplitMix64 + Lemire)."""
+
+    def __init__(self, seed: int):
+        self.state = ctypes.c_uint64(seed)
+
+    def next(self) -> int:
+        return lib().orc_splitmix64(ctypes.byref(self.state))
+
+    def bounded(self, n: int) -> int:
+        return lib().orc_bounded(ctypes.byref(self.state), n)
+
+    def uniform_int(self, lo: int, hi: int) -> int:
+        """Uniform integer in [lo, hi]."""
+        return lo + self.bounded(hi - lo + 1)
+
+
+# ---------------------------------------------------------------- pool ----
+
+def desc(num_layers, num_kv_heads, head_dim, num_blocks, elem_bytes, page_size=16) -> PoolDesc:
+    return PoolDesc(num_layers, num_kv_heads, head_dim, page_size, num_blocks, elem_bytes)
+
+
+def pool_bytes(d: PoolDesc) -> int:
+    return lib().orc_pool_bytes(ctypes.byref(d))
+
+
+def pool_shape(d: PoolDesc):
+    return (d.num_layers, 2, d.num_blocks, d.page_size, d.num_kv_heads, d.head_dim)
+
+
+def append(d: PoolDesc, pool: np.ndarray, layer: int, k: np.ndarray, v: np.ndarray,
+           slots: np.ndarray) -> int:
+    """In-place append into ``pool``; returns -1 or the first bad token index."""
+    slots = np.ascontiguousarray(slots, np.int32)
+    return lib().orc_append(ctypes.byref(d), _p(pool), layer, _p(k), _p(v), _p(slots), slots.size)
+
+
+def gather(d: PoolDesc, pool: np.ndarray, layer: int, indptr, indices, ctx_len):
+    indptr = np.ascontiguousarray(indptr, np.int32)
+    indices = np.ascontiguousarray(indices, np.int32)
+    ctx_len = np.ascontiguousarray(ctx_len, np.int32)
+    n = int(ctx_len.sum()) * d.num_kv_heads * d.head_dim
+    dt = pool.dtype
+    dk, dv = np.empty(n, dt), np.empty(n, dt)
+    rc = lib().orc_gather(ctypes.byref(d), _p(pool), layer, _p(indptr), _p(indices), _p(ctx_len),
+                          ctx_len.size, _p(dk), _p(dv))
+    if rc != 0:
+        raise ValueError("orc_gather: invalid block table or context length")
+    return dk, dv
+
+
+def copy_blocks(d: PoolDesc, pool: np.ndarray, src, dst) -> None:
+    src = np.ascontiguousarray(src, np.int32)
+    dst = np.ascontiguousarray(dst, np.int32)
+    if lib().orc_copy_blocks(ctypes.byref(d), _p(pool), _p(src), _p(dst), src.size) != 0:
+        raise ValueError("orc_copy_blocks: block id out of range")
+
+
+def decode_attention(d: PoolDesc, pool: np.ndarray, layer: int, q: np.ndarray, indptr, indices,
+                     ctx_len, scale: float | None = None, zero_sink: bool = False,
+                     precision: str = "f32") -> np.ndarray:
+    """q: [B, Hq, D] f32 values (bf16 queries passed already widened)."""
+    q = np.ascontiguousarray(q, np.float32)
+    B, Hq, D = q.shape
+    indptr = np.ascontiguousarray(indptr, np.int32)
+    indices = np.ascontiguousarray(indices, np.int32)
+    ctx_len = np.ascontiguousarray(ctx_len, np.int32)
+    if scale is None:
+        scale = float(np.float32(D ** -0.5))
+    if precision == "f32":
+        o = np.empty((B, Hq, D), np.float32)
+        rc = lib().orc_decode_attention_f32(ctypes.byref(d), _p(pool), layer, _p(q), B, Hq,
+                                            _p(indptr), _p(indices), _p(ctx_len), scale,
+                                            int(zero_sink), _p(o))
+    else:
+        o = np.empty((B, Hq, D), np.float64)
+        rc = lib().orc_decode_attention_f64(ctypes.byref(d), _p(pool), layer, _p(q), B, Hq,
+                                            _p(indptr), _p(indices), _p(ctx_len), float(scale),
+                                            int(zero_sink), _p(o))
+    if rc != 0:
+        raise ValueError("orc_decode_attention: invalid arguments")
+    return o
+
+
+def num_threads() -> int:
+    return lib().orc_num_threads()
+
+
+def set_num_threads(n: int) -> None:
+    lib().orc_set_num_threads(n)

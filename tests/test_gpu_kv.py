@@ -1,0 +1,247 @@
+"""GPU parity: append / gather / copy_blocks bit-exact against the oracle, and
+decode attention within the north-star tolerances (f32 max-abs 1e-5, bf16
+row-relative 2e-2), all through the C ABI of libmitten_kv."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from mitten_amd import DeviceIndexError, DeviceKvPool, PoolDesc
+from mitten_amd import device_pool as dp
+from mitten_amd import workloads as wl
+from oracle import oracle as orc
+from tests.helpers import assert_attention_close, bits, normal, odesc, to_device, to_host, widen
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = {
+    # name: (layers, Hq, Hkv, D, dtype)
+    "qwen0.5b-f32": (3, 14, 2, 64, "f32"),
+    "qwen7b-bf16": (2, 28, 4, 128, "bf16"),
+    "gemma2b-bf16": (2, 8, 1, 256, "bf16"),
+}
+
+
+def _i32(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a, np.int32)).cuda()
+
+
+def _pool(shape, num_blocks, seed):
+    L, Hq, Hkv, D, dt = SHAPES[shape]
+    desc = PoolDesc(L, Hkv, Hq, D, num_blocks, dt)
+    pool = DeviceKvPool(desc)
+    host = normal(seed, desc.shape, dt)
+    pool.write(host)
+    return desc, pool, host
+
+
+@pytest.mark.parametrize("shape", list(SHAPES))
+def test_append_bit_exact(shape):
+    desc, pool, host = _pool(shape, 40, 1)
+    rng = np.random.default_rng(2)
+    n = 37
+    slots = rng.choice(desc.num_blocks * 16, size=n, replace=False).astype(np.int32)
+    k = normal(3, (n, desc.num_kv_heads, desc.head_dim), desc.dtype)
+    v = normal(4, (n, desc.num_kv_heads, desc.head_dim), desc.dtype)
+    layer = desc.num_layers - 1
+    pool.append(layer, to_device(k), to_device(v), _i32(slots))
+    pool.check()
+    got = pool.read()
+    want = host.copy()
+    assert orc.append(odesc(desc), want, layer, k, v, slots) == -1
+    assert np.array_equal(bits(got), bits(want))
+    pool.close()
+
+
+@pytest.mark.parametrize("shape", ["qwen0.5b-f32", "qwen7b-bf16"])
+def test_append_all_layers_bit_exact(shape):
+    desc, pool, host = _pool(shape, 24, 5)
+    n = 50
+    slots = np.random.default_rng(6).choice(desc.num_blocks * 16, size=n, replace=False).astype(np.int32)
+    k = normal(7, (desc.num_layers, n, desc.num_kv_heads, desc.head_dim), desc.dtype)
+    v = normal(8, (desc.num_layers, n, desc.num_kv_heads, desc.head_dim), desc.dtype)
+    pool.append_all_layers(to_device(k), to_device(v), _i32(slots))
+    pool.check()
+    want = host.copy()
+    for layer in range(desc.num_layers):
+        orc.append(odesc(desc), want, layer, np.ascontiguousarray(k[layer]), np.ascontiguousarray(v[layer]), slots)
+    assert np.array_equal(bits(pool.read()), bits(want))
+    pool.close()
+
+
+def test_append_out_of_range_slot_is_reported_and_skipped():
+    desc, pool, host = _pool("qwen7b-bf16", 8, 9)
+    slots = np.array([3, desc.num_blocks * 16, -1, 17], np.int32)
+    k = normal(10, (4, desc.num_kv_heads, desc.head_dim), desc.dtype)
+    v = normal(11, (4, desc.num_kv_heads, desc.head_dim), desc.dtype)
+    pool.append(0, to_device(k), to_device(v), _i32(slots))
+    with pytest.raises(DeviceIndexError) as ei:
+        pool.check()
+    assert ei.value.bits & dp.DEVERR_SLOT
+    want = host.copy()
+    good = np.array([0, 3])
+    orc.append(odesc(desc), want, 0, np.ascontiguousarray(k[good]), np.ascontiguousarray(v[good]), slots[good])
+    assert np.array_equal(bits(pool.read()), bits(want))
+    pool.check()  # the error word was cleared
+    pool.close()
+
+
+@pytest.mark.parametrize("shape", list(SHAPES))
+def test_gather_bit_exact(shape):
+    rng = wl.SplitMix64(12)
+    ctx = [1, 15, 16, 17, 100, 333]
+    batch = wl.decode_batch_from_contexts(ctx, rng, extra_blocks=5)
+    desc, pool, host = _pool(shape, batch.num_blocks, 13)
+    layer = desc.num_layers - 1
+    ci = batch.ctx_indptr
+    k, v = pool.gather(layer, _i32(batch.block_indptr), _i32(batch.block_ids), _i32(ci), batch.max_ctx,
+                       total_tokens=int(ci[-1]))
+    pool.check()
+    wk, wv = orc.gather(odesc(desc), host, layer, batch.block_indptr, batch.block_ids, batch.ctx_lens)
+    assert np.array_equal(bits(to_host(k)), bits(wk))
+    assert np.array_equal(bits(to_host(v)), bits(wv))
+    pool.close()
+
+
+def test_append_then_gather_equals_contiguous_cat():
+    """Appending tokens one at a time and gathering yields the contiguous
+    cache Tensor::cat builds (model.rs:390-392), in [heads, seq, dim] order."""
+    import torch
+
+    desc = PoolDesc(1, 2, 14, 64, 12, "f32")
+    with DeviceKvPool(desc) as pool:
+        pool.write(normal(14, desc.shape, "f32"))
+        rng = wl.SplitMix64(15)
+        table = wl.permutation(desc.num_blocks, rng)[:9]
+        n = 131
+        ks = normal(16, (n, 2, 64), "f32")
+        vs = normal(17, (n, 2, 64), "f32")
+        for t in range(n):
+            slot = np.array([table[t // 16] * 16 + t % 16], np.int32)
+            pool.append(0, to_device(ks[t:t + 1]), to_device(vs[t:t + 1]), _i32(slot))
+        k, v = pool.gather(0, _i32([0, 9]), _i32(table), _i32([0, n]), n, total_tokens=n)
+        pool.check()
+        assert np.array_equal(to_host(k).reshape(2, n, 64), ks.transpose(1, 0, 2))
+        assert np.array_equal(to_host(v).reshape(2, n, 64), vs.transpose(1, 0, 2))
+        torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("shape", list(SHAPES))
+def test_copy_blocks_bit_exact(shape):
+    desc, pool, host = _pool(shape, 64, 18)
+    rng = np.random.default_rng(19)
+    ids = rng.permutation(desc.num_blocks).astype(np.int32)
+    src, dst = ids[:20], ids[20:40]
+    dp.validate_copy_pairs(desc, src, dst)
+    pool.copy_blocks(_i32(src), _i32(dst))
+    pool.check()
+    want = host.copy()
+    orc.copy_blocks(odesc(desc), want, src, dst)
+    assert np.array_equal(bits(pool.read()), bits(want))
+    pool.close()
+
+
+def test_copy_blocks_bad_id_reported():
+    desc, pool, host = _pool("qwen7b-bf16", 8, 20)
+    pool.copy_blocks(_i32([1, 2]), _i32([5, 99]))
+    with pytest.raises(DeviceIndexError) as ei:
+        pool.check()
+    assert ei.value.bits & dp.DEVERR_COPY
+    want = host.copy()
+    orc.copy_blocks(odesc(desc), want, [1], [5])
+    assert np.array_equal(bits(pool.read()), bits(want))
+    pool.close()
+
+
+# ---------------------------------------------------------------- attention ----
+
+def _attention_case(shape, ctx, seed, kernel=None, split_tokens=0, zero_sink=False, layer=None):
+    L, Hq, Hkv, D, dt = SHAPES[shape]
+    rng = wl.SplitMix64(seed)
+    batch = wl.decode_batch_from_contexts([c - 1 for c in ctx], rng, extra_blocks=3)
+    desc = PoolDesc(L, Hkv, Hq, D, batch.num_blocks, dt)
+    layer = L - 1 if layer is None else layer
+    with DeviceKvPool(desc) as pool:
+        host = normal(seed + 1, desc.shape, dt)
+        pool.write(host)
+        q = normal(seed + 2, (len(ctx), Hq, D), dt)
+        o = pool.decode_attention(layer, to_device(q), _i32(batch.block_indptr), _i32(batch.block_ids),
+                                  _i32(batch.ctx_lens), batch.max_ctx, zero_sink=zero_sink,
+                                  split_tokens=split_tokens, kernel=kernel)
+        pool.check()
+        got = to_host(o)
+    ref = orc.decode_attention(odesc(desc), host, layer, widen(q), batch.block_indptr, batch.block_ids,
+                               batch.ctx_lens, zero_sink=zero_sink)
+    return got, ref, dt
+
+
+CTX_EDGE = [1, 2, 15, 16, 17, 31, 32, 33, 127, 128, 129, 257, 500, 1000]
+
+
+@pytest.mark.parametrize("split_tokens", [0, 16, 48, 128])
+def test_attention_f32_gqa(split_tokens):
+    got, ref, dt = _attention_case("qwen0.5b-f32", CTX_EDGE, 30, split_tokens=split_tokens)
+    assert_attention_close(got, ref, dt)
+
+
+@pytest.mark.parametrize("kernel", ["mfma", "valu"])
+@pytest.mark.parametrize("split_tokens", [0, 32, 256])
+def test_attention_bf16_gqa(kernel, split_tokens):
+    got, ref, dt = _attention_case("qwen7b-bf16", CTX_EDGE, 31, kernel=kernel, split_tokens=split_tokens)
+    assert_attention_close(got, ref, dt)
+
+
+@pytest.mark.parametrize("kernel", ["mfma", "valu"])
+def test_attention_bf16_mqa_wide_head(kernel):
+    got, ref, dt = _attention_case("gemma2b-bf16", CTX_EDGE, 32, kernel=kernel)
+    assert_attention_close(got, ref, dt)
+
+
+@pytest.mark.parametrize("shape,kernel", [("qwen0.5b-f32", None), ("qwen7b-bf16", "mfma"),
+                                          ("qwen7b-bf16", "valu")])
+def test_attention_zero_sink(shape, kernel):
+    got, ref, dt = _attention_case(shape, [1, 5, 40, 300], 33, kernel=kernel, zero_sink=True, split_tokens=32)
+    assert_attention_close(got, ref, dt)
+
+
+def test_attention_bad_block_id_reported():
+    desc = PoolDesc(1, 4, 28, 128, 10, "bf16")
+    with DeviceKvPool(desc) as pool:
+        pool.write(normal(40, desc.shape, "bf16"))
+        q = to_device(normal(41, (2, 28, 128), "bf16"))
+        pool.decode_attention(0, q, _i32([0, 2, 4]), _i32([1, 2, 3, 10]), _i32([20, 30]), 30)
+        with pytest.raises(DeviceIndexError) as ei:
+            pool.check()
+        assert ei.value.bits & dp.DEVERR_BLOCK
+
+
+def test_attention_short_table_reported():
+    desc = PoolDesc(1, 4, 28, 128, 10, "bf16")
+    with DeviceKvPool(desc) as pool:
+        pool.write(normal(42, desc.shape, "bf16"))
+        q = to_device(normal(43, (1, 28, 128), "bf16"))
+        pool.decode_attention(0, q, _i32([0, 1]), _i32([4]), _i32([40]), 40)
+        with pytest.raises(DeviceIndexError) as ei:
+            pool.check()
+        assert ei.value.bits & dp.DEVERR_TABLE
+
+
+@pytest.mark.parametrize("name", ["qwen2.5-7b", "gemma-2b-mqa"])
+def test_attention_full_config_one_layer(name):
+    """One layer at the configuration's full batch and context lengths."""
+    c = wl.CONFIGS[name]
+    batch = wl.config_batch(name)
+    desc = PoolDesc(1, c["num_kv_heads"], c["num_q_heads"], c["head_dim"], batch.num_blocks, c["dtype"])
+    with DeviceKvPool(desc) as pool:
+        host = normal(50, desc.shape, desc.dtype)
+        pool.write(host)
+        q = normal(51, (batch.num_seqs, desc.num_q_heads, desc.head_dim), desc.dtype)
+        o = pool.decode_attention(0, to_device(q), _i32(batch.block_indptr), _i32(batch.block_ids),
+                                  _i32(batch.ctx_lens), batch.max_ctx)
+        pool.check()
+        got = to_host(o)
+    ref = orc.decode_attention(odesc(desc), host, 0, widen(q), batch.block_indptr, batch.block_ids,
+                               batch.ctx_lens)
+    assert_attention_close(got, ref, desc.dtype)

@@ -1,0 +1,386 @@
+"""Pins the CPU oracle before it is trusted as the parity checker.
+
+Each oracle function is checked against the reference's own known answers
+where they exist (kv_pool.rs:130-136), against library routines (numpy fancy
+indexing, scipy.special.softmax, torch's bf16 cast), against closed forms and
+invariants, and against brute force in float64 — chosen so that plausible
+mistakes (wrong GQA head map, a transposed operand, a dropped scale, wrong
+block/offset split of a slot) fail at least one check. The mutation tests at
+the end plant such mistakes in a numpy restatement and confirm the checks
+see them.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import scipy.special
+import scipy.stats
+
+from oracle import oracle as orc
+
+# ------------------------------------------------------------------ sizes ----
+
+
+def test_required_bytes_reference_kats():
+    # inference-engine/src/kv_pool.rs:130-136
+    assert orc.pool_bytes(orc.desc(1, 1, 1, 1, 1)) == 32
+    assert orc.pool_bytes(orc.desc(28, 4, 128, 512, 2)) == 2 * 512 * 16 * 28 * 4 * 128 * 2 == 469_762_048
+
+
+# --------------------------------------------------------------- bf16 / rng ----
+
+
+def test_bf16_round_to_nearest_even_matches_torch():
+    torch = pytest.importorskip("torch")
+    g = np.random.default_rng(0)
+    x = np.concatenate([
+        g.standard_normal(100_000).astype(np.float32) * 10.0 ** g.integers(-30, 30, 100_000),
+        np.array([0.0, -0.0, 1.0, 1.00390625, 1.01171875, 3.0e38, -3.4e38, 1e-40, np.inf, -np.inf],
+                 np.float32),
+    ]).astype(np.float32)
+    ours = orc.f32_to_bf16(x)
+    theirs = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(ours, theirs)
+    # ties go to even: 1 + 2^-8 sits exactly between 1.0 and 1 + 2^-7
+    assert orc.f32_to_bf16(np.array([1.00390625], np.float32))[0] == 0x3F80
+    back = orc.bf16_to_f32(ours)
+    assert np.array_equal(back, torch.from_numpy(theirs.view(np.int16)).view(torch.bfloat16).float().numpy())
+
+
+def test_bf16_nan_stays_nan():
+    x = np.array([np.nan, -np.nan], np.float32)
+    assert np.all(np.isnan(orc.bf16_to_f32(orc.f32_to_bf16(x))))
+
+
+def test_normal_generator_is_standard_normal_and_seeded():
+    a = orc.fill_normal(123, 200_001)
+    b = orc.fill_normal(123, 200_001)
+    c = orc.fill_normal(124, 200_001)
+    assert np.array_equal(a, b) and not np.array_equal(a, c)
+    assert abs(a.mean()) < 0.01 and abs(a.std() - 1.0) < 0.01
+    assert scipy.stats.kstest(a, "norm").pvalue > 1e-3
+
+
+def test_splitmix64_and_bounded_match_python_workload_rng():
+    from mitten_amd import workloads as wl
+
+    r1, r2 = orc.SplitMix64(99), wl.SplitMix64(99)
+    for _ in range(50):
+        assert r1.next() == r2.next()
+    for n in (1, 2, 7, 1000, 8192 - 1024 + 1, 2**31 - 1):
+        assert r1.bounded(n) == r2.bounded(n)
+    # First SplitMix64 output of seed 0 (published test value of the generator).
+    assert orc.SplitMix64(0).next() == 0xE220A8397B1DCDAF
+
+
+def test_bounded_is_uniform():
+    r = orc.SplitMix64(5)
+    draws = np.array([r.bounded(7) for _ in range(70_000)])
+    counts = np.bincount(draws, minlength=7)
+    assert scipy.stats.chisquare(counts).pvalue > 1e-3
+
+
+# --------------------------------------------------------------- helpers ----
+
+def _pool(L, H, D, nblocks, es, seed):
+    d = orc.desc(L, H, D, nblocks, es)
+    g = np.random.default_rng(seed)
+    x = g.standard_normal(int(np.prod(orc.pool_shape(d))), dtype=np.float32).reshape(orc.pool_shape(d))
+    return d, (x if es == 4 else orc.f32_to_bf16(x))
+
+
+def _widen(a):
+    return a if a.dtype == np.float32 else orc.bf16_to_f32(a)
+
+
+def _tables(ctx, nblocks, seed):
+    g = np.random.default_rng(seed)
+    nb = [(c + 15) // 16 for c in ctx]
+    perm = g.permutation(nblocks)[: sum(nb)].astype(np.int32)
+    indptr = np.zeros(len(ctx) + 1, np.int32)
+    indptr[1:] = np.cumsum(nb)
+    return indptr, perm
+
+
+# ---------------------------------------------------------------- append ----
+
+
+@pytest.mark.parametrize("es", [4, 2])
+def test_append_matches_fancy_indexing(es):
+    d, pool = _pool(3, 2, 8, 5, es, 1)
+    g = np.random.default_rng(2)
+    n = 30
+    slots = g.choice(5 * 16, n, replace=False).astype(np.int32)
+    k = g.standard_normal((n, 2, 8), dtype=np.float32)
+    v = g.standard_normal((n, 2, 8), dtype=np.float32)
+    if es == 2:
+        k, v = orc.f32_to_bf16(k), orc.f32_to_bf16(v)
+    want = pool.copy()
+    flat = want.reshape(3, 2, 5 * 16, 2, 8)
+    flat[1, 0, slots] = k
+    flat[1, 1, slots] = v
+    assert orc.append(d, pool, 1, k, v, slots) == -1
+    assert np.array_equal(pool, want)
+
+
+def test_append_slot_split_is_block_then_offset():
+    """slot 17 is block 1, offset 1 (page_size 16), not block 17/..."""
+    d, pool = _pool(1, 1, 8, 3, 4, 3)
+    k = np.full((1, 1, 8), 7.0, np.float32)
+    v = np.full((1, 1, 8), -7.0, np.float32)
+    orc.append(d, pool, 0, k, v, np.array([17], np.int32))
+    assert np.all(pool[0, 0, 1, 1, 0] == 7.0) and np.all(pool[0, 1, 1, 1, 0] == -7.0)
+
+
+def test_append_rejects_out_of_range_slot():
+    d, pool = _pool(1, 1, 8, 2, 4, 4)
+    before = pool.copy()
+    k = np.zeros((2, 1, 8), np.float32)
+    assert orc.append(d, pool, 0, k, k, np.array([3, 32], np.int32)) == 1
+    assert orc.append(d, pool, 0, k, k, np.array([-1, 0], np.int32)) == 0
+    assert np.array_equal(pool[0, :, 0, 4:], before[0, :, 0, 4:])
+
+
+# ---------------------------------------------------------------- gather ----
+
+
+@pytest.mark.parametrize("es", [4, 2])
+def test_gather_matches_indexing_and_layout(es):
+    d, pool = _pool(2, 3, 16, 40, es, 5)
+    ctx = [1, 16, 17, 100, 250]
+    indptr, ids = _tables(ctx, 40, 6)
+    gk, gv = orc.gather(d, pool, 1, indptr, ids, ctx)
+    off = 0
+    for b, n in enumerate(ctx):
+        tab = ids[indptr[b]:indptr[b + 1]]
+        t = np.arange(n)
+        wk = pool[1, 0, tab[t // 16], t % 16]  # [n, H, D]
+        wv = pool[1, 1, tab[t // 16], t % 16]
+        size = 3 * n * 16
+        assert np.array_equal(gk[off:off + size].reshape(3, n, 16), wk.transpose(1, 0, 2))
+        assert np.array_equal(gv[off:off + size].reshape(3, n, 16), wv.transpose(1, 0, 2))
+        off += size
+    assert off == gk.size
+
+
+def test_append_then_gather_is_the_contiguous_cat():
+    """Appending rows one at a time then gathering gives the cache that
+    Tensor::cat(vec![cache, k], 2) grows (model.rs:390-392), [heads, seq, dim]."""
+    d, pool = _pool(1, 2, 8, 10, 4, 7)
+    table = np.array([9, 2, 5, 0], np.int32)
+    g = np.random.default_rng(8)
+    rows_k = g.standard_normal((50, 2, 8), dtype=np.float32)
+    rows_v = g.standard_normal((50, 2, 8), dtype=np.float32)
+    cat_k = np.zeros((2, 0, 8), np.float32)
+    for t in range(50):
+        orc.append(d, pool, 0, rows_k[t:t + 1], rows_v[t:t + 1], np.array([table[t // 16] * 16 + t % 16], np.int32))
+        cat_k = np.concatenate([cat_k, rows_k[t][:, None, :]], axis=1)
+    gk, gv = orc.gather(d, pool, 0, np.array([0, 4], np.int32), table, [50])
+    assert np.array_equal(gk.reshape(2, 50, 8), cat_k)
+    assert np.array_equal(gv.reshape(2, 50, 8), rows_v.transpose(1, 0, 2))
+
+
+def test_gather_invariant_under_block_permutation():
+    d, pool = _pool(1, 2, 8, 30, 2, 9)
+    ctx = [40, 70]
+    indptr, ids = _tables(ctx, 30, 10)
+    base = orc.gather(d, pool, 0, indptr, ids, ctx)
+    perm = np.random.default_rng(11).permutation(30).astype(np.int32)
+    moved = np.empty_like(pool)
+    moved[:, :, perm] = pool
+    again = orc.gather(d, moved, 0, indptr, perm[ids], ctx)
+    assert np.array_equal(base[0], again[0]) and np.array_equal(base[1], again[1])
+
+
+def test_gather_rejects_short_table():
+    d, pool = _pool(1, 1, 8, 4, 4, 12)
+    with pytest.raises(ValueError):
+        orc.gather(d, pool, 0, np.array([0, 1], np.int32), np.array([0], np.int32), [17])
+
+
+# ----------------------------------------------------------- copy_blocks ----
+
+
+def test_copy_blocks_closed_form_all_layers_k_and_v():
+    d, pool = _pool(3, 2, 8, 12, 2, 13)
+    src = np.array([0, 5, 7], np.int32)
+    dst = np.array([11, 1, 3], np.int32)
+    want = pool.copy()
+    want[:, :, dst] = pool[:, :, src]
+    orc.copy_blocks(d, pool, src, dst)
+    assert np.array_equal(pool, want)
+
+
+def test_copy_on_write_preserves_other_holders():
+    """COW: the writer's private copy equals the shared block except at the
+    newly written slot; the shared block is unchanged for its other holders."""
+    d, pool = _pool(2, 2, 8, 6, 4, 14)
+    shared, private = 2, 5
+    orc.copy_blocks(d, pool, [shared], [private])
+    before_shared = pool[:, :, shared].copy()
+    k = np.ones((1, 2, 8), np.float32)
+    orc.append(d, pool, 1, k, k, np.array([private * 16 + 4], np.int32))
+    assert np.array_equal(pool[:, :, shared], before_shared)
+    diff = pool[:, :, private] != before_shared
+    assert diff.any() and not diff[:, :, :4].any() and not diff[:, :, 5:].any() and not diff[0].any()
+
+
+# ------------------------------------------------------------- attention ----
+
+
+def _np_attention(pool, layer, q, indptr, ids, ctx, Hkv, scale, zero_sink=False):
+    """float64 restatement using library routines: np.repeat for the GQA
+    expansion (model.rs:398-408) and scipy.special.softmax (model.rs:414)."""
+    B, Hq, D = q.shape
+    rep = Hq // Hkv
+    out = np.zeros((B, Hq, D))
+    p64 = _widen(pool).astype(np.float64)
+    for b in range(B):
+        n = ctx[b]
+        tab = ids[indptr[b]:indptr[b + 1]]
+        t = np.arange(n)
+        K = p64[layer, 0, tab[t // 16], t % 16].transpose(1, 0, 2)  # [Hkv, n, D]
+        V = p64[layer, 1, tab[t // 16], t % 16].transpose(1, 0, 2)
+        if zero_sink:
+            K = np.concatenate([np.zeros((Hkv, 1, D)), K], axis=1)
+            V = np.concatenate([np.zeros((Hkv, 1, D)), V], axis=1)
+        Ke, Ve = np.repeat(K, rep, axis=0), np.repeat(V, rep, axis=0)
+        s = np.einsum("hd,htd->ht", q[b].astype(np.float64), Ke) * scale
+        p = scipy.special.softmax(s, axis=-1)
+        out[b] = np.einsum("ht,htd->hd", p, Ve)
+    return out
+
+
+CASES = [  # (Hq, Hkv, D, es)
+    (14, 2, 64, 4), (28, 4, 128, 2), (8, 1, 256, 2), (4, 4, 32, 4),
+]
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,es", CASES)
+@pytest.mark.parametrize("zero_sink", [False, True])
+def test_attention_against_float64_library_restatement(Hq, Hkv, D, es, zero_sink):
+    ctx = [1, 15, 16, 17, 90, 203]
+    nblocks = sum((c + 15) // 16 for c in ctx) + 3
+    d, pool = _pool(2, Hkv, D, nblocks, es, 20)
+    indptr, ids = _tables(ctx, nblocks, 21)
+    q = np.random.default_rng(22).standard_normal((len(ctx), Hq, D), dtype=np.float32)
+    if es == 2:
+        q = orc.bf16_to_f32(orc.f32_to_bf16(q))
+    scale = float(np.float32(D ** -0.5))
+    want = _np_attention(pool, 1, q, indptr, ids, ctx, Hkv, scale, zero_sink)
+    o32 = orc.decode_attention(d, pool, 1, q, indptr, ids, ctx, zero_sink=zero_sink)
+    o64 = orc.decode_attention(d, pool, 1, q, indptr, ids, ctx, zero_sink=zero_sink, precision="f64")
+    assert np.max(np.abs(o64 - want)) < 1e-12
+    assert np.max(np.abs(o32 - want)) < 2e-6
+
+
+def test_attention_closed_forms():
+    Hq, Hkv, D = 6, 2, 16
+    ctx = [1, 33]
+    nblocks = 4
+    d, pool = _pool(1, Hkv, D, nblocks, 4, 23)
+    indptr = np.array([0, 1, 4], np.int32)
+    ids = np.array([3, 0, 2, 1], np.int32)
+    q = np.random.default_rng(24).standard_normal((2, Hq, D), dtype=np.float32)
+    # ctx = 1: the output is the single value row.
+    o = orc.decode_attention(d, pool, 0, q, indptr, ids, ctx)
+    for h in range(Hq):
+        assert np.allclose(o[0, h], pool[0, 1, 3, 0, h // 3], atol=1e-7)
+    # constant V: the output is that constant, whatever the scores.
+    p2 = pool.copy()
+    p2[0, 1, :, :, 1, :] = np.arange(D, dtype=np.float32)
+    o = orc.decode_attention(d, p2, 0, q, indptr, ids, ctx)
+    assert np.allclose(o[1, 3:], np.arange(D), atol=1e-5)
+    # one dominant key: the output is (almost) its value row.
+    p3 = pool.copy()
+    qd = np.zeros((2, Hq, D), np.float32)
+    qd[1, :, 0] = 1.0
+    p3[0, 0, 2, 5, :, 0] = 200.0  # token 16+5 of sequence 1 lives in block 2 offset 5
+    o = orc.decode_attention(d, p3, 0, qd, indptr, ids, ctx)
+    assert np.allclose(o[1, 0], p3[0, 1, 2, 5, 0], atol=1e-5)
+    assert np.allclose(o[1, 5], p3[0, 1, 2, 5, 1], atol=1e-5)
+
+
+def test_attention_gqa_group_shares_kv_head():
+    """Query heads h and h' of the same group with equal queries give equal
+    outputs; heads of different groups do not."""
+    Hq, Hkv, D = 8, 2, 16
+    d, pool = _pool(1, Hkv, D, 3, 4, 25)
+    q = np.tile(np.random.default_rng(26).standard_normal((1, 1, D), dtype=np.float32), (1, Hq, 1))
+    o = orc.decode_attention(d, pool, 0, q, np.array([0, 3], np.int32), np.array([0, 1, 2], np.int32), [40])
+    assert np.array_equal(o[0, 0], o[0, 3]) and np.array_equal(o[0, 4], o[0, 7])
+    assert not np.allclose(o[0, 0], o[0, 4])
+
+
+def test_attention_invariant_under_block_permutation_bit_exact():
+    Hq, Hkv, D = 4, 2, 32
+    ctx = [50, 80]
+    d, pool = _pool(1, Hkv, D, 20, 2, 27)
+    indptr, ids = _tables(ctx, 20, 28)
+    q = np.random.default_rng(29).standard_normal((2, Hq, D), dtype=np.float32)
+    base = orc.decode_attention(d, pool, 0, q, indptr, ids, ctx)
+    perm = np.random.default_rng(30).permutation(20).astype(np.int32)
+    moved = np.empty_like(pool)
+    moved[:, :, perm] = pool
+    again = orc.decode_attention(d, moved, 0, q, indptr, perm[ids], ctx)
+    assert np.array_equal(base, again)
+
+
+def test_zero_sink_equals_explicit_phantom_slot():
+    """zero_sink on n tokens == plain attention on n+1 tokens whose first
+    K/V row is zero (the reference's init_cache zeros, model.rs:210-213)."""
+    Hq, Hkv, D = 4, 2, 16
+    d, pool = _pool(1, Hkv, D, 8, 4, 31)
+    n = 37
+    q = np.random.default_rng(32).standard_normal((1, Hq, D), dtype=np.float32)
+    t = np.arange(n)
+    rows_k = pool[0, 0, t // 16, t % 16].copy()
+    rows_v = pool[0, 1, t // 16, t % 16].copy()
+    with_sink = orc.decode_attention(d, pool, 0, q, np.array([0, 3], np.int32), np.arange(3, dtype=np.int32),
+                                     [n], zero_sink=True)
+    p2 = np.zeros_like(pool)
+    slots = np.arange(1, n + 1, dtype=np.int32) + 4 * 16
+    orc.append(d, p2, 0, rows_k, rows_v, slots)  # phantom zero row at block 4 offset 0
+    plain = orc.decode_attention(d, p2, 0, q, np.array([0, 3], np.int32), np.array([4, 5, 6], np.int32), [n + 1])
+    assert np.allclose(with_sink, plain, atol=1e-6)
+    assert not np.allclose(with_sink, orc.decode_attention(d, pool, 0, q, np.array([0, 3], np.int32),
+                                                           np.arange(3, dtype=np.int32), [n]), atol=1e-3)
+
+
+# ------------------------------------------------- planted mistakes (CPU) ----
+
+
+def test_checks_detect_planted_mistakes():
+    """Plausible mistakes, planted in a copy of the float64 restatement, move
+    the result far outside the f32 tolerance, so the checks above have power."""
+    Hq, Hkv, D = 8, 2, 32
+    ctx = [70, 45]
+    d, pool = _pool(1, Hkv, D, 12, 4, 33)
+    indptr, ids = _tables(ctx, 12, 34)
+    q = np.random.default_rng(35).standard_normal((2, Hq, D), dtype=np.float32)
+    scale = float(np.float32(D ** -0.5))
+    good = orc.decode_attention(d, pool, 0, q, indptr, ids, ctx)
+    assert np.max(np.abs(good - _np_attention(pool, 0, q, indptr, ids, ctx, Hkv, scale))) < 2e-6
+    mistakes = {
+        "gqa map h % Hkv": lambda: _np_attention_headmap(pool, q, indptr, ids, ctx, Hkv, scale),
+        "scale dropped": lambda: _np_attention(pool, 0, q, indptr, ids, ctx, Hkv, 1.0),
+        "K and V swapped": lambda: _np_attention(pool[:, ::-1].copy(), 0, q, indptr, ids, ctx, Hkv, scale),
+        "last token dropped": lambda: _np_attention(pool, 0, q, indptr, ids, [c - 1 for c in ctx], Hkv, scale),
+    }
+    for name, fn in mistakes.items():
+        assert np.max(np.abs(good - fn())) > 1e-3, name
+
+
+def _np_attention_headmap(pool, q, indptr, ids, ctx, Hkv, scale):
+    B, Hq, D = q.shape
+    out = np.zeros((B, Hq, D))
+    for b in range(B):
+        n = ctx[b]
+        tab = ids[indptr[b]:indptr[b + 1]]
+        t = np.arange(n)
+        K = pool[0, 0, tab[t // 16], t % 16].transpose(1, 0, 2).astype(np.float64)
+        V = pool[0, 1, tab[t // 16], t % 16].transpose(1, 0, 2).astype(np.float64)
+        for h in range(Hq):
+            s = K[h % Hkv] @ q[b, h] * scale
+            out[b, h] = scipy.special.softmax(s) @ V[h % Hkv]
+    return out
