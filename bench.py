@@ -1,0 +1,204 @@
+"""Decode-step benchmark of the paged-KV hot path on one MI355X.
+
+One step = for every layer of the Qwen2.5-7B-shaped batch (28 layers, 28 query
+heads, 4 KV heads, head_dim 128, bf16 KV, block size 16, 64 sequences with
+context lengths uniform in [1024, 8192], block tables drawn from a seeded
+permutation of the pool): append the step's K/V row of every sequence into its
+slot, then run paged GQA decode attention over context + 1 tokens.
+
+Prints one JSON line: whole-step HBM throughput in algorithmic bytes (K/V
+read once, Q read, O written, appends read+written, block tables and slot
+ids), tokens/s, the attention kernel's roofline fraction measured with HIP
+events on its stream over the timed region, and the CPU baseline (the
+oracle's reference-faithful restatement of the reference's CPU attention,
+timed on a bounded sample on this host).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "paged KV append+decode-attn achieved HBM GB/s (% peak); decode tokens/s"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="qwen2.5-7b")
+    ap.add_argument("--split-tokens", type=int, default=0)
+    ap.add_argument("--kernel", choices=["auto", "mfma", "valu"], default="auto")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def cpu_info():
+    model = platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return model
+
+
+def cpu_baseline(cfg, batch, step_bytes):
+    """Reference-faithful CPU decode (contiguous f32 cache grown by a copy per
+    token, repeat_kv materialised, mask, softmax, matmuls) for one layer of
+    every sequence of the batch, scaled to a full step. The primary figure is
+    one thread, sequences one after another, as the reference executes
+    requests serially (inference-backend/src/burn_backend.rs:44-71); the same
+    sample threaded over sequences is reported beside it."""
+    from oracle import oracle as orc
+
+    ctx = batch.ctx_lens
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    orc.set_num_threads(1)
+    t1 = orc.ref_faithful_batch(ctx, cfg["num_kv_heads"], cfg["num_q_heads"], cfg["head_dim"], seed=1)
+    orc.set_num_threads(threads)
+    tn = orc.ref_faithful_batch(ctx, cfg["num_kv_heads"], cfg["num_q_heads"], cfg["head_dim"], seed=2)
+    step_1t, step_nt = t1 * cfg["num_layers"], tn * cfg["num_layers"]
+    return {
+        "value": round(step_bytes / step_1t / 1e9, 3),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"1 of {cfg['num_layers']} layers x all {batch.num_seqs} sequences, 1 thread, "
+                   f"{t1:.1f} s; scaled to a full step"),
+        "tokens_per_s": round(batch.num_seqs / step_1t, 2),
+        "ms_per_step": round(step_1t * 1e3, 1),
+        "threaded": {"value": round(step_bytes / step_nt / 1e9, 3), "unit": "GB/s", "cores": threads,
+                     "tokens_per_s": round(batch.num_seqs / step_nt, 2),
+                     "sample": f"same sample, {threads} threads over sequences, {tn:.1f} s"},
+        "cpu_model": cpu_info(),
+        "host_cpus": os.cpu_count(),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: every box here has one MI355X and this path runs "
+              f"on a single device (requested --gpus {args.gpus}).", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from mitten_amd import DeviceKvPool, PoolDesc
+    from mitten_amd import workloads as wl
+
+    cfg = wl.CONFIGS[args.config]
+    batch = wl.config_batch(args.config)
+    L, Hq, Hkv, D, dt = cfg["num_layers"], cfg["num_q_heads"], cfg["num_kv_heads"], cfg["head_dim"], cfg["dtype"]
+    B = batch.num_seqs
+    desc = PoolDesc(L, Hkv, Hq, D, batch.num_blocks, dt)
+    dev = torch.device("cuda:0")
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    es = desc.elem_bytes
+
+    pool = DeviceKvPool(desc)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(batch.seed)
+    view = pool.tensor()
+    for layer in range(L):  # N(0,1) K/V in every slot, one layer at a time
+        view[layer].normal_(generator=gen)
+    del view
+    q = torch.randn((L, B, Hq, D), generator=gen, device=dev, dtype=torch.float32).to(tdt)
+    k_new = torch.randn((L, B, Hkv, D), generator=gen, device=dev, dtype=torch.float32).to(tdt)
+    v_new = torch.randn((L, B, Hkv, D), generator=gen, device=dev, dtype=torch.float32).to(tdt)
+    out = torch.empty_like(q)
+    i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(dev)
+    indptr, ids, ctx, slots = (i32(batch.block_indptr), i32(batch.block_ids), i32(batch.ctx_lens),
+                               i32(batch.slot_mapping))
+    max_ctx = batch.max_ctx
+    kernel = None if args.kernel == "auto" else args.kernel
+    ws = torch.empty(max(1, pool.workspace_size(B, max_ctx, args.split_tokens)), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+
+    attn_bytes = wl.algorithmic_bytes_attention(batch, Hq, Hkv, D, es)
+    app_bytes = wl.algorithmic_bytes_append(B, Hkv, D, es)
+    step_bytes = L * (attn_bytes + app_bytes)
+
+    def step(events=None):
+        for layer in range(L):
+            pool.append(layer, k_new[layer], v_new[layer], slots, stream=stream)
+            if events is not None:
+                events[layer][0].record(stream)
+            pool.decode_attention(layer, q[layer], indptr, ids, ctx, max_ctx, out=out[layer],
+                                  split_tokens=args.split_tokens, workspace=ws, kernel=kernel, stream=stream)
+            if events is not None:
+                events[layer][1].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    pool.check()
+
+    ev = [[[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(L)]
+          for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        step(ev[s])
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    pool.check()
+    elapsed = t1 - t0
+    ms_step = elapsed / args.steps * 1e3
+    attn_ms = [e[0].elapsed_time(e[1]) for st in ev for e in st]
+    attn_avg_s = float(np.mean(attn_ms)) / 1e3
+    gbs = step_bytes / (elapsed / args.steps) / 1e9
+    attn_gbs = attn_bytes / attn_avg_s / 1e9
+
+    result = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dt,
+        "data": "synthetic: N(0,1) K/V/Q from a seed; block tables from a seeded permutation of the pool",
+        "config": {"workload": f"{args.config} decode step (append + paged decode attention per layer)",
+                   "layers": L, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "block_size": 16,
+                   "sequences": B, "ctx_range": [cfg["ctx_lo"], cfg["ctx_hi"]],
+                   "tokens_attended": batch.total_tokens, "pool_blocks": batch.num_blocks,
+                   "pool_bytes": pool.nbytes, "seed": batch.seed, "split_tokens": args.split_tokens,
+                   "kernel": args.kernel},
+        "pct_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
+        "tokens_per_s": round(B / (elapsed / args.steps), 1),
+        "step_bytes": step_bytes,
+        "roofline": {"bound": "hbm", "achieved": round(attn_gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(attn_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "decode_attention (per layer launch)",
+                     "bytes_per_launch": attn_bytes, "avg_launch_us": round(attn_avg_s * 1e6, 2)},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(cfg, batch, step_bytes)
+    pool.close()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -412,3 +412,52 @@ ORC_API void orc_set_num_threads(int n) {
   (void)n;
 #endif
 }
+
+/* Timed CPU baseline over a batch: for every sequence b (in parallel over
+ * sequences with OpenMP), one decode step of one layer executed as
+ * orc_ref_faithful_decode does, starting from a contiguous cache of
+ * ctx[b] - 1 tokens (filled with seeded N(0,1) values) and appending one
+ * token. Cache set-up is outside the timed region; returns the wall time of
+ * the decode steps in seconds. */
+ORC_API double orc_ref_faithful_batch(const int32_t *ctx, int32_t num_seqs, int32_t Hkv, int32_t Hq,
+                                      int32_t D, uint64_t seed) {
+  float **kc = (float **)calloc(num_seqs, sizeof(float *));
+  float **vc = (float **)calloc(num_seqs, sizeof(float *));
+  float **qn = (float **)calloc(num_seqs, sizeof(float *));
+  float **on = (float **)calloc(num_seqs, sizeof(float *));
+#pragma omp parallel for schedule(dynamic)
+  for (int b = 0; b < num_seqs; b++) {
+    const int64_t T = ctx[b] - 1;
+    kc[b] = (float *)malloc(sizeof(float) * Hkv * (T > 0 ? T : 1) * D);
+    vc[b] = (float *)malloc(sizeof(float) * Hkv * (T > 0 ? T : 1) * D);
+    qn[b] = (float *)malloc(sizeof(float) * (Hq + 2 * Hkv) * D);
+    on[b] = (float *)malloc(sizeof(float) * Hq * D);
+    orc_fill_normal_f32(seed + 3 * (uint64_t)b, Hkv * T * D, kc[b]);
+    orc_fill_normal_f32(seed + 3 * (uint64_t)b + 1, Hkv * T * D, vc[b]);
+    orc_fill_normal_f32(seed + 3 * (uint64_t)b + 2, (Hq + 2 * Hkv) * D, qn[b]);
+  }
+  double t0 = 0.0, t1 = 0.0;
+#ifdef _OPENMP
+  t0 = omp_get_wtime();
+#endif
+#pragma omp parallel for schedule(dynamic)
+  for (int b = 0; b < num_seqs; b++) {
+    const float scale = 1.0f / sqrtf((float)D);
+    orc_ref_faithful_decode(&kc[b], &vc[b], ctx[b] - 1, Hkv, Hq, D, qn[b] + Hq * D,
+                            qn[b] + (Hq + Hkv) * D, qn[b], scale, on[b]);
+  }
+#ifdef _OPENMP
+  t1 = omp_get_wtime();
+#endif
+  for (int b = 0; b < num_seqs; b++) {
+    free(kc[b]);
+    free(vc[b]);
+    free(qn[b]);
+    free(on[b]);
+  }
+  free(kc);
+  free(vc);
+  free(qn);
+  free(on);
+  return t1 - t0;
+}

@@ -63,6 +63,7 @@ def lib():
             "orc_decode_attention_f64": (ctypes.c_int, [dp, P, ctypes.c_int, P, i32, i32, P, P, P,
                                                         f64, ctypes.c_int, P]),
             "orc_ref_faithful_decode": (ctypes.c_int, [P, P, i64, i32, i32, i32, P, P, P, f32, P]),
+            "orc_ref_faithful_batch": (ctypes.c_double, [P, i32, i32, i32, i32, ctypes.c_uint64]),
             "orc_num_threads": (ctypes.c_int, []),
             "orc_set_num_threads": (None, [ctypes.c_int]),
         }
@@ -184,6 +185,13 @@ def decode_attention(d: PoolDesc, pool: np.ndarray, layer: int, q: np.ndarray, i
     if rc != 0:
         raise ValueError("orc_decode_attention: invalid arguments")
     return o
+
+
+def ref_faithful_batch(ctx, Hkv: int, Hq: int, D: int, seed: int = 1) -> float:
+    """Seconds for one reference-faithful decode step (one layer) of every
+    sequence; ctx[b] counts the appended token."""
+    c = np.ascontiguousarray(ctx, np.int32)
+    return lib().orc_ref_faithful_batch(_p(c), c.size, Hkv, Hq, D, ctypes.c_uint64(seed))
 
 
 def num_threads() -> int:
