@@ -40,10 +40,30 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="qwen2.5-7b")
+    ap.add_argument("--mode", choices=["step", "planned", "split"], default="step",
+                    help="step: plan + fused append/attention per layer; planned: plan, append, "
+                         "attention; split: append + split-grid attention")
+    ap.add_argument("--pieces", type=int, default=0)
     ap.add_argument("--split-tokens", type=int, default=0)
     ap.add_argument("--kernel", choices=["auto", "mfma", "valu"], default="auto")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-launch-events", action="store_true",
+                    help="time the steps without per-launch HIP events (roofline fields null)")
     return ap.parse_args()
+
+
+def profiled_traffic(config: str, mode: str):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary of this
+    workload (FETCH_SIZE and WRITE_SIZE, scaled by a 1 GiB copy kernel)."""
+    path = os.path.join(ROOT, "profiles", f"decode_{mode}_{config}_hbm_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1]), os.path.relpath(path, ROOT)
+    except OSError:
+        pass
+    return None, None
 
 
 def cpu_info():
@@ -134,38 +154,63 @@ def main():
     attn_bytes = wl.algorithmic_bytes_attention(batch, Hq, Hkv, D, es)
     app_bytes = wl.algorithmic_bytes_append(B, Hkv, D, es)
     step_bytes = L * (attn_bytes + app_bytes)
+    # Bytes of the launch the HIP events bracket: the fused step moves the
+    # append's bytes too.
+    launch_bytes = attn_bytes + (app_bytes if args.mode == "step" else 0)
+
+    ctx_host = batch.ctx_lens.copy()
+    plan = pool.plan(ctx_host, pieces=args.pieces, stream=stream)
+
+    run_layer = pool.bind_decode_step(plan, k_new, v_new, q, indptr, ids, out, kernel=kernel, stream=stream)
 
     def step(events=None):
+        """events: None, or L+1 timing events recorded between launches (the
+        fused step has nothing else between consecutive layers)."""
+        if args.mode != "split":
+            plan.build(ctx_host, args.pieces, stream=stream)  # host plan of this step
         for layer in range(L):
-            pool.append(layer, k_new[layer], v_new[layer], slots, stream=stream)
+            if args.mode != "step":
+                pool.append(layer, k_new[layer], v_new[layer], slots, stream=stream)
             if events is not None:
-                events[layer][0].record(stream)
-            pool.decode_attention(layer, q[layer], indptr, ids, ctx, max_ctx, out=out[layer],
-                                  split_tokens=args.split_tokens, workspace=ws, kernel=kernel, stream=stream)
-            if events is not None:
-                events[layer][1].record(stream)
+                events[layer].record(stream)
+            if args.mode == "step":
+                run_layer(layer)
+            elif args.mode == "planned":
+                pool.decode_attention_planned(layer, plan, q[layer], indptr, ids, out=out[layer],
+                                              kernel=kernel, stream=stream)
+            else:
+                pool.decode_attention(layer, q[layer], indptr, ids, ctx, max_ctx, out=out[layer],
+                                      split_tokens=args.split_tokens, workspace=ws, kernel=kernel,
+                                      stream=stream)
+        if events is not None:
+            events[L].record(stream)
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
     pool.check()
 
-    ev = [[[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(L)]
-          for _ in range(args.steps)]
+    # Launch timing: an event chain around every layer's launch on every
+    # EVENT_EVERY-th timed step (events cost GPU time; sampling keeps the
+    # timed steps close to unperturbed).
+    EVENT_EVERY = 4
+    timed = [s for s in range(args.steps) if s % EVENT_EVERY == 0 and not args.no_launch_events]
+    ev = {s: [torch.cuda.Event(enable_timing=True) for _ in range(L + 1)] for s in timed}
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for s in range(args.steps):
-        step(ev[s])
+        step(ev.get(s))
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     pool.check()
     elapsed = t1 - t0
     ms_step = elapsed / args.steps * 1e3
-    attn_ms = [e[0].elapsed_time(e[1]) for st in ev for e in st]
+    attn_ms = [e[i].elapsed_time(e[i + 1]) for e in ev.values() for i in range(L)] or [float("nan")]
     attn_avg_s = float(np.mean(attn_ms)) / 1e3
     gbs = step_bytes / (elapsed / args.steps) / 1e9
-    attn_gbs = attn_bytes / attn_avg_s / 1e9
+    attn_gbs = launch_bytes / attn_avg_s / 1e9
 
+    traffic, traffic_src = profiled_traffic(args.config, args.mode)
     result = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -183,19 +228,24 @@ def main():
                    "layers": L, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "block_size": 16,
                    "sequences": B, "ctx_range": [cfg["ctx_lo"], cfg["ctx_hi"]],
                    "tokens_attended": batch.total_tokens, "pool_blocks": batch.num_blocks,
-                   "pool_bytes": pool.nbytes, "seed": batch.seed, "split_tokens": args.split_tokens,
-                   "kernel": args.kernel},
+                   "pool_bytes": pool.nbytes, "seed": batch.seed, "mode": args.mode,
+                   "plan": plan.info(), "split_tokens": args.split_tokens, "kernel": args.kernel},
         "pct_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "tokens_per_s": round(B / (elapsed / args.steps), 1),
         "step_bytes": step_bytes,
         "roofline": {"bound": "hbm", "achieved": round(attn_gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(attn_gbs / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": "decode_attention (per layer launch)",
-                     "bytes_per_launch": attn_bytes, "avg_launch_us": round(attn_avg_s * 1e6, 2)},
+                     "frac": round(attn_gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src,
+                     "kernel": {"step": "mkv_decode_step (append + attention + merge, per layer)",
+                                "planned": "mkv_decode_attention_planned (attention + merge, per layer)",
+                                "split": "mkv_decode_attention (attention + merge, per layer)"}[args.mode],
+                     "bytes_per_launch": launch_bytes, "avg_launch_us": round(attn_avg_s * 1e6, 2),
+                     "launches_timed": len(attn_ms) if ev else 0},
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg, batch, step_bytes)
+    plan.close()
     pool.close()
     print(json.dumps(result), flush=True)
 

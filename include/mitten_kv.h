@@ -172,6 +172,41 @@ MKV_API int mkv_decode_attention_workspace_size(const mkv_pool *pool, int32_t nu
                                         int32_t max_ctx_len, int32_t split_tokens,
                                         uint64_t *out_bytes);
 
+/* ---- planned decode (production path) ----------------------------------- */
+
+/* A decode plan is the work decomposition of one engine step, built on the
+ * host from the host-side context lengths (the scheduler has them: it is the
+ * Batch it assembles, inference-engine/src/scheduler.rs:29-77) and uploaded
+ * once; every layer's attention call of that step reuses it. The
+ * concatenation of all sequences' blocks is cut into `pieces` equal runs,
+ * one workgroup each, so the work per workgroup does not depend on how
+ * ragged the contexts are. The plan owns its metadata and split-K scratch. */
+typedef struct mkv_decode_plan mkv_decode_plan;
+
+MKV_API int mkv_decode_plan_create(mkv_pool *pool, mkv_decode_plan **out_plan);
+MKV_API int mkv_decode_plan_destroy(mkv_decode_plan *plan);
+/* h_ctx_lens: host array, tokens each sequence attends (>= 1).
+ * pieces: 0 = chosen by the library. Uploads asynchronously on `stream`. */
+MKV_API int mkv_decode_plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens,
+                                  int32_t num_seqs, int32_t pieces, void *stream);
+MKV_API int mkv_decode_plan_info(const mkv_decode_plan *plan, int32_t *out_pieces,
+                                 int32_t *out_blocks_per_piece, int32_t *out_merge_seqs);
+/* mkv_decode_attention over the plan's sequences and context lengths. */
+MKV_API int mkv_decode_attention_planned(mkv_pool *pool, const mkv_decode_plan *plan,
+                                         int32_t layer, const void *d_q, void *d_o,
+                                         const int32_t *d_block_indptr,
+                                         const int32_t *d_block_ids, float scale,
+                                         uint32_t flags, void *stream);
+/* One decode step of one layer in one launch: for every sequence b, write
+ * d_k_new[b], d_v_new[b] ([num_seqs][num_kv_heads][head_dim]) at position
+ * ctx_b - 1 (its slot from its block table), then attend over ctx_b tokens.
+ * Equal to mkv_append at those slots followed by
+ * mkv_decode_attention_planned. Replaces model.rs:390-416 for one layer. */
+MKV_API int mkv_decode_step(mkv_pool *pool, const mkv_decode_plan *plan, int32_t layer,
+                            const void *d_k_new, const void *d_v_new, const void *d_q, void *d_o,
+                            const int32_t *d_block_indptr, const int32_t *d_block_ids,
+                            float scale, uint32_t flags, void *stream);
+
 /* ---- host-side validation (pure CPU; no device access) ------------------- */
 
 /* 0 <= slot < num_blocks*page_size for every slot. */

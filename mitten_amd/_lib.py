@@ -47,6 +47,12 @@ DEVICE_SIGNATURES = {
     "mkv_copy_blocks": (c_int, [P, P, P, i32, P]),
     "mkv_decode_attention": (c_int, [P, i32, P, P, P, P, P, i32, i32, f32, u32, i32, P, u64, P]),
     "mkv_decode_attention_workspace_size": (c_int, [P, i32, i32, i32, ctypes.POINTER(u64)]),
+    "mkv_decode_plan_create": (c_int, [P, ctypes.POINTER(P)]),
+    "mkv_decode_plan_destroy": (c_int, [P]),
+    "mkv_decode_plan_build": (c_int, [P, I32P, i32, i32, P]),
+    "mkv_decode_plan_info": (c_int, [P, I32P, I32P, I32P]),
+    "mkv_decode_attention_planned": (c_int, [P, P, i32, P, P, P, P, f32, u32, P]),
+    "mkv_decode_step": (c_int, [P, P, i32, P, P, P, P, P, P, f32, u32, P]),
     "mkv_validate_slots": (c_int, [DESC_P, I32P, i32]),
     "mkv_validate_block_tables": (c_int, [DESC_P, I32P, I32P, I32P, i32, i32]),
     "mkv_validate_copy_pairs": (c_int, [DESC_P, I32P, I32P, i32]),
@@ -85,7 +91,9 @@ def device_lib():
             import torch  # noqa: F401
         except ImportError:
             pass
-        _device = _load(_build.DEVICE_LIB, DEVICE_SIGNATURES)
+        # MITTEN_KV_LIBRARY selects another build of the same library
+        # (for example a variant compiled with other tuning constants).
+        _device = _load(os.environ.get("MITTEN_KV_LIBRARY", _build.DEVICE_LIB), DEVICE_SIGNATURES)
     return _device
 
 

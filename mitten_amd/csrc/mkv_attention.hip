@@ -1,32 +1,40 @@
 // Paged GQA/MQA decode attention, straight from the block pool.
 //
-// Work decomposition: one wave64 per unit (sequence b, context split, KV head
-// h, query chunk qc); a 256-thread workgroup holds four consecutive units, so
-// with 4 KV heads one workgroup streams all heads of the same blocks. Each
-// unit runs an online (max-subtracted, base-2) softmax over its split and
-// either writes the final normalised row (single split) or an unnormalised
-// partial (m, l, o[D]) that merge_kernel combines by log-sum-exp.
-//
-// Two kernels:
-//   attn_mfma_kernel  bf16 KV, head_dim 64/128/256, up to 16 query heads per
-//                     wave. S^T = K.Q^T on v_mfma_f32_16x16x32_bf16 with K
-//                     loaded straight into the A-operand layout (16 B per
-//                     lane, no LDS), O^T = V^T.P^T on v_mfma_f32_16x16x16_bf16
-//                     with V transposed in registers by a 4x4 DPP quad
-//                     transpose. The S^T accumulator layout equals the P^T
-//                     operand layout, and the O^T accumulator puts query row
-//                     q = lane%16 where the softmax state lives, so no
-//                     cross-lane traffic is needed for the rescale.
-//   attn_valu_kernel  any dtype, head_dim 32/64/128/256: lanes split each
-//                     token row into 16-byte chunks, scores reduce across
-//                     the row's lanes with shuffles. f32 pools use this one.
-//
 // Arithmetic follows inference-model-qwen/src/model.rs:394-416: scores are
 // (q.k) * scale with scale = head_dim^-0.5 (model.rs:298), softmax is the
-// max-subtracted exponential, the output is p.v; the KV head of query head h
-// is h / (num_q_heads/num_kv_heads) (repeat_kv, model.rs:398-408).
+// max-subtracted exponential, the output is p.v; query head h reads KV head
+// h / (num_q_heads/num_kv_heads) (repeat_kv, model.rs:398-408). Softmax runs
+// online in base 2 with f32 state; a sequence's context can be cut into
+// segments whose unnormalised partials (m, l, o[D]) merge by log-sum-exp.
+//
+// Hot loop (one wave64 per (sequence segment, KV head, chunk of <= 16 query
+// heads)), bf16 KV with head_dim 64/128/256:
+//   S^T = K.Q^T  v_mfma_f32_16x16x32_bf16: each lane loads 16 B of one K row
+//                straight into the A-operand layout (no LDS);
+//   O^T = V^T.P^T v_mfma_f32_16x16x16_bf16: the S^T accumulator layout is
+//                already the P^T operand layout; V is transposed in registers
+//                by a 4x4 DPP quad transpose; the O^T accumulator keeps query
+//                row q = lane%16, where that row's softmax state lives;
+//   loads run three blocks deep in a register ring, so two blocks stay in
+//   flight while one is computed; the running max moves only when it grows
+//   by more than 2^8, so O is rarely rescaled.
+// Other dtypes/shapes use a VALU loop: lanes split a token row into 16-byte
+// chunks and reduce scores across the row's lanes with shuffles.
+//
+// Two work decompositions:
+//   split grid (mkv_decode_attention): units (sequence, split, KV head, query
+//     chunk) over a grid sized by max_ctx_len; partials merge in merge_split.
+//   plan (mkv_decode_attention_planned / mkv_decode_step): the host cuts the
+//     concatenation of all sequences' blocks into equal pieces, one workgroup
+//     per piece (all KV heads of the same blocks in one workgroup), so every
+//     workgroup streams the same bytes whatever the context lengths;
+//     sequences cut by a piece boundary merge in merge_planned (a second
+//     launch: merging inside the first through an arrival counter needs an
+//     agent-scope release/acquire per piece, which measured slower).
 #include <algorithm>
 #include <cmath>
+#include <new>
+#include <vector>
 
 #include "mkv_internal.h"
 
@@ -38,65 +46,37 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kRescaleSlack = 8.0f;  // log2 units: p <= 2^8 between rescales
+constexpr int kQChunkMfma = 16;
+constexpr int kQChunkValu = 8;
+constexpr int kRing = 3;               // MFMA loop: blocks loaded ahead + 1
 
-struct AttnArgs {
+// Kernel-side geometry and per-call arguments shared by every variant.
+struct KArgs {
   const uint8_t *k_plane;  // layer's K plane
   const uint8_t *v_plane;  // layer's V plane
-  const void *q;
-  void *o;
+  uint8_t *k_plane_w;      // same planes, writable (fused append)
+  uint8_t *v_plane_w;
+  const void *q;           // [B][Hq][D]
+  void *o;                 // [B][Hq][D]
+  const uint8_t *new_k;    // fused append: [B][Hkv][D] or nullptr
+  const uint8_t *new_v;
   const int32_t *indptr;
   const int32_t *ids;
-  const int32_t *ctx_lens;
-  float *ws_ml;  // [B][Hq][S] (m, l) pairs
-  float *ws_o;   // [B][Hq][S][D]
+  float *ws_ml;  // partial (m, l) pairs
+  float *ws_o;   // partial o rows, f32 [D]
   uint32_t *d_err;
   int64_t nblocks;
   int64_t row_bytes;
   int64_t block_bytes;
-  int64_t total_units;
-  int32_t B, Hq, Hkv, G, nqc, S, split_tokens, max_ctx;
+  int32_t Hq, Hkv, G, nqc;
   float sl2;  // scale * log2(e)
   int32_t zero_sink;
 };
 
-struct Unit {
-  int b, split, h, qc;
-  int ctx, t_begin, t_end, nsp, tab0;
-};
-
-// Decodes the wave's unit and validates its sequence; false = nothing to do.
-__device__ __forceinline__ bool decode_unit(const AttnArgs &a, int lane, Unit &u) {
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  int64_t id = (int64_t)blockIdx.x * 4 + wave;
-  if (id >= a.total_units) return false;
-  u.qc = (int)(id % a.nqc);
-  id /= a.nqc;
-  u.h = (int)(id % a.Hkv);
-  id /= a.Hkv;
-  u.split = (int)(id % a.S);
-  u.b = (int)(id / a.S);
-  const bool first = u.split == 0 && u.h == 0 && u.qc == 0 && lane == 0;
-  u.ctx = a.ctx_lens[u.b];
-  if (u.ctx < 1 || u.ctx > a.max_ctx) {
-    if (first) record_error(a.d_err, MKV_DEVERR_CTX);
-    return false;
-  }
-  u.t_begin = u.split * a.split_tokens;
-  if (u.t_begin >= u.ctx) return false;
-  u.t_end = min(u.ctx, u.t_begin + a.split_tokens);
-  u.nsp = (u.ctx + a.split_tokens - 1) / a.split_tokens;
-  u.tab0 = a.indptr[u.b];
-  const int tabn = a.indptr[u.b + 1] - u.tab0;
-  if (u.tab0 < 0 || tabn < (u.ctx + kPageSize - 1) / kPageSize) {
-    if (first) record_error(a.d_err, MKV_DEVERR_TABLE);
-    return false;
-  }
-  return true;
-}
-
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Final normalisation of one row, including the optional phantom zero key
+// Normalisation factor of one row, including the optional phantom zero key
 // (score 0, value 0) of the reference's Qwen cache (model.rs:210-213).
 __device__ __forceinline__ float final_scale(float m, float l, int zero_sink) {
   if (zero_sink) {
@@ -107,149 +87,41 @@ __device__ __forceinline__ float final_scale(float m, float l, int zero_sink) {
   return 1.0f / l;
 }
 
-// ---------------------------------------------------------------------------
-// VALU kernel.
-// ---------------------------------------------------------------------------
-template <int D, bool BF16>
-__global__ void __launch_bounds__(256) attn_valu_kernel(AttnArgs a) {
-  constexpr int ES = BF16 ? 2 : 4;
-  constexpr int VEC = 16 / ES;
-  constexpr int LPT = D / VEC;
-  static_assert(LPT >= 1 && LPT <= 64 && (64 % LPT) == 0, "unsupported head_dim");
-  constexpr int TPI = 64 / LPT;
-  constexpr int QC = 8;
-  const int lane = threadIdx.x & 63;
-  Unit u;
-  if (!decode_unit(a, lane, u)) return;
-  const int lt = lane / LPT, ld = lane % LPT;
-  const int q0 = u.qc * QC;
-  const int nq = min(QC, a.G - q0);
-  const int hq0 = u.h * a.G + q0;
-
-  auto load_chunk = [&](const uint8_t *p, float (&f)[VEC]) {
-    const u32x4 w = *reinterpret_cast<const u32x4 *>(p);
-    if constexpr (BF16) {
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        f[2 * e] = bf16_lo(w[e]);
-        f[2 * e + 1] = bf16_hi(w[e]);
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; e++) f[e] = __uint_as_float(w[e]);
-    }
-  };
-
-  float qv[QC][VEC];
-#pragma unroll
-  for (int g = 0; g < QC; g++) {
-    if (g < nq) {
-      const uint8_t *qp = reinterpret_cast<const uint8_t *>(a.q) +
-                          ((int64_t)(u.b * a.Hq + hq0 + g) * D + ld * VEC) * ES;
-      load_chunk(qp, qv[g]);
-#pragma unroll
-      for (int e = 0; e < VEC; e++) qv[g][e] *= a.sl2;
-    } else {
-#pragma unroll
-      for (int e = 0; e < VEC; e++) qv[g][e] = 0.0f;
-    }
-  }
-  float m[QC], l[QC], acc[QC][VEC];
-#pragma unroll
-  for (int g = 0; g < QC; g++) {
-    m[g] = -INFINITY;
-    l[g] = 0.0f;
-#pragma unroll
-    for (int e = 0; e < VEC; e++) acc[g][e] = 0.0f;
-  }
-  const int64_t head_off = (int64_t)u.h * D * ES + ld * 16;
-  const int n_iter = (u.t_end - u.t_begin + TPI - 1) / TPI;
-  for (int it = 0; it < n_iter; it++) {
-    const int t = u.t_begin + it * TPI + lt;
-    bool valid = t < u.t_end;
-    float kf[VEC], vf[VEC];
-#pragma unroll
-    for (int e = 0; e < VEC; e++) kf[e] = vf[e] = 0.0f;
-    if (valid) {
-      const int32_t blk = a.ids[u.tab0 + t / kPageSize];
-      if (blk < 0 || blk >= a.nblocks) {
-        record_error(a.d_err, MKV_DEVERR_BLOCK);
-        valid = false;
-      } else {
-        const int64_t off = (int64_t)blk * a.block_bytes + (t % kPageSize) * a.row_bytes + head_off;
-        load_chunk(a.k_plane + off, kf);
-        load_chunk(a.v_plane + off, vf);
-      }
-    }
-#pragma unroll
-    for (int g = 0; g < QC; g++) {
-      if (g >= nq) break;
-      float s = 0.0f;
-#pragma unroll
-      for (int e = 0; e < VEC; e++) s = fmaf(qv[g][e], kf[e], s);
-#pragma unroll
-      for (int o = LPT / 2; o >= 1; o >>= 1) s += __shfl_xor(s, o);
-      if (valid) {
-        const float mn = fmaxf(m[g], s);
-        const float al = fast_exp2(m[g] - mn);
-        const float p = fast_exp2(s - mn);
-        l[g] = l[g] * al + p;
-#pragma unroll
-        for (int e = 0; e < VEC; e++) acc[g][e] = fmaf(p, vf[e], acc[g][e] * al);
-        m[g] = mn;
-      }
-    }
-  }
-  // Merge the TPI token slots of the wave (lanes sharing ld).
-#pragma unroll
-  for (int o = LPT; o < 64; o <<= 1) {
-#pragma unroll
-    for (int g = 0; g < QC; g++) {
-      if (g >= nq) break;
-      const float mo = __shfl_xor(m[g], o);
-      const float lo = __shfl_xor(l[g], o);
-      const float M = fmaxf(m[g], mo);
-      const float fa = m[g] == -INFINITY ? 0.0f : fast_exp2(m[g] - M);
-      const float fb = mo == -INFINITY ? 0.0f : fast_exp2(mo - M);
-      l[g] = l[g] * fa + lo * fb;
-#pragma unroll
-      for (int e = 0; e < VEC; e++) acc[g][e] = acc[g][e] * fa + __shfl_xor(acc[g][e], o) * fb;
-      m[g] = M;
-    }
-  }
-  if (lt != 0) return;
-#pragma unroll
-  for (int g = 0; g < QC; g++) {
-    if (g >= nq) break;
-    const int hq = hq0 + g;
-    if (u.nsp == 1) {
-      const float f = final_scale(m[g], l[g], a.zero_sink);
-      uint8_t *op = reinterpret_cast<uint8_t *>(a.o) + ((int64_t)(u.b * a.Hq + hq) * D + ld * VEC) * ES;
-      u32x4 w;
-      if constexpr (BF16) {
-#pragma unroll
-        for (int e = 0; e < 4; e++) w[e] = pack_bf16x2(acc[g][2 * e] * f, acc[g][2 * e + 1] * f);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; e++) w[e] = __float_as_uint(acc[g][e] * f);
-      }
-      *reinterpret_cast<u32x4 *>(op) = w;
-    } else {
-      const int64_t idx = ((int64_t)u.b * a.Hq + hq) * a.S + u.split;
-      float *wo = a.ws_o + idx * D + ld * VEC;
-#pragma unroll
-      for (int e = 0; e < VEC; e++) wo[e] = acc[g][e];
-      if (ld == 0) {
-        a.ws_ml[2 * idx] = m[g];
-        a.ws_ml[2 * idx + 1] = l[g];
-      }
-    }
+// Writes the step's new K/V row of (sequence, KV head) into its slot:
+// block `blk`, row `row`. Lanes split the two D-element rows in 16 B chunks.
+template <int D, int ES>
+__device__ __forceinline__ void store_new_row(const KArgs &a, int lane, int b, int h, int32_t blk,
+                                              int row) {
+  constexpr int NC = D * ES / 16;
+  const int64_t src = ((int64_t)b * a.Hkv + h) * D * ES;
+  const int64_t dst = (int64_t)blk * a.block_bytes + (int64_t)row * a.row_bytes + (int64_t)h * D * ES;
+  for (int c = lane; c < 2 * NC; c += 64) {
+    const int kv = c >= NC, cc = c - kv * NC;
+    const u32x4 w = *reinterpret_cast<const u32x4 *>((kv ? a.new_v : a.new_k) + src + 16 * cc);
+    *reinterpret_cast<u32x4 *>((kv ? a.v_plane_w : a.k_plane_w) + dst + 16 * cc) = w;
   }
 }
 
-// ---------------------------------------------------------------------------
-// MFMA kernel (bf16).
-// ---------------------------------------------------------------------------
+// One (sequence, KV head, query chunk) stretch of blocks [j0, j1) of a
+// sequence with `ctx` tokens whose block table starts at ids + tab0.
+struct Seg {
+  int b, h, qc;
+  int ctx;
+  int j0, j1;
+  const int32_t *table;  // ids + tab0
+  const uint8_t *nk;     // fused append: new K row (this head) or nullptr
+  const uint8_t *nv;
+};
+
+// ===========================================================================
+// MFMA path (bf16).
+// ===========================================================================
+
+template <int D>
+struct MState {
+  f32x4 O[D / 32][2];
+  float m, l;
+};
 
 // 4x4 transpose of 32-bit words inside each DPP quad (lanes 4k..4k+3): on
 // return x[k] of lane r holds what x[r] of lane k held. Two butterfly stages
@@ -270,164 +142,627 @@ __device__ __forceinline__ void quad_transpose(uint32_t (&x)[4], int lane) {
   }
 }
 
+// Q^T operand of S^T = K.Q^T: lane holds Q[q0 + lane%16][32r + 8*(lane/16) .. +8],
+// zero for rows past the group.
 template <int D>
-__global__ void __launch_bounds__(256) attn_mfma_kernel(AttnArgs a) {
-  static_assert(D % 32 == 0 && D <= 256, "unsupported head_dim");
-  constexpr int NR = D / 32;  // 16-byte K loads and V loads per lane per block
-  const int lane = threadIdx.x & 63;
-  Unit u;
-  if (!decode_unit(a, lane, u)) return;
+__device__ __forceinline__ void mfma_load_q(const KArgs &a, int lane, int b, int h, int qc,
+                                            bf16x8 (&qop)[D / 32]) {
+  const int m16 = lane & 15, g4 = lane >> 4;
+  const int q0 = qc * kQChunkMfma;
+  const int nq = min(kQChunkMfma, a.G - q0);
+  const uint16_t *qp = reinterpret_cast<const uint16_t *>(a.q) +
+                       (int64_t)(b * a.Hq + h * a.G + q0 + min(m16, nq - 1)) * D;
+#pragma unroll
+  for (int r = 0; r < D / 32; r++) {
+    u32x4 w = *reinterpret_cast<const u32x4 *>(qp + 32 * r + 8 * g4);
+    if (m16 >= nq) w = u32x4{0, 0, 0, 0};
+    qop[r] = __builtin_bit_cast(bf16x8, w);
+  }
+}
+
+// One 16-token block: scores, online softmax update, O += P.V.
+template <int D>
+__device__ __forceinline__ void mfma_block(const u32x4 (&kq)[D / 32], const u32x4 (&vq)[D / 32],
+                                           int tb, int ctx, bool bad, const bf16x8 (&qop)[D / 32],
+                                           float sl2, int lane, MState<D> &st) {
+  constexpr int NR = D / 32;
+  const int g4 = lane >> 4, rq = lane & 3;
+  f32x4 S = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+    S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kq[r]), qop[r], S, 0, 0, 0);
+  // Lane holds S[token tb + 4*g4 + i][q = lane%16].
+  float x[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) x[i] = (!bad && tb + 4 * g4 + i < ctx) ? S[i] * sl2 : -INFINITY;
+  float mloc = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+  mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+  mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+  const bool need = mloc > st.m + kRescaleSlack;
+  if (__ballot(need)) {
+    const float mn = need ? mloc : st.m;
+    const float al = fast_exp2(st.m - mn);
+    st.l *= al;
+#pragma unroll
+    for (int s = 0; s < NR; s++) {
+      st.O[s][0] *= al;
+      st.O[s][1] *= al;
+    }
+    st.m = mn;
+  }
+  float p[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) p[i] = fast_exp2(x[i] - st.m);
+  st.l += (p[0] + p[1]) + (p[2] + p[3]);
+  // P^T operand: tokens 4*g4 .. +4 of query lane%16, bf16.
+  const uint32_t p01 = pack_bf16x2(p[0], p[1]), p23 = pack_bf16x2(p[2], p[3]);
+  const i16x4 pb = __builtin_bit_cast(i16x4, (uint64_t)p01 | ((uint64_t)p23 << 32));
+  // V rows past the context (or of a rejected block) are zeroed: stale slots
+  // may hold any bit pattern, and 0 * NaN would poison the sum.
+  const bool vvalid = !bad && tb + 4 * g4 + rq < ctx;
+#pragma unroll
+  for (int s = 0; s < NR; s++) {
+    uint32_t w[4] = {vq[s][0], vq[s][1], vq[s][2], vq[s][3]};
+    if (!vvalid) w[0] = w[1] = w[2] = w[3] = 0u;
+    quad_transpose(w, lane);
+    // w[k] = (V[4*g4+k][32s + 2*(lane%16)], V[4*g4+k][32s + 2*(lane%16) + 1])
+    const uint32_t e01 = (w[0] & 0xffffu) | (w[1] << 16), e23 = (w[2] & 0xffffu) | (w[3] << 16);
+    const uint32_t o01 = (w[0] >> 16) | (w[1] & 0xffff0000u), o23 = (w[2] >> 16) | (w[3] & 0xffff0000u);
+    const i16x4 ve = __builtin_bit_cast(i16x4, (uint64_t)e01 | ((uint64_t)e23 << 32));
+    const i16x4 vo = __builtin_bit_cast(i16x4, (uint64_t)o01 | ((uint64_t)o23 << 32));
+    st.O[s][0] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ve, pb, st.O[s][0], 0, 0, 0);
+    st.O[s][1] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vo, pb, st.O[s][1], 0, 0, 0);
+  }
+}
+
+// Blocks [sg.j0, sg.j1) (at most 64) of one segment, loads kRing deep.
+template <int D>
+__device__ __forceinline__ void mfma_run(const KArgs &a, const Seg &sg, int lane,
+                                         const bf16x8 (&qop)[D / 32], MState<D> &st) {
+  constexpr int NR = D / 32;
   const int m16 = lane & 15, g4 = lane >> 4, a4 = m16 >> 2, rq = m16 & 3;
-  const int q0 = u.qc * 16;
-  const int nq = min(16, a.G - q0);
-
-  // Q^T operand of S^T = K.Q^T: lane holds Q[q0+m16][32r + 8*g4 .. +8].
-  bf16x8 qop[NR];
-  {
-    const uint16_t *qp = reinterpret_cast<const uint16_t *>(a.q) +
-                         (int64_t)(u.b * a.Hq + u.h * a.G + q0 + min(m16, nq - 1)) * D;
+  const int n = sg.j1 - sg.j0;
+  // Block ids of the stretch, one per lane; rejected ids read block 0 and
+  // are masked.
+  int32_t idv = lane < n ? sg.table[sg.j0 + lane] : 0;
+  const bool badv = lane < n && (idv < 0 || idv >= a.nblocks);
+  if (badv) {
+    record_error(a.d_err, MKV_DEVERR_BLOCK);
+    idv = 0;
+  }
+  const uint64_t badmask = __ballot(badv);
+  const int64_t head_off = (int64_t)sg.h * D * 2;
+  const int64_t k_lane = (int64_t)m16 * a.row_bytes + head_off + 16 * g4;          // + 64 r
+  const int64_t v_lane = (int64_t)(4 * g4 + rq) * a.row_bytes + head_off + 16 * a4;  // + 64 s
+  const int last_blk = (sg.ctx - 1) / kPageSize, new_row = (sg.ctx - 1) % kPageSize;
+  u32x4 kb[kRing][NR], vb[kRing][NR];
+  auto issue = [&](u32x4 (&kd)[NR], u32x4 (&vd)[NR], int jj) {
+    const int32_t blk = __builtin_amdgcn_readlane(idv, jj - sg.j0);
+    const uint8_t *kp = a.k_plane + (int64_t)blk * a.block_bytes + k_lane;
+    const uint8_t *vp = a.v_plane + (int64_t)blk * a.block_bytes + v_lane;
+    if (sg.nk && jj == last_blk) {  // the step's new row comes from the input
+      if (m16 == new_row) kp = sg.nk + 16 * g4;
+      if (4 * g4 + rq == new_row) vp = sg.nv + 16 * a4;
+    }
 #pragma unroll
-    for (int r = 0; r < NR; r++) {
-      u32x4 w = *reinterpret_cast<const u32x4 *>(qp + 32 * r + 8 * g4);
-      if (m16 >= nq) w = u32x4{0, 0, 0, 0};
-      qop[r] = __builtin_bit_cast(bf16x8, w);
+    for (int r = 0; r < NR; r++) kd[r] = *reinterpret_cast<const u32x4 *>(kp + 64 * r);
+#pragma unroll
+    for (int s = 0; s < NR; s++) vd[s] = *reinterpret_cast<const u32x4 *>(vp + 64 * s);
+  };
+#pragma unroll
+  for (int s = 0; s < kRing - 1; s++)
+    if (sg.j0 + s < sg.j1) issue(kb[s], vb[s], sg.j0 + s);
+  for (int j = sg.j0; j < sg.j1; j += kRing) {
+#pragma unroll
+    for (int s = 0; s < kRing; s++) {
+      const int jj = j + s;
+      if (jj < sg.j1) {
+        if (jj + kRing - 1 < sg.j1) issue(kb[(s + kRing - 1) % kRing], vb[(s + kRing - 1) % kRing], jj + kRing - 1);
+        const bool bad = (badmask >> (jj - sg.j0)) & 1;
+        mfma_block<D>(kb[s], vb[s], jj * kPageSize, sg.ctx, bad, qop, a.sl2, lane, st);
+      }
     }
   }
-  f32x4 O[NR][2];
-#pragma unroll
-  for (int s = 0; s < NR; s++) O[s][0] = O[s][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY, l = 0.0f;
+}
 
-  const int64_t head_off = (int64_t)u.h * D * 2;
-  const int64_t k_lane = (int64_t)m16 * a.row_bytes + head_off + 16 * g4;          // + 64*r
-  const int64_t v_lane = (int64_t)(4 * g4 + rq) * a.row_bytes + head_off + 16 * a4;  // + 64*s
-  const int j0 = u.t_begin / kPageSize, j1 = (u.t_end + kPageSize - 1) / kPageSize;
-
-  for (int j = j0; j < j1; j++) {
-    int32_t blk = a.ids[u.tab0 + j];
-    const bool bad = blk < 0 || blk >= a.nblocks;
-    if (bad) {
-      if (lane == 0) record_error(a.d_err, MKV_DEVERR_BLOCK);
-      continue;
-    }
-    const uint8_t *kb = a.k_plane + (int64_t)blk * a.block_bytes + k_lane;
-    const uint8_t *vb = a.v_plane + (int64_t)blk * a.block_bytes + v_lane;
-    u32x4 kq[NR], vq[NR];
+template <int D>
+__device__ __forceinline__ void mfma_segment(const KArgs &a, const Seg &sg, int lane, MState<D> &st) {
+  bf16x8 qop[D / 32];
+  mfma_load_q<D>(a, lane, sg.b, sg.h, sg.qc, qop);
 #pragma unroll
-    for (int r = 0; r < NR; r++) kq[r] = *reinterpret_cast<const u32x4 *>(kb + 64 * r);
-#pragma unroll
-    for (int s = 0; s < NR; s++) vq[s] = *reinterpret_cast<const u32x4 *>(vb + 64 * s);
-
-    // Scores: lane holds S[token 4*g4+i][q = m16].
-    f32x4 S = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int r = 0; r < NR; r++)
-      S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kq[r]), qop[r], S, 0, 0, 0);
-    const int tb = j * kPageSize;
-    float x[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) x[i] = (tb + 4 * g4 + i < u.t_end) ? S[i] * a.sl2 : -INFINITY;
-    float mloc = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-    const float mn = fmaxf(m, mloc);
-    const float al = fast_exp2(m - mn);
-    float p[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) p[i] = fast_exp2(x[i] - mn);
-    l = l * al + ((p[0] + p[1]) + (p[2] + p[3]));
-    m = mn;
-#pragma unroll
-    for (int s = 0; s < NR; s++) {
-      O[s][0] *= al;
-      O[s][1] *= al;
-    }
-    // P^T operand: tokens 4*g4 .. +4 for query m16, bf16.
-    const uint32_t p01 = pack_bf16x2(p[0], p[1]), p23 = pack_bf16x2(p[2], p[3]);
-    const i16x4 pb = __builtin_bit_cast(i16x4, (uint64_t)p01 | ((uint64_t)p23 << 32));
-    // V rows past the context are zeroed (stale slots may hold any bits).
-    const bool vvalid = tb + 4 * g4 + rq < u.t_end;
-#pragma unroll
-    for (int s = 0; s < NR; s++) {
-      uint32_t w[4] = {vq[s][0], vq[s][1], vq[s][2], vq[s][3]};
-      if (!vvalid) w[0] = w[1] = w[2] = w[3] = 0u;
-      quad_transpose(w, lane);
-      // w[k] = (V[4*g4+k][32s + 2*m16], V[4*g4+k][32s + 2*m16 + 1])
-      const uint32_t e01 = (w[0] & 0xffffu) | (w[1] << 16), e23 = (w[2] & 0xffffu) | (w[3] << 16);
-      const uint32_t o01 = (w[0] >> 16) | (w[1] & 0xffff0000u), o23 = (w[2] >> 16) | (w[3] & 0xffff0000u);
-      const i16x4 ve = __builtin_bit_cast(i16x4, (uint64_t)e01 | ((uint64_t)e23 << 32));
-      const i16x4 vo = __builtin_bit_cast(i16x4, (uint64_t)o01 | ((uint64_t)o23 << 32));
-      O[s][0] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ve, pb, O[s][0], 0, 0, 0);
-      O[s][1] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vo, pb, O[s][1], 0, 0, 0);
-    }
+  for (int s = 0; s < D / 32; s++) st.O[s][0] = st.O[s][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  st.m = -INFINITY;
+  st.l = 0.0f;
+  for (int c = sg.j0; c < sg.j1; c += 64) {
+    Seg part = sg;
+    part.j0 = c;
+    part.j1 = min(sg.j1, c + 64);
+    mfma_run<D>(a, part, lane, qop, st);
   }
-  l += __shfl_xor(l, 16);
-  l += __shfl_xor(l, 32);
-  if (m16 >= nq || m == -INFINITY) return;
-  // Lane holds O[q0+m16][32s + 8*g4 + 2i + hh] = O[s][hh][i].
-  const int hq = u.h * a.G + q0 + m16;
-  if (u.nsp == 1) {
-    const float f = final_scale(m, l, a.zero_sink);
-    uint16_t *op = reinterpret_cast<uint16_t *>(a.o) + (int64_t)(u.b * a.Hq + hq) * D + 8 * g4;
+  st.l += __shfl_xor(st.l, 16);
+  st.l += __shfl_xor(st.l, 32);
+}
+
+// Lane holds O[q0 + lane%16][32s + 8*(lane/16) + c], c = 2i + hh, in O[s][hh][i].
+template <int D>
+__device__ __forceinline__ void mfma_store(const KArgs &a, const Seg &sg, int lane, const MState<D> &st,
+                                           bool final, int64_t prow_base, int64_t prow_stride) {
+  const int m16 = lane & 15, g4 = lane >> 4;
+  const int q0 = sg.qc * kQChunkMfma;
+  if (m16 >= min(kQChunkMfma, a.G - q0)) return;
+  const int hq = sg.h * a.G + q0 + m16;
+  if (final) {
+    const float f = final_scale(st.m, st.l, a.zero_sink);
+    uint16_t *op = reinterpret_cast<uint16_t *>(a.o) + (int64_t)(sg.b * a.Hq + hq) * D + 8 * g4;
 #pragma unroll
-    for (int s = 0; s < NR; s++) {
+    for (int s = 0; s < D / 32; s++) {
       u32x4 w;
 #pragma unroll
-      for (int i = 0; i < 4; i++) w[i] = pack_bf16x2(O[s][0][i] * f, O[s][1][i] * f);
+      for (int i = 0; i < 4; i++) w[i] = pack_bf16x2(st.O[s][0][i] * f, st.O[s][1][i] * f);
       *reinterpret_cast<u32x4 *>(op + 32 * s) = w;
     }
   } else {
-    const int64_t idx = ((int64_t)u.b * a.Hq + hq) * a.S + u.split;
-    float *wo = a.ws_o + idx * D + 8 * g4;
+    const int64_t prow = prow_base + (int64_t)hq * prow_stride;
+    float *wo = a.ws_o + prow * D + 8 * g4;
 #pragma unroll
-    for (int s = 0; s < NR; s++) {
-      f32x4 lo4 = {O[s][0][0], O[s][1][0], O[s][0][1], O[s][1][1]};
-      f32x4 hi4 = {O[s][0][2], O[s][1][2], O[s][0][3], O[s][1][3]};
-      *reinterpret_cast<f32x4 *>(wo + 32 * s) = lo4;
-      *reinterpret_cast<f32x4 *>(wo + 32 * s + 4) = hi4;
+    for (int s = 0; s < D / 32; s++) {
+      *reinterpret_cast<f32x4 *>(wo + 32 * s) = f32x4{st.O[s][0][0], st.O[s][1][0], st.O[s][0][1], st.O[s][1][1]};
+      *reinterpret_cast<f32x4 *>(wo + 32 * s + 4) = f32x4{st.O[s][0][2], st.O[s][1][2], st.O[s][0][3], st.O[s][1][3]};
     }
-    if (g4 == 0) {
-      a.ws_ml[2 * idx] = m;
-      a.ws_ml[2 * idx + 1] = l;
+    if (g4 == 0) *reinterpret_cast<float2 *>(a.ws_ml + 2 * prow) = make_float2(st.m, st.l);
+  }
+}
+
+// ===========================================================================
+// VALU path (any dtype).
+// ===========================================================================
+
+template <int D, bool BF16>
+struct VTraits {
+  static constexpr int ES = BF16 ? 2 : 4;
+  static constexpr int VEC = 16 / ES;  // elements per 16 B chunk
+  static constexpr int LPT = D / VEC;  // lanes per token row
+  static constexpr int TPI = 64 / LPT; // tokens per wave iteration
+  static_assert(LPT >= 1 && LPT <= 64 && (64 % LPT) == 0, "unsupported head_dim");
+};
+
+template <int D, bool BF16>
+struct VState {
+  float m[kQChunkValu], l[kQChunkValu], acc[kQChunkValu][VTraits<D, BF16>::VEC];
+};
+
+template <bool BF16, int VEC>
+__device__ __forceinline__ void load_chunk(const uint8_t *p, float (&f)[VEC]) {
+  const u32x4 w = *reinterpret_cast<const u32x4 *>(p);
+  if constexpr (BF16) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      f[2 * e] = bf16_lo(w[e]);
+      f[2 * e + 1] = bf16_hi(w[e]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; e++) f[e] = __uint_as_float(w[e]);
+  }
+}
+
+template <int D, bool BF16>
+__device__ __forceinline__ void valu_segment(const KArgs &a, const Seg &sg, int lane, VState<D, BF16> &st) {
+  using T = VTraits<D, BF16>;
+  constexpr int ES = T::ES, VEC = T::VEC, LPT = T::LPT, TPI = T::TPI, QC = kQChunkValu;
+  const int lt = lane / LPT, ld = lane % LPT;
+  const int q0 = sg.qc * QC;
+  const int nq = min(QC, a.G - q0);
+  const int hq0 = sg.h * a.G + q0;
+  float qv[QC][VEC];
+#pragma unroll
+  for (int g = 0; g < QC; g++) {
+    if (g < nq) {
+      load_chunk<BF16, VEC>(reinterpret_cast<const uint8_t *>(a.q) +
+                                ((int64_t)(sg.b * a.Hq + hq0 + g) * D + ld * VEC) * ES,
+                            qv[g]);
+#pragma unroll
+      for (int e = 0; e < VEC; e++) qv[g][e] *= a.sl2;
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; e++) qv[g][e] = 0.0f;
+    }
+    st.m[g] = -INFINITY;
+    st.l[g] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < VEC; e++) st.acc[g][e] = 0.0f;
+  }
+  const int64_t head_off = (int64_t)sg.h * D * ES + ld * 16;
+  const int t_begin = sg.j0 * kPageSize, t_end = min(sg.ctx, sg.j1 * kPageSize);
+  const int n_iter = (t_end - t_begin + TPI - 1) / TPI;
+  for (int it = 0; it < n_iter; it++) {
+    const int t = t_begin + it * TPI + lt;
+    bool valid = t < t_end;
+    float kf[VEC], vf[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; e++) kf[e] = vf[e] = 0.0f;
+    if (valid) {
+      if (sg.nk && t == sg.ctx - 1) {
+        load_chunk<BF16, VEC>(sg.nk + ld * 16, kf);
+        load_chunk<BF16, VEC>(sg.nv + ld * 16, vf);
+      } else {
+        const int32_t blk = sg.table[t / kPageSize];
+        if (blk < 0 || blk >= a.nblocks) {
+          record_error(a.d_err, MKV_DEVERR_BLOCK);
+          valid = false;
+        } else {
+          const int64_t off = (int64_t)blk * a.block_bytes + (t % kPageSize) * a.row_bytes + head_off;
+          load_chunk<BF16, VEC>(a.k_plane + off, kf);
+          load_chunk<BF16, VEC>(a.v_plane + off, vf);
+        }
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < QC; g++) {
+      if (g >= nq) break;
+      float s = 0.0f;
+#pragma unroll
+      for (int e = 0; e < VEC; e++) s = fmaf(qv[g][e], kf[e], s);
+#pragma unroll
+      for (int o = LPT / 2; o >= 1; o >>= 1) s += __shfl_xor(s, o);
+      if (valid) {
+        const float mn = fmaxf(st.m[g], s);
+        const float al = fast_exp2(st.m[g] - mn);
+        const float p = fast_exp2(s - mn);
+        st.l[g] = st.l[g] * al + p;
+#pragma unroll
+        for (int e = 0; e < VEC; e++) st.acc[g][e] = fmaf(p, vf[e], st.acc[g][e] * al);
+        st.m[g] = mn;
+      }
+    }
+  }
+  // Merge the TPI token slots of the wave (lanes sharing ld).
+#pragma unroll
+  for (int o = LPT; o < 64; o <<= 1) {
+#pragma unroll
+    for (int g = 0; g < QC; g++) {
+      if (g >= nq) break;
+      const float mo = __shfl_xor(st.m[g], o);
+      const float lo = __shfl_xor(st.l[g], o);
+      const float M = fmaxf(st.m[g], mo);
+      const float fa = st.m[g] == -INFINITY ? 0.0f : fast_exp2(st.m[g] - M);
+      const float fb = mo == -INFINITY ? 0.0f : fast_exp2(mo - M);
+      st.l[g] = st.l[g] * fa + lo * fb;
+#pragma unroll
+      for (int e = 0; e < VEC; e++) st.acc[g][e] = st.acc[g][e] * fa + __shfl_xor(st.acc[g][e], o) * fb;
+      st.m[g] = M;
     }
   }
 }
 
-// ---------------------------------------------------------------------------
-// Split-K merge: one wave per (sequence, query head) with more than one split.
-// ---------------------------------------------------------------------------
-template <bool BF16>
-__global__ void __launch_bounds__(256) merge_kernel(AttnArgs a, int D) {
+template <int D, bool BF16>
+__device__ __forceinline__ void valu_store(const KArgs &a, const Seg &sg, int lane, const VState<D, BF16> &st,
+                                           bool final, int64_t prow_base, int64_t prow_stride) {
+  using T = VTraits<D, BF16>;
+  constexpr int ES = T::ES, VEC = T::VEC, LPT = T::LPT, QC = kQChunkValu;
+  if (lane >= LPT) return;
+  const int ld = lane;
+  const int q0 = sg.qc * QC;
+  const int nq = min(QC, a.G - q0);
+#pragma unroll
+  for (int g = 0; g < QC; g++) {
+    if (g >= nq) break;
+    const int hq = sg.h * a.G + q0 + g;
+    if (final) {
+      const float f = final_scale(st.m[g], st.l[g], a.zero_sink);
+      uint8_t *op = reinterpret_cast<uint8_t *>(a.o) + ((int64_t)(sg.b * a.Hq + hq) * D + ld * VEC) * ES;
+      u32x4 w;
+      if constexpr (BF16) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) w[e] = pack_bf16x2(st.acc[g][2 * e] * f, st.acc[g][2 * e + 1] * f);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; e++) w[e] = __float_as_uint(st.acc[g][e] * f);
+      }
+      *reinterpret_cast<u32x4 *>(op) = w;
+    } else {
+      const int64_t prow = prow_base + (int64_t)hq * prow_stride;
+      float *wo = a.ws_o + prow * D + ld * VEC;
+#pragma unroll
+      for (int e = 0; e < VEC; e += 4)
+        *reinterpret_cast<f32x4 *>(wo + e) = f32x4{st.acc[g][e], st.acc[g][e + 1], st.acc[g][e + 2], st.acc[g][e + 3]};
+      if (ld == 0) *reinterpret_cast<float2 *>(a.ws_ml + 2 * prow) = make_float2(st.m[g], st.l[g]);
+    }
+  }
+}
+
+// Processes one segment with the selected path and stores its result.
+template <int D, bool BF16, bool MFMA>
+__device__ __forceinline__ void run_segment(const KArgs &a, const Seg &sg, int lane, bool final,
+                                            int64_t prow_base, int64_t prow_stride) {
+  if constexpr (MFMA) {
+    MState<D> st;
+    mfma_segment<D>(a, sg, lane, st);
+    mfma_store<D>(a, sg, lane, st, final, prow_base, prow_stride);
+  } else {
+    VState<D, BF16> st;
+    valu_segment<D, BF16>(a, sg, lane, st);
+    valu_store<D, BF16>(a, sg, lane, st, final, prow_base, prow_stride);
+  }
+}
+
+// Log-sum-exp merge of n partial rows ws[base + s*stride], s < n, into o.
+// Lane s holds partial s's (m, l); lane d holds dims d + 64k of every
+// partial. All loads of up to 16 partials issue before the first use, so a
+// merge costs about one memory round trip; weights exp2(m_s - M) are
+// broadcast with readlane.
+template <int D, bool BF16>
+__device__ __forceinline__ void merge_rows(const KArgs &a, int lane, int64_t base, int64_t stride, int n,
+                                           int64_t out_row) {
+  constexpr int DPL = (D + 63) / 64;
+  constexpr int SB = 16;
+  float M = -INFINITY;
+  for (int s0 = 0; s0 < n; s0 += 64)
+    if (s0 + lane < n) M = fmaxf(M, a.ws_ml[2 * (base + (s0 + lane) * stride)]);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+  float L = 0.0f, acc[DPL];
+#pragma unroll
+  for (int k = 0; k < DPL; k++) acc[k] = 0.0f;
+  for (int s0 = 0; s0 < n; s0 += 64) {
+    float w = 0.0f;
+    if (s0 + lane < n) {
+      const float2 ml = *reinterpret_cast<const float2 *>(a.ws_ml + 2 * (base + (s0 + lane) * stride));
+      w = fast_exp2(ml.x - M);
+      L += ml.y * w;
+    }
+    const int cnt = min(64, n - s0);
+    for (int s1 = 0; s1 < cnt; s1 += SB) {
+      float ov[SB][DPL];
+#pragma unroll
+      for (int i = 0; i < SB; i++)
+#pragma unroll
+        for (int k = 0; k < DPL; k++) {
+          const int d = lane + 64 * k;
+          ov[i][k] = (s1 + i < cnt && d < D) ? a.ws_o[(base + (int64_t)(s0 + s1 + i) * stride) * D + d] : 0.0f;
+        }
+#pragma unroll
+      for (int i = 0; i < SB; i++) {
+        const float wi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), (s1 + i) & 63));
+#pragma unroll
+        for (int k = 0; k < DPL; k++) acc[k] = fmaf(wi, ov[i][k], acc[k]);
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o);
+  const float f = final_scale(M, L, a.zero_sink);
+#pragma unroll
+  for (int k = 0; k < DPL; k++) {
+    const int d = lane + 64 * k;
+    if (d >= D) break;
+    if constexpr (BF16)
+      reinterpret_cast<uint16_t *>(a.o)[out_row * D + d] = (uint16_t)f32_to_bf16_bits(acc[k] * f);
+    else
+      reinterpret_cast<float *>(a.o)[out_row * D + d] = acc[k] * f;
+  }
+}
+
+// ===========================================================================
+// Split-grid decomposition.
+// ===========================================================================
+
+struct SplitArgs {
+  const int32_t *ctx_lens;
+  int64_t total_units;
+  int32_t B, S, split_tokens, max_ctx;
+};
+
+template <int D, bool BF16, bool MFMA>
+__global__ void __launch_bounds__(256) attn_split_kernel(KArgs a, SplitArgs sp) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int64_t id = (int64_t)blockIdx.x * 4 + wave;
+  if (id >= sp.total_units) return;
+  Seg sg;
+  sg.qc = (int)(id % a.nqc);
+  id /= a.nqc;
+  sg.h = (int)(id % a.Hkv);
+  id /= a.Hkv;
+  const int split = (int)(id % sp.S);
+  sg.b = (int)(id / sp.S);
+  const bool first = split == 0 && sg.h == 0 && sg.qc == 0 && lane == 0;
+  sg.ctx = sp.ctx_lens[sg.b];
+  if (sg.ctx < 1 || sg.ctx > sp.max_ctx) {
+    if (first) record_error(a.d_err, MKV_DEVERR_CTX);
+    return;
+  }
+  const int t_begin = split * sp.split_tokens;
+  if (t_begin >= sg.ctx) return;
+  const int nsp = (sg.ctx + sp.split_tokens - 1) / sp.split_tokens;
+  const int nb = (sg.ctx + kPageSize - 1) / kPageSize;
+  const int tab0 = a.indptr[sg.b];
+  if (tab0 < 0 || a.indptr[sg.b + 1] - tab0 < nb) {
+    if (first) record_error(a.d_err, MKV_DEVERR_TABLE);
+    return;
+  }
+  sg.table = a.ids + tab0;
+  sg.j0 = t_begin / kPageSize;
+  sg.j1 = min(nb, (t_begin + sp.split_tokens) / kPageSize);
+  sg.nk = sg.nv = nullptr;
+  run_segment<D, BF16, MFMA>(a, sg, lane, nsp == 1, ((int64_t)sg.b * a.Hq) * sp.S + split, sp.S);
+}
+
+template <int D, bool BF16>
+__global__ void __launch_bounds__(256) merge_split_kernel(KArgs a, SplitArgs sp) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t row = (int64_t)blockIdx.x * 4 + wave;
-  if (row >= (int64_t)a.B * a.Hq) return;
+  if (row >= (int64_t)sp.B * a.Hq) return;
   const int b = (int)(row / a.Hq);
-  const int ctx = a.ctx_lens[b];
-  if (ctx < 1 || ctx > a.max_ctx) return;
-  const int nsp = (ctx + a.split_tokens - 1) / a.split_tokens;
+  const int ctx = sp.ctx_lens[b];
+  if (ctx < 1 || ctx > sp.max_ctx) return;
+  const int nsp = (ctx + sp.split_tokens - 1) / sp.split_tokens;
   if (nsp <= 1) return;
-  const float *ml = a.ws_ml + 2 * row * a.S;
-  float M = -INFINITY;
-  for (int s = 0; s < nsp; s++) M = fmaxf(M, ml[2 * s]);
-  float L = 0.0f;
-  for (int s = 0; s < nsp; s++) L += ml[2 * s + 1] * fast_exp2(ml[2 * s] - M);
-  const float f = final_scale(M, L, a.zero_sink);
-  const float *wo = a.ws_o + row * a.S * D;
-  for (int d = lane; d < D; d += 64) {
-    float acc = 0.0f;
-    for (int s = 0; s < nsp; s++) acc += wo[(int64_t)s * D + d] * fast_exp2(ml[2 * s] - M);
-    acc *= f;
-    if constexpr (BF16)
-      reinterpret_cast<uint16_t *>(a.o)[row * D + d] = (uint16_t)f32_to_bf16_bits(acc);
-    else
-      reinterpret_cast<float *>(a.o)[row * D + d] = acc;
+  merge_rows<D, BF16>(a, lane, row * sp.S, 1, nsp, row);
+}
+
+// ===========================================================================
+// Planned decomposition.
+// ===========================================================================
+
+struct PlanDev {
+  const int32_t *ctx;         // [B] tokens attended
+  const int32_t *seq_blk0;    // [B+1] first flattened block of each sequence
+  const int32_t *piece_seq;   // [P] sequence holding each piece's first block
+  const int32_t *merge_seqs;  // [n_merge] sequences cut by a piece boundary
+  int32_t B, P, BP, total_blocks, n_merge;
+};
+
+// One workgroup per (piece, group of <= 4 (KV head, query chunk) waves).
+template <int D, bool BF16, bool MFMA>
+__global__ void __launch_bounds__(256) attn_planned_kernel(KArgs a, PlanDev pd) {
+  constexpr int ES = BF16 ? 2 : 4;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hc = (int)blockIdx.y * (int)(blockDim.x >> 6) + wave;
+  if (hc >= a.Hkv * a.nqc) return;
+  Seg sg;
+  sg.h = hc / a.nqc;
+  sg.qc = hc % a.nqc;
+  const int p = blockIdx.x;
+  int f = p * pd.BP;
+  const int f_end = min(f + pd.BP, pd.total_blocks);
+  int b = pd.piece_seq[p];
+  for (; f < f_end; ++b) {
+    const int sb = pd.seq_blk0[b], nb = pd.seq_blk0[b + 1] - sb;
+    sg.b = b;
+    sg.ctx = pd.ctx[b];
+    sg.j0 = f - sb;
+    sg.j1 = min(nb, f_end - sb);
+    f = sb + sg.j1;
+    const int tab0 = a.indptr[b];
+    if (tab0 < 0 || a.indptr[b + 1] - tab0 < nb) {
+      if (lane == 0) record_error(a.d_err, MKV_DEVERR_TABLE);
+      continue;
+    }
+    sg.table = a.ids + tab0;
+    sg.nk = sg.nv = nullptr;
+    if (a.new_k && sg.j1 == nb) {
+      // This piece holds the sequence's last block: the step's new row.
+      const int32_t blk = sg.table[nb - 1];
+      if (blk < 0 || blk >= a.nblocks) {
+        if (lane == 0) record_error(a.d_err, MKV_DEVERR_BLOCK);
+      } else {
+        const int64_t src = ((int64_t)b * a.Hkv + sg.h) * D * ES;
+        sg.nk = a.new_k + src;
+        sg.nv = a.new_v + src;
+        if (sg.qc == 0) store_new_row<D, ES>(a, lane, b, sg.h, blk, (sg.ctx - 1) % kPageSize);
+      }
+    }
+    const bool single = sb / pd.BP == (sb + nb - 1) / pd.BP;
+    run_segment<D, BF16, MFMA>(a, sg, lane, single, (int64_t)(p + b) * a.Hq, 1);
   }
 }
 
-// ---------------------------------------------------------------------------
+// One wave per (sequence cut by piece boundaries, query head).
+template <int D, bool BF16>
+__global__ void __launch_bounds__(256) merge_planned_kernel(KArgs a, PlanDev pd) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  if (row >= (int64_t)pd.n_merge * a.Hq) return;
+  const int b = pd.merge_seqs[row / a.Hq];
+  const int hq = (int)(row % a.Hq);
+  const int sb = pd.seq_blk0[b], nb = pd.seq_blk0[b + 1] - sb;
+  const int first = sb / pd.BP, last = (sb + nb - 1) / pd.BP;
+  merge_rows<D, BF16>(a, lane, (int64_t)(first + b) * a.Hq + hq, a.Hq, last - first + 1,
+                      (int64_t)b * a.Hq + hq);
+}
+
+// ===========================================================================
 // Host side.
-// ---------------------------------------------------------------------------
+// ===========================================================================
+
+static bool mfma_applies(const Geom &g) {
+  return g.dtype == MKV_DTYPE_BF16 && (g.D == 64 || g.D == 128 || g.D == 256);
+}
+
+static int check_common(const Pool *p, int32_t layer, uint32_t flags, float scale, bool &use_mfma) {
+  const Geom &g = p->g;
+  if (layer < 0 || layer >= g.L)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "layer %d out of range [0, %d)", layer, g.L);
+  if (g.D != 32 && g.D != 64 && g.D != 128 && g.D != 256)
+    return set_error(MKV_ERR_INVALID_ARGUMENT,
+                     "decode attention supports head_dim 32/64/128/256 (pool has %d)", g.D);
+  if (!(scale > 0.0f) || !std::isfinite(scale))
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "scale must be finite and > 0");
+  use_mfma = mfma_applies(g) && !(flags & MKV_ATTN_FORCE_VALU);
+  if ((flags & MKV_ATTN_FORCE_MFMA) && !use_mfma)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "MFMA kernel needs bf16 KV and head_dim 64/128/256");
+  return MKV_OK;
+}
+
+static KArgs make_kargs(Pool *p, int32_t layer, const void *d_q, void *d_o, const int32_t *indptr,
+                        const int32_t *ids, float scale, uint32_t flags, bool use_mfma) {
+  const Geom &g = p->g;
+  KArgs a;
+  a.k_plane_w = p->data + (int64_t)layer * 2 * g.plane_bytes;
+  a.v_plane_w = a.k_plane_w + g.plane_bytes;
+  a.k_plane = a.k_plane_w;
+  a.v_plane = a.v_plane_w;
+  a.q = d_q;
+  a.o = d_o;
+  a.new_k = a.new_v = nullptr;
+  a.indptr = indptr;
+  a.ids = ids;
+  a.ws_ml = a.ws_o = nullptr;
+  a.d_err = p->d_err;
+  a.nblocks = g.nblocks;
+  a.row_bytes = g.row_bytes;
+  a.block_bytes = g.block_bytes;
+  a.Hq = g.Hq;
+  a.Hkv = g.Hkv;
+  a.G = g.Hq / g.Hkv;
+  const int qcw = use_mfma ? kQChunkMfma : kQChunkValu;
+  a.nqc = (a.G + qcw - 1) / qcw;
+  a.sl2 = scale * kLog2e;
+  a.zero_sink = (flags & MKV_ATTN_ZERO_SINK) ? 1 : 0;
+  return a;
+}
+
+// Launches attention kernel `Kern<D, BF16, MFMA>` for the pool geometry.
+#define MKV_DISPATCH(KERNEL, GRID, BLOCK, STREAM, ...)                                             \
+  do {                                                                                             \
+    if (use_mfma) {                                                                                \
+      if (g.D == 64) hipLaunchKernelGGL((KERNEL<64, true, true>), GRID, BLOCK, 0, STREAM, __VA_ARGS__);   \
+      else if (g.D == 128) hipLaunchKernelGGL((KERNEL<128, true, true>), GRID, BLOCK, 0, STREAM, __VA_ARGS__); \
+      else hipLaunchKernelGGL((KERNEL<256, true, true>), GRID, BLOCK, 0, STREAM, __VA_ARGS__);         \
+    } else if (g.dtype == MKV_DTYPE_BF16) {                                                        \
+      if (g.D == 32) hipLaunchKernelGGL((KERNEL<32, true, false>), GRID, BLOCK, 0, STREAM, __VA_ARGS__);   \
+      else if (g.D == 64) hipLaunchKernelGGL((KERNEL<64, true, false>), GRID, BLOCK, 0, STREAM, __VA_ARGS__); \
+      else if (g.D == 128) hipLaunchKernelGGL((KERNEL<128, true, false>), GRID, BLOCK, 0, STREAM, __VA_ARGS__); \
+      else hipLaunchKernelGGL((KERNEL<256, true, false>), GRID, BLOCK, 0, STREAM, __VA_ARGS__);         \
+    } else {                                                                                       \
+      if (g.D == 32) hipLaunchKernelGGL((KERNEL<32, false, false>), GRID, BLOCK, 0, STREAM, __VA_ARGS__);  \
+      else if (g.D == 64) hipLaunchKernelGGL((KERNEL<64, false, false>), GRID, BLOCK, 0, STREAM, __VA_ARGS__); \
+      else if (g.D == 128) hipLaunchKernelGGL((KERNEL<128, false, false>), GRID, BLOCK, 0, STREAM, __VA_ARGS__); \
+      else hipLaunchKernelGGL((KERNEL<256, false, false>), GRID, BLOCK, 0, STREAM, __VA_ARGS__);        \
+    }                                                                                              \
+  } while (0)
+
+// Launches merge kernel `KERNEL<D, BF16>` for the pool geometry.
+#define MKV_DISPATCH_MERGE(KERNEL, GRID, BLOCK, STREAM, ...)                                 \
+  do {                                                                                       \
+    const bool bf = g.dtype == MKV_DTYPE_BF16;                                               \
+    switch (g.D) {                                                                           \
+      case 32: if (bf) hipLaunchKernelGGL((KERNEL<32, true>), GRID, BLOCK, 0, STREAM, __VA_ARGS__);  \
+               else hipLaunchKernelGGL((KERNEL<32, false>), GRID, BLOCK, 0, STREAM, __VA_ARGS__); break; \
+      case 64: if (bf) hipLaunchKernelGGL((KERNEL<64, true>), GRID, BLOCK, 0, STREAM, __VA_ARGS__);  \
+               else hipLaunchKernelGGL((KERNEL<64, false>), GRID, BLOCK, 0, STREAM, __VA_ARGS__); break; \
+      case 128: if (bf) hipLaunchKernelGGL((KERNEL<128, true>), GRID, BLOCK, 0, STREAM, __VA_ARGS__); \
+                else hipLaunchKernelGGL((KERNEL<128, false>), GRID, BLOCK, 0, STREAM, __VA_ARGS__); break; \
+      default: if (bf) hipLaunchKernelGGL((KERNEL<256, true>), GRID, BLOCK, 0, STREAM, __VA_ARGS__); \
+               else hipLaunchKernelGGL((KERNEL<256, false>), GRID, BLOCK, 0, STREAM, __VA_ARGS__); break; \
+    }                                                                                        \
+  } while (0)
+
+// ---- split grid -------------------------------------------------------------
 
 static int choose_split(const Geom &g, int B, int max_ctx) {
   // Enough units to give every SIMD of the 256 CUs several waves, with at
@@ -440,20 +775,48 @@ static int choose_split(const Geom &g, int B, int max_ctx) {
   return (int)std::min<int64_t>(tokens, std::max(kPageSize, (max_ctx + kPageSize - 1) / kPageSize * kPageSize));
 }
 
-static uint64_t ws_bytes_for(const Geom &g, int B, int S) {
+static uint64_t split_ws_bytes(const Geom &g, int B, int S) {
   if (S <= 1) return 0;
   const uint64_t rows = (uint64_t)B * g.Hq * S;
-  const uint64_t ml = (rows * 8 + 255) / 256 * 256;
-  return ml + rows * g.D * 4;
+  return (rows * 8 + 255) / 256 * 256 + rows * g.D * 4;
 }
 
-static bool mfma_applies(const Geom &g) {
-  return g.dtype == MKV_DTYPE_BF16 && (g.D == 64 || g.D == 128 || g.D == 256);
+// ---- plan ---------------------------------------------------------------------
+
+struct Plan {
+  Pool *pool = nullptr;
+  int device = 0;
+  int32_t B = 0, P = 0, BP = 0, total = 0, n_merge = 0;
+  int32_t *d_meta = nullptr;  // ctx[B] | seq_blk0[B+1] | piece_seq[P] | merge_seqs[n_merge]
+  size_t meta_cap = 0;        // ints
+  int32_t *h_meta = nullptr;  // pinned staging
+  size_t h_cap = 0;
+  hipEvent_t uploaded = nullptr;
+  bool pending = false;
+  void *d_ws = nullptr;
+  uint64_t ws_cap = 0;
+  uint64_t ws_ml_bytes = 0;   // offset of the o rows inside d_ws
+};
+
+static PlanDev plan_dev(const Plan *pl) {
+  PlanDev d;
+  d.ctx = pl->d_meta;
+  d.seq_blk0 = d.ctx + pl->B;
+  d.piece_seq = d.seq_blk0 + pl->B + 1;
+  d.merge_seqs = d.piece_seq + pl->P;
+  d.B = pl->B;
+  d.P = pl->P;
+  d.BP = pl->BP;
+  d.total_blocks = pl->total;
+  d.n_merge = pl->n_merge;
+  return d;
 }
 
 }  // namespace mkv
 
 using namespace mkv;
+
+// ---- C ABI: split grid ------------------------------------------------------------------
 
 extern "C" int mkv_decode_attention_workspace_size(const mkv_pool *pool, int32_t num_seqs,
                                                    int32_t max_ctx_len, int32_t split_tokens,
@@ -464,7 +827,7 @@ extern "C" int mkv_decode_attention_workspace_size(const mkv_pool *pool, int32_t
     return set_error(MKV_ERR_INVALID_ARGUMENT, "bad sizes");
   const int st = split_tokens ? split_tokens : choose_split(p->g, num_seqs, max_ctx_len);
   const int S = max_ctx_len > 0 ? (max_ctx_len + st - 1) / st : 1;
-  *out_bytes = ws_bytes_for(p->g, num_seqs, S);
+  *out_bytes = split_ws_bytes(p->g, num_seqs, S);
   return MKV_OK;
 }
 
@@ -477,8 +840,9 @@ extern "C" int mkv_decode_attention(mkv_pool *pool, int32_t layer, const void *d
   if (!pool) return set_error(MKV_ERR_INVALID_ARGUMENT, "pool is NULL");
   Pool *p = reinterpret_cast<Pool *>(pool);
   const Geom &g = p->g;
-  if (layer < 0 || layer >= g.L)
-    return set_error(MKV_ERR_INVALID_ARGUMENT, "layer %d out of range [0, %d)", layer, g.L);
+  bool use_mfma = false;
+  int rc = check_common(p, layer, flags, scale, use_mfma);
+  if (rc) return rc;
   if (num_seqs < 0 || max_ctx_len < 0)
     return set_error(MKV_ERR_INVALID_ARGUMENT, "num_seqs and max_ctx_len must be >= 0");
   if (num_seqs == 0) return MKV_OK;
@@ -487,21 +851,11 @@ extern "C" int mkv_decode_attention(mkv_pool *pool, int32_t layer, const void *d
     return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL device pointer");
   if (!aligned16(d_q) || !aligned16(d_o))
     return set_error(MKV_ERR_INVALID_ARGUMENT, "q and o must be 16-byte aligned");
-  if (g.D != 32 && g.D != 64 && g.D != 128 && g.D != 256)
-    return set_error(MKV_ERR_INVALID_ARGUMENT, "decode attention supports head_dim 32/64/128/256 (pool has %d)", g.D);
   if (split_tokens < 0 || split_tokens % kPageSize)
     return set_error(MKV_ERR_INVALID_ARGUMENT, "split_tokens must be a multiple of %d", kPageSize);
-  if (!(scale > 0.0f) || !std::isfinite(scale))
-    return set_error(MKV_ERR_INVALID_ARGUMENT, "scale must be finite and > 0");
-  const bool use_mfma = mfma_applies(g) && !(flags & MKV_ATTN_FORCE_VALU);
-  if ((flags & MKV_ATTN_FORCE_MFMA) && !use_mfma)
-    return set_error(MKV_ERR_INVALID_ARGUMENT, "MFMA kernel needs bf16 KV and head_dim 64/128/256");
-  const int G = g.Hq / g.Hkv;
-  const int qcw = use_mfma ? 16 : 8;
-  const int nqc = (G + qcw - 1) / qcw;
   const int st = split_tokens ? split_tokens : choose_split(g, num_seqs, max_ctx_len);
   const int S = (max_ctx_len + st - 1) / st;
-  const uint64_t need = ws_bytes_for(g, num_seqs, S);
+  const uint64_t need = split_ws_bytes(g, num_seqs, S);
   DeviceGuard guard(p->device);
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
   void *ws = d_workspace;
@@ -512,8 +866,7 @@ extern "C" int mkv_decode_attention(mkv_pool *pool, int32_t layer, const void *d
                          (unsigned long long)workspace_bytes, (unsigned long long)need);
     } else {
       if (p->ws_bytes < need) {
-        // Earlier launches may still read the old buffer.
-        MKV_CHECK_HIP(hipStreamSynchronize(hs));
+        MKV_CHECK_HIP(hipStreamSynchronize(hs));  // earlier launches may read the old buffer
         if (p->ws) MKV_CHECK_HIP(hipFree(p->ws));
         p->ws = nullptr;
         p->ws_bytes = 0;
@@ -523,67 +876,209 @@ extern "C" int mkv_decode_attention(mkv_pool *pool, int32_t layer, const void *d
       ws = p->ws;
     }
   }
-  AttnArgs a;
-  a.k_plane = p->data + (int64_t)layer * 2 * g.plane_bytes;
-  a.v_plane = a.k_plane + g.plane_bytes;
-  a.q = d_q;
-  a.o = d_o;
-  a.indptr = d_block_indptr;
-  a.ids = d_block_ids;
-  a.ctx_lens = d_ctx_lens;
+  KArgs a = make_kargs(p, layer, d_q, d_o, d_block_indptr, d_block_ids, scale, flags, use_mfma);
   const uint64_t rows = (uint64_t)num_seqs * g.Hq * S;
   a.ws_ml = reinterpret_cast<float *>(ws);
   a.ws_o = ws ? reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(ws) + (rows * 8 + 255) / 256 * 256)
               : nullptr;
-  a.d_err = p->d_err;
-  a.nblocks = g.nblocks;
-  a.row_bytes = g.row_bytes;
-  a.block_bytes = g.block_bytes;
-  a.B = num_seqs;
-  a.Hq = g.Hq;
-  a.Hkv = g.Hkv;
-  a.G = G;
-  a.nqc = nqc;
-  a.S = S;
-  a.split_tokens = st;
-  a.max_ctx = max_ctx_len;
-  a.total_units = (int64_t)num_seqs * S * g.Hkv * nqc;
-  a.sl2 = scale * kLog2e;
-  a.zero_sink = (flags & MKV_ATTN_ZERO_SINK) ? 1 : 0;
-  const int64_t wgs = (a.total_units + 3) / 4;
+  SplitArgs sp;
+  sp.ctx_lens = d_ctx_lens;
+  sp.B = num_seqs;
+  sp.S = S;
+  sp.split_tokens = st;
+  sp.max_ctx = max_ctx_len;
+  sp.total_units = (int64_t)num_seqs * S * g.Hkv * a.nqc;
+  const int64_t wgs = (sp.total_units + 3) / 4;
   if (wgs > INT32_MAX) return set_error(MKV_ERR_INVALID_ARGUMENT, "launch too large");
-  const dim3 grid((unsigned)wgs), block(256);
-  if (use_mfma) {
-    switch (g.D) {
-      case 64: hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, block, 0, hs, a); break;
-      case 128: hipLaunchKernelGGL(attn_mfma_kernel<128>, grid, block, 0, hs, a); break;
-      default: hipLaunchKernelGGL(attn_mfma_kernel<256>, grid, block, 0, hs, a); break;
-    }
-    MKV_CHECK_LAUNCH("attn_mfma_kernel");
-  } else if (g.dtype == MKV_DTYPE_BF16) {
-    switch (g.D) {
-      case 32: hipLaunchKernelGGL((attn_valu_kernel<32, true>), grid, block, 0, hs, a); break;
-      case 64: hipLaunchKernelGGL((attn_valu_kernel<64, true>), grid, block, 0, hs, a); break;
-      case 128: hipLaunchKernelGGL((attn_valu_kernel<128, true>), grid, block, 0, hs, a); break;
-      default: hipLaunchKernelGGL((attn_valu_kernel<256, true>), grid, block, 0, hs, a); break;
-    }
-    MKV_CHECK_LAUNCH("attn_valu_kernel");
-  } else {
-    switch (g.D) {
-      case 32: hipLaunchKernelGGL((attn_valu_kernel<32, false>), grid, block, 0, hs, a); break;
-      case 64: hipLaunchKernelGGL((attn_valu_kernel<64, false>), grid, block, 0, hs, a); break;
-      case 128: hipLaunchKernelGGL((attn_valu_kernel<128, false>), grid, block, 0, hs, a); break;
-      default: hipLaunchKernelGGL((attn_valu_kernel<256, false>), grid, block, 0, hs, a); break;
-    }
-    MKV_CHECK_LAUNCH("attn_valu_kernel");
-  }
+  MKV_DISPATCH(attn_split_kernel, dim3((unsigned)wgs), dim3(256), hs, a, sp);
+  MKV_CHECK_LAUNCH("attn_split_kernel");
   if (S > 1) {
     const int64_t mwgs = ((int64_t)num_seqs * g.Hq + 3) / 4;
-    if (g.dtype == MKV_DTYPE_BF16)
-      hipLaunchKernelGGL(merge_kernel<true>, dim3((unsigned)mwgs), dim3(256), 0, hs, a, g.D);
-    else
-      hipLaunchKernelGGL(merge_kernel<false>, dim3((unsigned)mwgs), dim3(256), 0, hs, a, g.D);
-    MKV_CHECK_LAUNCH("merge_kernel");
+    MKV_DISPATCH_MERGE(merge_split_kernel, dim3((unsigned)mwgs), dim3(256), hs, a, sp);
+    MKV_CHECK_LAUNCH("merge_split_kernel");
   }
   return MKV_OK;
+}
+
+// ---- C ABI: plan --------------------------------------------------------------------
+
+extern "C" int mkv_decode_plan_create(mkv_pool *pool, mkv_decode_plan **out_plan) {
+  if (!pool || !out_plan) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL argument");
+  Plan *pl = new (std::nothrow) Plan();
+  if (!pl) return set_error(MKV_ERR_OUT_OF_MEMORY, "host allocation failed");
+  pl->pool = reinterpret_cast<Pool *>(pool);
+  pl->device = pl->pool->device;
+  DeviceGuard guard(pl->device);
+  hipError_t e = hipEventCreateWithFlags(&pl->uploaded, hipEventDisableTiming);
+  if (e != hipSuccess) {
+    delete pl;
+    return hip_fail(e, "hipEventCreate");
+  }
+  *out_plan = reinterpret_cast<mkv_decode_plan *>(pl);
+  return MKV_OK;
+}
+
+extern "C" int mkv_decode_plan_destroy(mkv_decode_plan *plan) {
+  if (!plan) return MKV_OK;
+  Plan *pl = reinterpret_cast<Plan *>(plan);
+  DeviceGuard guard(pl->device);
+  (void)hipDeviceSynchronize();
+  if (pl->d_meta) (void)hipFree(pl->d_meta);
+  if (pl->h_meta) (void)hipHostFree(pl->h_meta);
+  if (pl->d_ws) (void)hipFree(pl->d_ws);
+  if (pl->uploaded) (void)hipEventDestroy(pl->uploaded);
+  delete pl;
+  return MKV_OK;
+}
+
+extern "C" int mkv_decode_plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens,
+                                     int32_t num_seqs, int32_t pieces, void *stream) {
+  if (!plan) return set_error(MKV_ERR_INVALID_ARGUMENT, "plan is NULL");
+  Plan *pl = reinterpret_cast<Plan *>(plan);
+  const Geom &g = pl->pool->g;
+  if (num_seqs < 1 || !h_ctx_lens) return set_error(MKV_ERR_INVALID_ARGUMENT, "need num_seqs >= 1 context lengths");
+  if (pieces < 0) return set_error(MKV_ERR_INVALID_ARGUMENT, "pieces must be >= 0");
+  int64_t total = 0;
+  int max_nb = 0;
+  for (int32_t b = 0; b < num_seqs; b++) {
+    if (h_ctx_lens[b] < 1) return set_error(MKV_ERR_INVALID_ARGUMENT, "ctx_len[%d] = %d < 1", b, h_ctx_lens[b]);
+    const int nb = (h_ctx_lens[b] + kPageSize - 1) / kPageSize;
+    total += nb;
+    max_nb = std::max(max_nb, nb);
+  }
+  if (total > INT32_MAX / 2) return set_error(MKV_ERR_INVALID_ARGUMENT, "batch too large");
+  // Workgroup slots: ~8 waves per CU on 256 CUs, one wave per (KV head,
+  // query chunk); a piece is one workgroup row of the grid.
+  const int G = g.Hq / g.Hkv;
+  const int nqc = (G + kQChunkMfma - 1) / kQChunkMfma;
+  int64_t P = pieces ? pieces : std::max<int64_t>(1, 2048 / std::max(1, g.Hkv * nqc));
+  int64_t BP = std::max<int64_t>(1, (total + P - 1) / P);
+  P = (total + BP - 1) / BP;
+  DeviceGuard guard(pl->pool->device);
+  hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  std::vector<int32_t> merge;
+  const size_t n_ints = (size_t)num_seqs + (num_seqs + 1) + P + num_seqs;
+  // Staging: wait for the previous upload to leave the pinned buffer.
+  if (pl->pending) {
+    MKV_CHECK_HIP(hipEventSynchronize(pl->uploaded));
+    pl->pending = false;
+  }
+  if (pl->h_cap < n_ints) {
+    if (pl->h_meta) MKV_CHECK_HIP(hipHostFree(pl->h_meta));
+    pl->h_meta = nullptr;
+    pl->h_cap = 0;
+    MKV_CHECK_HIP(hipHostMalloc(reinterpret_cast<void **>(&pl->h_meta), n_ints * 4));
+    pl->h_cap = n_ints;
+  }
+  int32_t *ctx = pl->h_meta, *blk0 = ctx + num_seqs, *pseq = blk0 + num_seqs + 1;
+  int64_t acc = 0;
+  for (int32_t b = 0; b < num_seqs; b++) {
+    ctx[b] = h_ctx_lens[b];
+    blk0[b] = (int32_t)acc;
+    acc += (h_ctx_lens[b] + kPageSize - 1) / kPageSize;
+  }
+  blk0[num_seqs] = (int32_t)acc;
+  for (int32_t b = 0, piece = 0; piece < P; piece++) {
+    const int64_t f = piece * BP;
+    while (blk0[b + 1] <= f) b++;
+    pseq[piece] = b;
+  }
+  int32_t *mseq = pseq + P;
+  int n_merge = 0;
+  for (int32_t b = 0; b < num_seqs; b++)
+    if (blk0[b] / BP != (blk0[b + 1] - 1) / BP) mseq[n_merge++] = b;
+  const size_t used = (size_t)num_seqs + (num_seqs + 1) + P + n_merge;
+  if (pl->meta_cap < used) {
+    MKV_CHECK_HIP(hipStreamSynchronize(hs));  // earlier launches may read the old buffer
+    if (pl->d_meta) MKV_CHECK_HIP(hipFree(pl->d_meta));
+    pl->d_meta = nullptr;
+    pl->meta_cap = 0;
+    MKV_CHECK_HIP(hipMalloc(reinterpret_cast<void **>(&pl->d_meta), n_ints * 4));
+    pl->meta_cap = n_ints;
+  }
+  const uint64_t slots = (uint64_t)P + num_seqs;
+  const uint64_t rows = slots * g.Hq;
+  const uint64_t ml = (rows * 8 + 255) / 256 * 256;
+  const uint64_t need = ml + rows * g.D * 4;
+  if (pl->ws_cap < need) {
+    MKV_CHECK_HIP(hipStreamSynchronize(hs));
+    if (pl->d_ws) MKV_CHECK_HIP(hipFree(pl->d_ws));
+    pl->d_ws = nullptr;
+    pl->ws_cap = 0;
+    MKV_CHECK_HIP(hipMalloc(&pl->d_ws, need));
+    pl->ws_cap = need;
+  }
+  pl->ws_ml_bytes = ml;
+  MKV_CHECK_HIP(hipMemcpyAsync(pl->d_meta, pl->h_meta, used * 4, hipMemcpyHostToDevice, hs));
+  MKV_CHECK_HIP(hipEventRecord(pl->uploaded, hs));
+  pl->pending = true;
+  pl->B = num_seqs;
+  pl->P = (int32_t)P;
+  pl->BP = (int32_t)BP;
+  pl->total = (int32_t)total;
+  pl->n_merge = n_merge;
+  return MKV_OK;
+}
+
+extern "C" int mkv_decode_plan_info(const mkv_decode_plan *plan, int32_t *out_pieces,
+                                    int32_t *out_blocks_per_piece, int32_t *out_merge_seqs) {
+  if (!plan) return set_error(MKV_ERR_INVALID_ARGUMENT, "plan is NULL");
+  const Plan *pl = reinterpret_cast<const Plan *>(plan);
+  if (out_pieces) *out_pieces = pl->P;
+  if (out_blocks_per_piece) *out_blocks_per_piece = pl->BP;
+  if (out_merge_seqs) *out_merge_seqs = pl->n_merge;
+  return MKV_OK;
+}
+
+static int launch_planned(Pool *p, const Plan *pl, int32_t layer, const void *d_k_new, const void *d_v_new,
+                          const void *d_q, void *d_o, const int32_t *d_block_indptr,
+                          const int32_t *d_block_ids, float scale, uint32_t flags, void *stream) {
+  const Geom &g = p->g;
+  if (pl->pool != p) return set_error(MKV_ERR_INVALID_ARGUMENT, "plan belongs to another pool");
+  if (pl->B < 1) return set_error(MKV_ERR_INVALID_ARGUMENT, "plan was never built");
+  bool use_mfma = false;
+  int rc = check_common(p, layer, flags, scale, use_mfma);
+  if (rc) return rc;
+  if (!d_q || !d_o || !d_block_indptr || !d_block_ids)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL device pointer");
+  if (!aligned16(d_q) || !aligned16(d_o) || !aligned16(d_k_new) || !aligned16(d_v_new))
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "q, o and new K/V rows must be 16-byte aligned");
+  DeviceGuard guard(p->device);
+  hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  KArgs a = make_kargs(p, layer, d_q, d_o, d_block_indptr, d_block_ids, scale, flags, use_mfma);
+  a.new_k = reinterpret_cast<const uint8_t *>(d_k_new);
+  a.new_v = reinterpret_cast<const uint8_t *>(d_v_new);
+  a.ws_ml = reinterpret_cast<float *>(pl->d_ws);
+  a.ws_o = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(pl->d_ws) + pl->ws_ml_bytes);
+  const PlanDev pd = plan_dev(pl);
+  const int hcs = g.Hkv * a.nqc;
+  const int wpw = std::min(4, hcs);
+  const dim3 grid((unsigned)pl->P, (unsigned)((hcs + wpw - 1) / wpw)), block(64 * wpw);
+  MKV_DISPATCH(attn_planned_kernel, grid, block, hs, a, pd);
+  MKV_CHECK_LAUNCH("attn_planned_kernel");
+  if (pl->n_merge) {
+    const int64_t mwgs = ((int64_t)pl->n_merge * g.Hq + 3) / 4;
+    MKV_DISPATCH_MERGE(merge_planned_kernel, dim3((unsigned)mwgs), dim3(256), hs, a, pd);
+    MKV_CHECK_LAUNCH("merge_planned_kernel");
+  }
+  return MKV_OK;
+}
+
+extern "C" int mkv_decode_attention_planned(mkv_pool *pool, const mkv_decode_plan *plan, int32_t layer,
+                                            const void *d_q, void *d_o, const int32_t *d_block_indptr,
+                                            const int32_t *d_block_ids, float scale, uint32_t flags,
+                                            void *stream) {
+  if (!pool || !plan) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL pool or plan");
+  return launch_planned(reinterpret_cast<Pool *>(pool), reinterpret_cast<const Plan *>(plan), layer,
+                        nullptr, nullptr, d_q, d_o, d_block_indptr, d_block_ids, scale, flags, stream);
+}
+
+extern "C" int mkv_decode_step(mkv_pool *pool, const mkv_decode_plan *plan, int32_t layer,
+                               const void *d_k_new, const void *d_v_new, const void *d_q, void *d_o,
+                               const int32_t *d_block_indptr, const int32_t *d_block_ids, float scale,
+                               uint32_t flags, void *stream) {
+  if (!pool || !plan) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL pool or plan");
+  if (!d_k_new || !d_v_new) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL new K/V rows");
+  return launch_planned(reinterpret_cast<Pool *>(pool), reinterpret_cast<const Plan *>(plan), layer,
+                        d_k_new, d_v_new, d_q, d_o, d_block_indptr, d_block_ids, scale, flags, stream);
 }

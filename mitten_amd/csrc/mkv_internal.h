@@ -8,7 +8,7 @@
 #include <cstdio>
 #include <string>
 
-#include "../../include/mitten_kv.h"
+#include "mitten_kv.h"
 
 namespace mkv {
 

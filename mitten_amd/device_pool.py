@@ -312,6 +312,96 @@ class DeviceKvPool:
             _stream_handle(stream)))
         return out
 
+    # -- planned path -------------------------------------------------------------------------
+    def plan(self, ctx_lens, pieces: int = 0, stream=None) -> "DecodePlan":
+        """Work plan of one decode step from host context lengths (tokens
+        attended per sequence, including the token appended this step)."""
+        p = DecodePlan(self)
+        p.build(ctx_lens, pieces, stream)
+        return p
+
+    def _planned_args(self, plan, q, block_indptr, block_ids, out, scale, zero_sink, kernel):
+        d = self.desc
+        if plan.pool is not self:
+            raise BackendError(MKV_ERR_INVALID_ARGUMENT, "plan belongs to another pool")
+        B = plan.num_seqs
+        self._check_tensor(q, (B, d.num_q_heads, d.head_dim), "q")
+        self._i32(block_indptr, "block_indptr", B + 1)
+        self._i32(block_ids, "block_ids")
+        torch = _torch()
+        if out is None:
+            out = torch.empty_like(q)
+        self._check_tensor(out, (B, d.num_q_heads, d.head_dim), "out")
+        if scale is None:
+            scale = float(np.float32(d.head_dim ** -0.5))
+        flags = ATTN_ZERO_SINK if zero_sink else 0
+        if kernel == "valu":
+            flags |= ATTN_FORCE_VALU
+        elif kernel == "mfma":
+            flags |= ATTN_FORCE_MFMA
+        elif kernel is not None:
+            raise ValueError(f"unknown kernel {kernel!r}")
+        return out, scale, flags
+
+    def decode_attention_planned(self, layer: int, plan, q, block_indptr, block_ids, out=None,
+                                 scale: float | None = None, zero_sink: bool = False,
+                                 kernel: str | None = None, stream=None):
+        out, scale, flags = self._planned_args(plan, q, block_indptr, block_ids, out, scale, zero_sink, kernel)
+        _raise(self._lib.mkv_decode_attention_planned(
+            self._h, plan._h, layer, _dptr(q), _dptr(out), _dptr(block_indptr), _dptr(block_ids),
+            scale, flags, _stream_handle(stream)))
+        return out
+
+    def decode_step(self, layer: int, plan, k_new, v_new, q, block_indptr, block_ids, out=None,
+                    scale: float | None = None, zero_sink: bool = False, kernel: str | None = None,
+                    stream=None):
+        """Append k_new/v_new ([B, Hkv, D]) at position ctx-1 of every sequence,
+        then attend over ctx tokens, in one launch (plus the split-K merge)."""
+        d = self.desc
+        out, scale, flags = self._planned_args(plan, q, block_indptr, block_ids, out, scale, zero_sink, kernel)
+        B = plan.num_seqs
+        self._check_tensor(k_new, (B, d.num_kv_heads, d.head_dim), "k_new")
+        self._check_tensor(v_new, (B, d.num_kv_heads, d.head_dim), "v_new")
+        _raise(self._lib.mkv_decode_step(
+            self._h, plan._h, layer, _dptr(k_new), _dptr(v_new), _dptr(q), _dptr(out),
+            _dptr(block_indptr), _dptr(block_ids), scale, flags, _stream_handle(stream)))
+        return out
+
+    def bind_decode_step(self, plan, k_new, v_new, q, block_indptr, block_ids, out,
+                         scale: float | None = None, zero_sink: bool = False,
+                         kernel: str | None = None, stream=None):
+        """Validates, once, the buffers of every layer of one decode step
+        (k_new, v_new: [L, B, Hkv, D]; q, out: [L, B, Hq, D]) and returns
+        `run(layer)`, which enqueues mkv_decode_step for that layer with no
+        per-call Python checks (the engine's per-layer hot loop)."""
+        d = self.desc
+        L, B = d.num_layers, plan.num_seqs
+        self._check_tensor(k_new, (L, B, d.num_kv_heads, d.head_dim), "k_new")
+        self._check_tensor(v_new, (L, B, d.num_kv_heads, d.head_dim), "v_new")
+        self._check_tensor(q, (L, B, d.num_q_heads, d.head_dim), "q")
+        self._check_tensor(out, (L, B, d.num_q_heads, d.head_dim), "out")
+        _, scale, flags = self._planned_args(plan, q[0], block_indptr, block_ids, out[0], scale, zero_sink,
+                                             kernel)
+        fn = self._lib.mkv_decode_step
+        h, ph = self._h, plan._h
+        sh = _stream_handle(stream)
+        kv_stride = B * d.num_kv_heads * d.head_dim * d.elem_bytes
+        qo_stride = B * d.num_q_heads * d.head_dim * d.elem_bytes
+        kb, vb, qb, ob = k_new.data_ptr(), v_new.data_ptr(), q.data_ptr(), out.data_ptr()
+        ip, ix = _dptr(block_indptr), _dptr(block_ids)
+        args = [(h, ph, layer, ctypes.c_void_p(kb + layer * kv_stride), ctypes.c_void_p(vb + layer * kv_stride),
+                 ctypes.c_void_p(qb + layer * qo_stride), ctypes.c_void_p(ob + layer * qo_stride), ip, ix,
+                 scale, flags, sh) for layer in range(L)]
+        keep = (k_new, v_new, q, out, block_indptr, block_ids)
+
+        def run(layer: int) -> None:
+            st = fn(*args[layer])
+            if st:
+                _raise(st)
+
+        run.keep_alive = keep
+        return run
+
     # -- host read-back / upload (tests) ------------------------------------------------------
     def read(self) -> np.ndarray:
         """Copy of the whole pool as numpy (uint16 bit patterns for bf16)."""
@@ -350,3 +440,38 @@ class DeviceKvPool:
         }
         t = torch.as_tensor(view, device=f"cuda:{self.device}")
         return t if self.desc.dtype == "f32" else t.view(dt)
+
+
+class DecodePlan:
+    """Host-built work plan of one decode step (balanced pieces of the batch's
+    blocks), reused by every layer of the step."""
+
+    def __init__(self, pool: DeviceKvPool):
+        self.pool = pool
+        self._lib = pool._lib
+        h = ctypes.c_void_p()
+        _raise(self._lib.mkv_decode_plan_create(pool._h, ctypes.byref(h)))
+        self._h = h
+        self.num_seqs = 0
+
+    def build(self, ctx_lens, pieces: int = 0, stream=None) -> None:
+        c = np.ascontiguousarray(ctx_lens, np.int32)
+        self._ctx = c  # the upload is asynchronous; keep the host copy alive
+        _raise(self._lib.mkv_decode_plan_build(self._h, _i32p(c), c.size, pieces, _stream_handle(stream)))
+        self.num_seqs = int(c.size)
+
+    def info(self):
+        p, bp, m = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+        _raise(self._lib.mkv_decode_plan_info(self._h, ctypes.byref(p), ctypes.byref(bp), ctypes.byref(m)))
+        return {"pieces": p.value, "blocks_per_piece": bp.value, "merge_seqs": m.value}
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._lib.mkv_decode_plan_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -245,3 +245,127 @@ def test_attention_full_config_one_layer(name):
     ref = orc.decode_attention(odesc(desc), host, 0, widen(q), batch.block_indptr, batch.block_ids,
                                batch.ctx_lens)
     assert_attention_close(got, ref, desc.dtype)
+
+
+# ------------------------------------------------------------ planned path ----
+
+def _planned_case(shape, ctx, seed, pieces=0, kernel=None, zero_sink=False, fused=False):
+    """Returns (got, ref, dtype, pool_after, pool_want) for one layer."""
+    L, Hq, Hkv, D, dt = SHAPES[shape]
+    rng = wl.SplitMix64(seed)
+    batch = wl.decode_batch_from_contexts([c - 1 for c in ctx], rng, extra_blocks=3)
+    desc = PoolDesc(L, Hkv, Hq, D, batch.num_blocks, dt)
+    layer = L - 1
+    B = len(ctx)
+    host = normal(seed + 1, desc.shape, dt)
+    q = normal(seed + 2, (B, Hq, D), dt)
+    kn = normal(seed + 3, (B, Hkv, D), dt)
+    vn = normal(seed + 4, (B, Hkv, D), dt)
+    with DeviceKvPool(desc) as pool:
+        pool.write(host)
+        plan = pool.plan(batch.ctx_lens, pieces=pieces)
+        args = (_i32(batch.block_indptr), _i32(batch.block_ids))
+        if fused:
+            o = pool.decode_step(layer, plan, to_device(kn), to_device(vn), to_device(q), *args,
+                                 zero_sink=zero_sink, kernel=kernel)
+        else:
+            o = pool.decode_attention_planned(layer, plan, to_device(q), *args, zero_sink=zero_sink, kernel=kernel)
+        pool.check()
+        got = to_host(o)
+        after = pool.read()
+        info = plan.info()
+        plan.close()
+    want = host.copy()
+    if fused:
+        assert orc.append(odesc(desc), want, layer, kn, vn, batch.slot_mapping) == -1
+    ref = orc.decode_attention(odesc(desc), want, layer, widen(q), batch.block_indptr, batch.block_ids,
+                               batch.ctx_lens, zero_sink=zero_sink)
+    return got, ref, dt, after, want, info
+
+
+PLAN_CTX = [1, 2, 15, 16, 17, 33, 100, 129, 257, 500, 1000, 3, 64, 65, 700]
+
+
+@pytest.mark.parametrize("pieces", [0, 1, 7, 40, 300])
+@pytest.mark.parametrize("shape,kernel", [("qwen0.5b-f32", None), ("qwen7b-bf16", "mfma"),
+                                          ("qwen7b-bf16", "valu"), ("gemma2b-bf16", "mfma")])
+def test_planned_attention(shape, kernel, pieces):
+    got, ref, dt, after, want, info = _planned_case(shape, PLAN_CTX, 60, pieces=pieces, kernel=kernel)
+    assert_attention_close(got, ref, dt)
+    assert np.array_equal(bits(after), bits(want))  # attention never writes the pool
+
+
+@pytest.mark.parametrize("pieces", [0, 5, 64])
+@pytest.mark.parametrize("shape,kernel", [("qwen0.5b-f32", None), ("qwen7b-bf16", "mfma"),
+                                          ("qwen7b-bf16", "valu"), ("gemma2b-bf16", "mfma")])
+def test_decode_step_fused_append(shape, kernel, pieces):
+    got, ref, dt, after, want, info = _planned_case(shape, PLAN_CTX, 61, pieces=pieces, kernel=kernel, fused=True)
+    assert np.array_equal(bits(after), bits(want)), "fused append is not bit-exact"
+    assert_attention_close(got, ref, dt)
+
+
+@pytest.mark.parametrize("shape", ["qwen0.5b-f32", "qwen7b-bf16"])
+def test_planned_zero_sink(shape):
+    got, ref, dt, *_ = _planned_case(shape, [1, 7, 40, 300], 62, pieces=9, zero_sink=True, fused=True)
+    assert_attention_close(got, ref, dt)
+
+
+@pytest.mark.parametrize("name", ["qwen2.5-7b", "gemma-2b-mqa"])
+def test_decode_step_full_config_one_layer(name):
+    """Fused append + planned attention at the configuration's full size."""
+    c = wl.CONFIGS[name]
+    batch = wl.config_batch(name)
+    desc = PoolDesc(1, c["num_kv_heads"], c["num_q_heads"], c["head_dim"], batch.num_blocks, c["dtype"])
+    B = batch.num_seqs
+    host = normal(70, desc.shape, desc.dtype)
+    q = normal(71, (B, desc.num_q_heads, desc.head_dim), desc.dtype)
+    kn = normal(72, (B, desc.num_kv_heads, desc.head_dim), desc.dtype)
+    vn = normal(73, (B, desc.num_kv_heads, desc.head_dim), desc.dtype)
+    with DeviceKvPool(desc) as pool:
+        pool.write(host)
+        plan = pool.plan(batch.ctx_lens)
+        o = pool.decode_step(0, plan, to_device(kn), to_device(vn), to_device(q), _i32(batch.block_indptr),
+                             _i32(batch.block_ids))
+        pool.check()
+        got = to_host(o)
+        after = pool.read()
+        plan.close()
+    assert orc.append(odesc(desc), host, 0, kn, vn, batch.slot_mapping) == -1
+    assert np.array_equal(bits(after), bits(host))
+    ref = orc.decode_attention(odesc(desc), host, 0, widen(q), batch.block_indptr, batch.block_ids,
+                               batch.ctx_lens)
+    assert_attention_close(got, ref, desc.dtype)
+
+
+def test_bound_decode_step_matches_per_call():
+    """bind_decode_step (validated once, bare ABI calls per layer) gives the
+    same pool and outputs as decode_step called layer by layer."""
+    import torch
+
+    L, Hq, Hkv, D, dt = SHAPES["qwen7b-bf16"]
+    rng = wl.SplitMix64(80)
+    batch = wl.decode_batch_from_contexts([30, 200, 1, 77], rng, extra_blocks=2)
+    desc = PoolDesc(L, Hkv, Hq, D, batch.num_blocks, dt)
+    host = normal(81, desc.shape, dt)
+    B = batch.num_seqs
+    q = to_device(normal(82, (L, B, Hq, D), dt))
+    kn = to_device(normal(83, (L, B, Hkv, D), dt))
+    vn = to_device(normal(84, (L, B, Hkv, D), dt))
+    ip, ix = _i32(batch.block_indptr), _i32(batch.block_ids)
+    results = []
+    for bound in (False, True):
+        with DeviceKvPool(desc) as pool:
+            pool.write(host)
+            plan = pool.plan(batch.ctx_lens, pieces=3)
+            out = torch.empty_like(q)
+            run = pool.bind_decode_step(plan, kn, vn, q, ip, ix, out) if bound else None
+            for layer in range(L):
+                if bound:
+                    run(layer)
+                else:
+                    pool.decode_step(layer, plan, kn[layer], vn[layer], q[layer], ip, ix, out=out[layer])
+            pool.check()
+            results.append((pool.read(), to_host(out)))
+            plan.close()
+    assert np.array_equal(bits(results[0][0]), bits(results[1][0]))
+    assert np.array_equal(bits(results[0][1]), bits(results[1][1]))
