@@ -1,0 +1,343 @@
+"""Host-side bookkeeping: the reference's own unit tests, ported one for one
+(kv_pool.rs:104-162, radix_cache.rs:305-425), then the block manager that
+feeds the device pool (refcounts, decode growth, copy-on-write, compaction).
+CPU only."""
+from __future__ import annotations
+
+import time
+
+import numpy as np
+import pytest
+
+from mitten_amd.host import BlockManager, DoubleFree, KvCachePool, OutOfBlocks, PageTable, RadixCache
+
+# ---------------------------------------------- kv_pool.rs:104-162 (ported) ----
+
+
+def test_allocate_and_free():
+    pool = KvCachePool(16, 16)
+    p1 = pool.allocate(1)
+    assert pool.free_pages() == 15
+    pool.free(p1)
+    assert pool.free_pages() == 16
+
+
+def test_allocate_exhaustion():
+    pool = KvCachePool(2, 16)
+    assert pool.allocate(1) is not None
+    assert pool.allocate(1) is not None
+    assert pool.allocate(1) is None
+    assert pool.free_pages() == 0
+
+
+def test_required_bytes():
+    assert KvCachePool.required_bytes(1, 16, 1, 1, 1, 1) == 32
+    assert KvCachePool.required_bytes(512, 16, 28, 4, 128, 2) == 2 * 512 * 16 * 28 * 4 * 128 * 2
+
+
+def test_double_free_panics():
+    pool = KvCachePool(4, 16)
+    p = pool.allocate(1)
+    pool.free(p)
+    with pytest.raises(DoubleFree):
+        pool.free(p)
+
+
+def test_page_table_roundtrip():
+    pt = PageTable()
+    pt.insert(7, 0, 7)
+    assert pt.lookup(7, 0) == 7
+    assert pt.remove_request(7) == [7]
+    assert pt.lookup(7, 0) is None
+
+
+def test_allocation_order_and_lifo_reuse():
+    """new() reverses 0..n so pages come out 0,1,2,... (kv_pool.rs:19-20);
+    a freed page is the next one handed out (stack)."""
+    pool = KvCachePool(5, 16)
+    assert [pool.allocate(1) for _ in range(3)] == [0, 1, 2]
+    pool.free(1)
+    pool.free(0)
+    assert pool.allocate(2) == 0 and pool.allocate(2) == 1 and pool.allocate(2) == 3
+
+
+# ------------------------------------------ radix_cache.rs:305-425 (ported) ----
+
+
+def test_empty_match():
+    cache = RadixCache(4, 16)
+    length, pages, nodes = cache.match_prefix([1, 2, 3])
+    assert length == 0 and pages == [] and nodes == []
+
+
+def test_insert_and_match_full():
+    cache = RadixCache(4, 16)
+    cache.insert_prefix([1, 2, 3, 4], [10])
+    length, pages, nodes = cache.match_prefix([1, 2, 3, 4, 5])
+    assert length == 4 and pages == [10] and len(nodes) == 1
+
+
+def test_edge_split():
+    cache = RadixCache(2, 16)
+    cache.insert_prefix([1, 2, 3, 4], [10, 11])
+    cache.insert_prefix([1, 2, 5, 6], [10, 12])
+    l1, p1, _ = cache.match_prefix([1, 2, 3, 4])
+    assert l1 == 4 and p1 == [10, 11]
+    l2, p2, _ = cache.match_prefix([1, 2, 5, 6])
+    assert l2 == 4 and p2 == [10, 12]
+
+
+def test_lru_eviction():
+    cache = RadixCache(2, 2)
+    cache.insert_prefix([1, 2], [10])
+    cache.insert_prefix([3, 4], [11])
+    assert cache.total_cached_pages() == 2
+    cache.insert_prefix([5, 6], [12])  # evicts [1, 2]
+    assert cache.total_cached_pages() == 2
+    length, _, _ = cache.match_prefix([1, 2])
+    assert length == 0
+    assert cache.take_evicted() == [10]  # returned, not leaked (reference drops it)
+
+
+def test_lock_prevents_eviction():
+    cache = RadixCache(2, 1)
+    cache.insert_prefix([1, 2], [10])
+    _, _, nodes = cache.match_prefix([1, 2])
+    cache.insert_prefix([3, 4], [11])
+    assert cache.total_cached_pages() == 2  # overflowed: nothing was evictable
+    cache.unlock_nodes(nodes)
+    freed = cache.evict_pages(1)
+    assert len(freed) == 1
+
+
+def test_insert_and_match_partial_edge():
+    cache = RadixCache(4, 16)
+    cache.insert_prefix([1, 2, 3, 4], [10])
+    cache.insert_prefix([1, 2, 5, 6], [11])
+    length, pages, _ = cache.match_prefix([1, 2, 3, 4])
+    assert len(pages) == length // 4
+    length2, pages2, _ = cache.match_prefix([1, 2, 5, 6])
+    assert len(pages2) == length2 // 4
+
+
+def test_promote_request():
+    cache = RadixCache(8, 16)
+    cache.promote_request(list(range(1, 9)), 8, [42])
+    length, pages, _ = cache.match_prefix(list(range(1, 9)))
+    assert length == 8 and pages == [42]
+
+
+def test_page_alignment():
+    cache = RadixCache(4, 16)
+    cache.insert_prefix([1, 2, 3, 4, 5, 6], [10])
+    length, pages, _ = cache.match_prefix([1, 2, 3, 4, 5, 6])
+    assert length == 4 and pages == [10]
+
+
+# ------------------------------------------------- radix: further semantics ----
+
+
+def test_split_creates_intermediate_node_and_keeps_pages():
+    cache = RadixCache(2, 16)
+    cache.insert_prefix([1, 2, 3, 4, 5, 6], [10, 11, 12])
+    assert cache.num_nodes() == 2  # root + leaf
+    cache.insert_prefix([1, 2, 3, 4, 7, 8], [10, 11, 13])
+    assert cache.num_nodes() == 4  # root, [1..4], [5,6], [7,8]
+    assert cache.total_cached_pages() == 4
+    assert cache.match_prefix([1, 2, 3, 4, 5, 6])[1] == [10, 11, 12]
+    assert cache.match_prefix([1, 2, 3, 4, 7, 8])[1] == [10, 11, 13]
+
+
+def test_eviction_order_follows_the_lazy_heap():
+    """The LRU heap holds stale entries (radix_cache.rs:40,160,233-234): an entry
+    is skipped only if its node is gone or not evictable (:250-255). So a leaf
+    touched after insertion is still evicted at its insertion stamp, first."""
+    cache = RadixCache(2, 8)
+    for i, t in enumerate(([1, 2], [3, 4], [5, 6])):
+        cache.insert_prefix(t, [10 + i])
+    _, _, n = cache.match_prefix([1, 2])
+    cache.unlock_nodes(n)
+    assert cache.evict_pages(1) == [10]
+    assert cache.evict_pages(1) == [11]
+    assert cache.evict_pages(1) == [12]
+    assert cache.evict_pages(1) == []
+
+
+def test_locked_leaf_is_skipped_until_unlocked():
+    cache = RadixCache(2, 8)
+    for i, t in enumerate(([1, 2], [3, 4])):
+        cache.insert_prefix(t, [10 + i])
+    _, _, n = cache.match_prefix([1, 2])
+    assert cache.evict_pages(1) == [11]
+    assert cache.evict_pages(1) == []  # [1,2] locked; its heap entry was consumed
+    cache.unlock_nodes(n)  # re-queued on unlock
+    assert cache.evict_pages(1) == [10]
+
+
+def test_parent_becomes_evictable_after_children_go():
+    cache = RadixCache(2, 8)
+    cache.insert_prefix([1, 2, 3, 4], [10, 11])
+    cache.insert_prefix([1, 2, 5, 6], [10, 12])
+    freed = cache.evict_pages(3)
+    assert sorted(freed) == [10, 11, 12]
+    assert cache.total_cached_pages() == 0 and cache.num_nodes() == 1
+
+
+# ---------------------------------------------------------- block manager ----
+
+
+def _tokens(seed, n):
+    return np.random.default_rng(seed).integers(0, 50_000, n).astype(np.uint32)
+
+
+def test_admit_allocates_ceil_pages_and_decode_grows():
+    bm = BlockManager(64, 16)
+    assert bm.admit(1, _tokens(0, 40)) == 0
+    assert len(bm.table(1)) == 3
+    slots, cow = bm.append(1, 40)  # the prompt's K/V
+    assert cow == [] and bm.seq_len(1) == 40
+    t = bm.table(1)
+    assert list(slots) == [t[p // 16] * 16 + p % 16 for p in range(40)]
+    for step in range(30):  # decode: a block is added whenever pos % 16 == 0
+        s, _ = bm.append(1, 1)
+        pos = 40 + step
+        assert s[0] == bm.table(1)[pos // 16] * 16 + pos % 16
+    assert len(bm.table(1)) == (70 + 15) // 16
+    bm.check_invariants()
+
+
+def test_radix_sharing_refcounts_and_no_double_free():
+    """A finished request's promoted pages stay in the tree; releasing the
+    request must not free them (the reference frees them twice: scheduler.rs:169
+    and later eviction)."""
+    bm = BlockManager(32, 16)
+    toks = _tokens(1, 64)
+    bm.admit(1, toks)
+    bm.append(1, 64)
+    bm.promote(1, toks)
+    assert bm.cached_pages() == 4
+    assert all(bm.refcount(b) == 2 for b in bm.table(1))
+    bm.release(1)
+    assert bm.free_blocks() == 28
+    bm.check_invariants()
+    cached = bm.admit(2, np.concatenate([toks, _tokens(2, 20)]))
+    assert cached == 64
+    assert all(bm.refcount(b) == 2 for b in bm.table(2)[:4])
+    bm.append(2, 20)
+    bm.check_invariants()
+    bm.release(2)
+    assert bm.evict(100) == 4
+    assert bm.free_blocks() == 32
+    bm.check_invariants()
+
+
+def test_fork_then_copy_on_write_of_shared_partial_block():
+    bm = BlockManager(16, 16)
+    bm.admit(1, _tokens(3, 20))
+    bm.append(1, 20)  # blocks: [full, partial(4 tokens)]
+    bm.fork(1, 2)
+    t1, t2 = bm.table(1), bm.table(2)
+    assert list(t1) == list(t2) and all(bm.refcount(b) == 2 for b in t1)
+    slots, cow = bm.append(2, 1)  # writes into the shared partial block -> copy first
+    assert len(cow) == 1 and cow[0][0] == t1[1]
+    assert bm.table(2)[1] == cow[0][1] != t1[1]
+    assert slots[0] == cow[0][1] * 16 + 4
+    slots1, cow1 = bm.append(1, 1)  # last holder writes in place
+    assert cow1 == [] and slots1[0] == t1[1] * 16 + 4
+    bm.check_invariants()
+
+
+def test_compaction_moves_tail_blocks_into_holes():
+    bm = BlockManager(40, 16)
+    for s in range(8):
+        bm.admit(s, _tokens(10 + s, 50))
+        bm.append(s, 50)
+    for s in (1, 4, 6):
+        bm.release(s)
+    live = bm.live_blocks()
+    before = {s: bm.table(s).copy() for s in (0, 2, 3, 5, 7)}
+    src, dst = bm.plan_compaction()
+    assert len(src) == len(dst) and set(src).isdisjoint(dst)
+    assert all(d < live for d in dst) and all(s >= live for s in src)
+    moved = dict(zip(src.tolist(), dst.tolist()))
+    for s, t in before.items():
+        assert list(bm.table(s)) == [moved.get(b, b) for b in t]
+        assert max(bm.table(s)) < live
+    bm.check_invariants()
+    bm.admit(99, _tokens(99, 16))
+    assert bm.table(99)[0] == live  # free ids are now exactly [live, N)
+
+
+def test_admission_exhaustion_is_reported_and_changes_nothing():
+    bm = BlockManager(4, 16)
+    bm.admit(1, _tokens(4, 48))
+    with pytest.raises(OutOfBlocks):
+        bm.admit(2, _tokens(5, 32))
+    assert bm.free_blocks() == 1
+    bm.check_invariants()
+
+
+def test_batch_metadata_matches_tables():
+    bm = BlockManager(64, 16)
+    for s, n in ((5, 10), (6, 33), (7, 16)):
+        bm.admit(s, _tokens(s, n))
+        bm.append(s, n)
+    indptr, ids, ctx = bm.batch([6, 5, 7])
+    assert list(ctx) == [33, 10, 16]
+    assert list(ids[indptr[0]:indptr[1]]) == list(bm.table(6))
+    assert list(ids[indptr[2]:indptr[3]]) == list(bm.table(7))
+
+
+def test_scheduler_overhead_bound():
+    """scheduler_bench.rs:46-79 analogue: 1000 decode iterations over 32
+    sequences (append + batch metadata) within 1000 ms."""
+    bm = BlockManager(4096, 16)
+    seqs = list(range(32))
+    for s in seqs:
+        bm.admit(s, _tokens(100 + s, 16))
+        bm.append(s, 16)
+    t0 = time.perf_counter()
+    for _ in range(1000):
+        for s in seqs:
+            bm.append(s, 1)
+        bm.batch(seqs)
+    assert time.perf_counter() - t0 < 1.0
+    bm.check_invariants()
+
+
+def test_random_lifecycle_keeps_invariants():
+    rng = np.random.default_rng(7)
+    bm = BlockManager(256, 16, max_cached_pages=64)
+    live, next_id, prompts = set(), 0, {}
+    shared = _tokens(999, 64)
+    for it in range(400):
+        op = rng.integers(0, 5)
+        if op == 0 or not live:
+            n = int(rng.integers(1, 80))
+            toks = np.concatenate([shared[: int(rng.integers(0, 65))], _tokens(it, n)])
+            try:
+                cached = bm.admit(next_id, toks)
+            except OutOfBlocks:
+                continue
+            bm.append(next_id, len(toks) - cached)
+            prompts[next_id] = toks
+            live.add(next_id)
+            next_id += 1
+        elif op == 1:
+            s = int(rng.choice(sorted(live)))
+            try:
+                bm.append(s, int(rng.integers(1, 20)))
+            except OutOfBlocks:
+                pass
+        elif op == 2:
+            s = int(rng.choice(sorted(live)))
+            bm.promote(s, prompts[s])
+        elif op == 3:
+            s = int(rng.choice(sorted(live)))
+            bm.release(s)
+            live.discard(s)
+        else:
+            bm.evict(int(rng.integers(1, 8)))
+        bm.check_invariants()
+    bm.plan_compaction()
+    bm.check_invariants()
