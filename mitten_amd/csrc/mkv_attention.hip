@@ -160,10 +160,11 @@ __device__ __forceinline__ void mfma_load_q(const KArgs &a, int lane, int b, int
   }
 }
 
-// One 16-token block: scores, online softmax update, O += P.V.
+// One 16-token block whose first `nvalid` rows are context: scores, online
+// softmax update, O += P.V.
 template <int D>
 __device__ __forceinline__ void mfma_block(const u32x4 (&kq)[D / 32], const u32x4 (&vq)[D / 32],
-                                           int tb, int ctx, bool bad, const bf16x8 (&qop)[D / 32],
+                                           int nvalid, bool bad, const bf16x8 (&qop)[D / 32],
                                            float sl2, int lane, MState<D> &st) {
   constexpr int NR = D / 32;
   const int g4 = lane >> 4, rq = lane & 3;
@@ -174,7 +175,7 @@ __device__ __forceinline__ void mfma_block(const u32x4 (&kq)[D / 32], const u32x
   // Lane holds S[token tb + 4*g4 + i][q = lane%16].
   float x[4];
 #pragma unroll
-  for (int i = 0; i < 4; i++) x[i] = (!bad && tb + 4 * g4 + i < ctx) ? S[i] * sl2 : -INFINITY;
+  for (int i = 0; i < 4; i++) x[i] = (!bad && 4 * g4 + i < nvalid) ? S[i] * sl2 : -INFINITY;
   float mloc = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
   mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
   mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
@@ -199,7 +200,7 @@ __device__ __forceinline__ void mfma_block(const u32x4 (&kq)[D / 32], const u32x
   const i16x4 pb = __builtin_bit_cast(i16x4, (uint64_t)p01 | ((uint64_t)p23 << 32));
   // V rows past the context (or of a rejected block) are zeroed: stale slots
   // may hold any bit pattern, and 0 * NaN would poison the sum.
-  const bool vvalid = !bad && tb + 4 * g4 + rq < ctx;
+  const bool vvalid = !bad && 4 * g4 + rq < nvalid;
 #pragma unroll
   for (int s = 0; s < NR; s++) {
     uint32_t w[4] = {vq[s][0], vq[s][1], vq[s][2], vq[s][3]};
@@ -259,7 +260,7 @@ __device__ __forceinline__ void mfma_run(const KArgs &a, const Seg &sg, int lane
       if (jj < sg.j1) {
         if (jj + kRing - 1 < sg.j1) issue(kb[(s + kRing - 1) % kRing], vb[(s + kRing - 1) % kRing], jj + kRing - 1);
         const bool bad = (badmask >> (jj - sg.j0)) & 1;
-        mfma_block<D>(kb[s], vb[s], jj * kPageSize, sg.ctx, bad, qop, a.sl2, lane, st);
+        mfma_block<D>(kb[s], vb[s], min(kPageSize, sg.ctx - jj * kPageSize), bad, qop, a.sl2, lane, st);
       }
     }
   }
@@ -488,49 +489,51 @@ __device__ __forceinline__ void run_segment(const KArgs &a, const Seg &sg, int l
 
 // Log-sum-exp merge of n partial rows ws[base + s*stride], s < n, into o.
 // Lane s holds partial s's (m, l); lane d holds dims d + 64k of every
-// partial. All loads of up to 16 partials issue before the first use, so a
-// merge costs about one memory round trip; weights exp2(m_s - M) are
-// broadcast with readlane.
+// partial. Up to 16 partials merge in one memory round trip: all their loads
+// are issued before the first use; weights exp2(m_s - M) are broadcast with
+// readlane. More partials take further rounds of 16.
 template <int D, bool BF16>
 __device__ __forceinline__ void merge_rows(const KArgs &a, int lane, int64_t base, int64_t stride, int n,
                                            int64_t out_row) {
   constexpr int DPL = (D + 63) / 64;
   constexpr int SB = 16;
-  float M = -INFINITY;
-  for (int s0 = 0; s0 < n; s0 += 64)
-    if (s0 + lane < n) M = fmaxf(M, a.ws_ml[2 * (base + (s0 + lane) * stride)]);
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
-  float L = 0.0f, acc[DPL];
+  float acc[DPL];
 #pragma unroll
   for (int k = 0; k < DPL; k++) acc[k] = 0.0f;
-  for (int s0 = 0; s0 < n; s0 += 64) {
-    float w = 0.0f;
-    if (s0 + lane < n) {
-      const float2 ml = *reinterpret_cast<const float2 *>(a.ws_ml + 2 * (base + (s0 + lane) * stride));
-      w = fast_exp2(ml.x - M);
-      L += ml.y * w;
-    }
-    const int cnt = min(64, n - s0);
-    for (int s1 = 0; s1 < cnt; s1 += SB) {
-      float ov[SB][DPL];
+  float M = -INFINITY, L = 0.0f;
+  for (int s0 = 0; s0 < n; s0 += SB) {
+    const int cnt = min(SB, n - s0);
+    float2 ml = make_float2(-INFINITY, 0.0f);
+    if (lane < cnt) ml = *reinterpret_cast<const float2 *>(a.ws_ml + 2 * (base + (int64_t)(s0 + lane) * stride));
+    float ov[SB][DPL];
 #pragma unroll
-      for (int i = 0; i < SB; i++)
+    for (int i = 0; i < SB; i++)
 #pragma unroll
-        for (int k = 0; k < DPL; k++) {
-          const int d = lane + 64 * k;
-          ov[i][k] = (s1 + i < cnt && d < D) ? a.ws_o[(base + (int64_t)(s0 + s1 + i) * stride) * D + d] : 0.0f;
-        }
-#pragma unroll
-      for (int i = 0; i < SB; i++) {
-        const float wi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), (s1 + i) & 63));
-#pragma unroll
-        for (int k = 0; k < DPL; k++) acc[k] = fmaf(wi, ov[i][k], acc[k]);
+      for (int k = 0; k < DPL; k++) {
+        const int d = lane + 64 * k;
+        ov[i][k] = (i < cnt && d < D) ? a.ws_o[(base + (int64_t)(s0 + i) * stride) * D + d] : 0.0f;
       }
-    }
-  }
+    float mb = ml.x;
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o);
+    for (int o = 8; o >= 1; o >>= 1) mb = fmaxf(mb, __shfl_xor(mb, o));
+    mb = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, mb)));
+    const float Mn = fmaxf(M, mb);
+    const float carry = M == -INFINITY ? 0.0f : fast_exp2(M - Mn);
+    const float w = (lane < cnt && ml.x != -INFINITY) ? fast_exp2(ml.x - Mn) : 0.0f;
+    float lw = ml.y * w;
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) lw += __shfl_xor(lw, o);
+    L = L * carry + __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, lw)));
+#pragma unroll
+    for (int k = 0; k < DPL; k++) acc[k] *= carry;
+#pragma unroll
+    for (int i = 0; i < SB; i++) {
+      const float wi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), i));
+#pragma unroll
+      for (int k = 0; k < DPL; k++) acc[k] = fmaf(wi, ov[i][k], acc[k]);
+    }
+    M = Mn;
+  }
   const float f = final_scale(M, L, a.zero_sink);
 #pragma unroll
   for (int k = 0; k < DPL; k++) {
@@ -611,8 +614,148 @@ struct PlanDev {
   const int32_t *seq_blk0;    // [B+1] first flattened block of each sequence
   const int32_t *piece_seq;   // [P] sequence holding each piece's first block
   const int32_t *merge_seqs;  // [n_merge] sequences cut by a piece boundary
+  const int32_t *flat_seq;    // [total] sequence of each flattened block
+  const int32_t *flat_meta;   // [total] kMetaValid | kMetaLast | kMetaSingle bits
+  int32_t *flat_id;           // [total] block id (written per step from the tables)
   int32_t B, P, BP, total_blocks, n_merge;
 };
+
+// flat_meta bits of a flattened block.
+constexpr int kMetaValid = 31;       // rows of the block inside the context (1..16)
+constexpr int kMetaLast = 1 << 5;    // last block of its sequence (holds the new row)
+constexpr int kMetaSingle = 1 << 6;  // its sequence lies inside one piece (final store)
+
+// Once per plan build: flat_id[f] = block id of flattened block f from the
+// caller's block tables; an id outside the pool or a short table becomes -1
+// and is reported.
+__global__ void __launch_bounds__(256) flatten_ids_kernel(PlanDev pd, const int32_t *__restrict__ indptr,
+                                                          const int32_t *__restrict__ ids, int64_t nblocks,
+                                                          uint32_t *__restrict__ d_err) {
+  const int f = blockIdx.x * blockDim.x + threadIdx.x;
+  if (f >= pd.total_blocks) return;
+  const int b = pd.flat_seq[f];
+  const int j = f - pd.seq_blk0[b];
+  const int tab0 = indptr[b], tabn = indptr[b + 1] - tab0;
+  int32_t id = -1;
+  if (tab0 < 0 || j >= tabn) {
+    record_error(d_err, MKV_DEVERR_TABLE);
+  } else {
+    id = ids[tab0 + j];
+    if (id < 0 || id >= nblocks) {
+      record_error(d_err, MKV_DEVERR_BLOCK);
+      id = -1;
+    }
+  }
+  pd.flat_id[f] = id;
+}
+
+// MFMA attention over one piece as a single block stream: the three-deep
+// load ring runs across sequence boundaries, and the next sequence's Q is
+// loaded while the current one is computed.
+template <int D>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1)))
+attn_stream_kernel(KArgs a, PlanDev pd) {
+  constexpr int NR = D / 32;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hc = (int)blockIdx.y * (int)(blockDim.x >> 6) + wave;
+  if (hc >= a.Hkv * a.nqc) return;
+  const int h = hc / a.nqc, qc = hc % a.nqc;
+  const int m16 = lane & 15, g4 = lane >> 4, a4 = m16 >> 2, rq = m16 & 3;
+  const int p = blockIdx.x;
+  const int f0 = p * pd.BP;
+  const int n = min(pd.BP, pd.total_blocks - f0);  // 1..64 items
+  int32_t idv = -1, seqv = 0, metav = 0;
+  if (lane < n) {
+    idv = pd.flat_id[f0 + lane];
+    seqv = pd.flat_seq[f0 + lane];
+    metav = pd.flat_meta[f0 + lane];
+  }
+  const bool badv = lane < n && (idv < 0 || idv >= a.nblocks);
+  if (badv) idv = 0;
+  const uint64_t badmask = __ballot(badv);
+  const int prev_seq = __shfl_up(seqv, 1);
+  const uint64_t startmask = __ballot(lane < n && (lane == 0 || seqv != prev_seq));
+  auto seq_at = [&](int k) { return __builtin_amdgcn_readlane(seqv, k); };
+  auto next_start = [&](int k) {  // first segment start after item k, or 64
+    const uint64_t m = k >= 63 ? 0 : (startmask >> (k + 1)) << (k + 1);
+    return m ? __builtin_ctzll(m) : 64;
+  };
+
+  const int64_t head_off = (int64_t)h * D * 2;
+  const int64_t k_lane = (int64_t)m16 * a.row_bytes + head_off + 16 * g4;
+  const int64_t v_lane = (int64_t)(4 * g4 + rq) * a.row_bytes + head_off + 16 * a4;
+  u32x4 kb[kRing][NR], vb[kRing][NR];
+  auto issue = [&](u32x4 (&kd)[NR], u32x4 (&vd)[NR], int k) {
+    const int32_t blk = __builtin_amdgcn_readlane(idv, k);
+    const int meta = __builtin_amdgcn_readlane(metav, k);
+    const uint8_t *kp = a.k_plane + (int64_t)blk * a.block_bytes + k_lane;
+    const uint8_t *vp = a.v_plane + (int64_t)blk * a.block_bytes + v_lane;
+    if (a.new_k && (meta & kMetaLast) && !((badmask >> k) & 1)) {
+      // The sequence's new row: write it into its slot and read it from the input.
+      const int b = seq_at(k), row = (meta & kMetaValid) - 1;
+      const int64_t src = ((int64_t)b * a.Hkv + h) * D * 2;
+      if (qc == 0) store_new_row<D, 2>(a, lane, b, h, blk, row);
+      if (m16 == row) kp = a.new_k + src + 16 * g4;
+      if (4 * g4 + rq == row) vp = a.new_v + src + 16 * a4;
+    }
+#pragma unroll
+    for (int r = 0; r < NR; r++) kd[r] = *reinterpret_cast<const u32x4 *>(kp + 64 * r);
+#pragma unroll
+    for (int r = 0; r < NR; r++) vd[r] = *reinterpret_cast<const u32x4 *>(vp + 64 * r);
+  };
+
+  bf16x8 qcur[NR], qnext[NR];
+  int seg = seq_at(0);
+  mfma_load_q<D>(a, lane, seg, h, qc, qcur);
+  int nxt = next_start(0);
+  if (nxt < n) mfma_load_q<D>(a, lane, seq_at(nxt), h, qc, qnext);
+#pragma unroll
+  for (int s = 0; s < kRing - 1; s++)
+    if (s < n) issue(kb[s], vb[s], s);
+
+  MState<D> st;
+  auto reset = [&]() {
+#pragma unroll
+    for (int s = 0; s < NR; s++) st.O[s][0] = st.O[s][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st.m = -INFINITY;
+    st.l = 0.0f;
+  };
+  auto finish = [&](int b, int first_item) {
+    st.l += __shfl_xor(st.l, 16);
+    st.l += __shfl_xor(st.l, 32);
+    Seg sg;
+    sg.b = b;
+    sg.h = h;
+    sg.qc = qc;
+    const bool single = __builtin_amdgcn_readlane(metav, first_item) & kMetaSingle;
+    mfma_store<D>(a, sg, lane, st, single, (int64_t)(p + b) * a.Hq, 1);
+  };
+  reset();
+  int seg_first = 0;
+  for (int j = 0; j < n; j += kRing) {
+#pragma unroll
+    for (int s = 0; s < kRing; s++) {
+      const int k = j + s;
+      if (k < n) {
+        if (k + kRing - 1 < n) issue(kb[(s + kRing - 1) % kRing], vb[(s + kRing - 1) % kRing], k + kRing - 1);
+        if (k > 0 && ((startmask >> k) & 1)) {  // a new sequence starts at item k
+          finish(seg, seg_first);
+          reset();
+          seg = seq_at(k);
+          seg_first = k;
+#pragma unroll
+          for (int r = 0; r < NR; r++) qcur[r] = qnext[r];
+          nxt = next_start(k);
+          if (nxt < n) mfma_load_q<D>(a, lane, seq_at(nxt), h, qc, qnext);
+        }
+        const int meta = __builtin_amdgcn_readlane(metav, k);
+        mfma_block<D>(kb[s], vb[s], meta & kMetaValid, (badmask >> k) & 1, qcur, a.sl2, lane, st);
+      }
+    }
+  }
+  finish(seg, seg_first);
+}
 
 // One workgroup per (piece, group of <= 4 (KV head, query chunk) waves).
 template <int D, bool BF16, bool MFMA>
@@ -796,6 +939,10 @@ struct Plan {
   void *d_ws = nullptr;
   uint64_t ws_cap = 0;
   uint64_t ws_ml_bytes = 0;   // offset of the o rows inside d_ws
+  int32_t *d_flat_id = nullptr;  // [total] block ids in piece order
+  size_t flat_cap = 0;
+  const int32_t *bound_indptr = nullptr;  // tables flat_id was built from
+  const int32_t *bound_ids = nullptr;
 };
 
 static PlanDev plan_dev(const Plan *pl) {
@@ -804,6 +951,9 @@ static PlanDev plan_dev(const Plan *pl) {
   d.seq_blk0 = d.ctx + pl->B;
   d.piece_seq = d.seq_blk0 + pl->B + 1;
   d.merge_seqs = d.piece_seq + pl->P;
+  d.flat_seq = d.merge_seqs + pl->n_merge;
+  d.flat_meta = d.flat_seq + pl->total;
+  d.flat_id = pl->d_flat_id;
   d.B = pl->B;
   d.P = pl->P;
   d.BP = pl->BP;
@@ -926,6 +1076,7 @@ extern "C" int mkv_decode_plan_destroy(mkv_decode_plan *plan) {
   if (pl->d_meta) (void)hipFree(pl->d_meta);
   if (pl->h_meta) (void)hipHostFree(pl->h_meta);
   if (pl->d_ws) (void)hipFree(pl->d_ws);
+  if (pl->d_flat_id) (void)hipFree(pl->d_flat_id);
   if (pl->uploaded) (void)hipEventDestroy(pl->uploaded);
   delete pl;
   return MKV_OK;
@@ -952,12 +1103,13 @@ extern "C" int mkv_decode_plan_build(mkv_decode_plan *plan, const int32_t *h_ctx
   const int G = g.Hq / g.Hkv;
   const int nqc = (G + kQChunkMfma - 1) / kQChunkMfma;
   int64_t P = pieces ? pieces : std::max<int64_t>(1, 2048 / std::max(1, g.Hkv * nqc));
+  P = std::max<int64_t>(P, (total + 63) / 64);  // a piece is at most 64 blocks (one per lane)
   int64_t BP = std::max<int64_t>(1, (total + P - 1) / P);
   P = (total + BP - 1) / BP;
   DeviceGuard guard(pl->pool->device);
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
   std::vector<int32_t> merge;
-  const size_t n_ints = (size_t)num_seqs + (num_seqs + 1) + P + num_seqs;
+  const size_t n_ints = (size_t)num_seqs + (num_seqs + 1) + P + num_seqs + 2 * (size_t)total;
   // Staging: wait for the previous upload to leave the pinned buffer.
   if (pl->pending) {
     MKV_CHECK_HIP(hipEventSynchronize(pl->uploaded));
@@ -987,7 +1139,17 @@ extern "C" int mkv_decode_plan_build(mkv_decode_plan *plan, const int32_t *h_ctx
   int n_merge = 0;
   for (int32_t b = 0; b < num_seqs; b++)
     if (blk0[b] / BP != (blk0[b + 1] - 1) / BP) mseq[n_merge++] = b;
-  const size_t used = (size_t)num_seqs + (num_seqs + 1) + P + n_merge;
+  int32_t *fseq = mseq + n_merge, *fmeta = fseq + total;
+  for (int32_t b = 0; b < num_seqs; b++) {
+    const int nb = blk0[b + 1] - blk0[b];
+    const int single = blk0[b] / BP == (blk0[b + 1] - 1) / BP ? kMetaSingle : 0;
+    for (int j = 0; j < nb; j++) {
+      const int last = j == nb - 1;
+      fseq[blk0[b] + j] = b;
+      fmeta[blk0[b] + j] = (last ? ctx[b] - kPageSize * j : kPageSize) | (last ? kMetaLast : 0) | single;
+    }
+  }
+  const size_t used = (size_t)num_seqs + (num_seqs + 1) + P + n_merge + 2 * (size_t)total;
   if (pl->meta_cap < used) {
     MKV_CHECK_HIP(hipStreamSynchronize(hs));  // earlier launches may read the old buffer
     if (pl->d_meta) MKV_CHECK_HIP(hipFree(pl->d_meta));
@@ -1009,6 +1171,15 @@ extern "C" int mkv_decode_plan_build(mkv_decode_plan *plan, const int32_t *h_ctx
     pl->ws_cap = need;
   }
   pl->ws_ml_bytes = ml;
+  if (pl->flat_cap < (size_t)total) {
+    MKV_CHECK_HIP(hipStreamSynchronize(hs));
+    if (pl->d_flat_id) MKV_CHECK_HIP(hipFree(pl->d_flat_id));
+    pl->d_flat_id = nullptr;
+    pl->flat_cap = 0;
+    MKV_CHECK_HIP(hipMalloc(reinterpret_cast<void **>(&pl->d_flat_id), (size_t)total * 4));
+    pl->flat_cap = (size_t)total;
+  }
+  pl->bound_indptr = pl->bound_ids = nullptr;  // block ids are re-read at first use
   MKV_CHECK_HIP(hipMemcpyAsync(pl->d_meta, pl->h_meta, used * 4, hipMemcpyHostToDevice, hs));
   MKV_CHECK_HIP(hipEventRecord(pl->uploaded, hs));
   pl->pending = true;
@@ -1054,8 +1225,27 @@ static int launch_planned(Pool *p, const Plan *pl, int32_t layer, const void *d_
   const int hcs = g.Hkv * a.nqc;
   const int wpw = std::min(4, hcs);
   const dim3 grid((unsigned)pl->P, (unsigned)((hcs + wpw - 1) / wpw)), block(64 * wpw);
-  MKV_DISPATCH(attn_planned_kernel, grid, block, hs, a, pd);
-  MKV_CHECK_LAUNCH("attn_planned_kernel");
+  if (use_mfma) {
+    // Block ids in piece order, read once per plan from the tables of its
+    // first call (the tables are fixed for the step the plan describes).
+    Plan *mpl = const_cast<Plan *>(pl);
+    if (mpl->bound_indptr != d_block_indptr || mpl->bound_ids != d_block_ids) {
+      hipLaunchKernelGGL(flatten_ids_kernel, dim3((unsigned)((pl->total + 255) / 256)), dim3(256), 0, hs, pd,
+                         d_block_indptr, d_block_ids, g.nblocks, p->d_err);
+      MKV_CHECK_LAUNCH("flatten_ids_kernel");
+      mpl->bound_indptr = d_block_indptr;
+      mpl->bound_ids = d_block_ids;
+    }
+    switch (g.D) {
+      case 64: hipLaunchKernelGGL(attn_stream_kernel<64>, grid, block, 0, hs, a, pd); break;
+      case 128: hipLaunchKernelGGL(attn_stream_kernel<128>, grid, block, 0, hs, a, pd); break;
+      default: hipLaunchKernelGGL(attn_stream_kernel<256>, grid, block, 0, hs, a, pd); break;
+    }
+    MKV_CHECK_LAUNCH("attn_stream_kernel");
+  } else {
+    MKV_DISPATCH(attn_planned_kernel, grid, block, hs, a, pd);
+    MKV_CHECK_LAUNCH("attn_planned_kernel");
+  }
   if (pl->n_merge) {
     const int64_t mwgs = ((int64_t)pl->n_merge * g.Hq + 3) / 4;
     MKV_DISPATCH_MERGE(merge_planned_kernel, dim3((unsigned)mwgs), dim3(256), hs, a, pd);
