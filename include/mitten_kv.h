@@ -72,7 +72,10 @@ enum {
   MKV_ATTN_ZERO_SINK = 1u << 0,  /* add the reference's phantom zero key/value:
                                     inference-model-qwen/src/model.rs:210-213 */
   MKV_ATTN_FORCE_VALU = 1u << 1, /* use the VALU kernel even where MFMA applies */
-  MKV_ATTN_FORCE_MFMA = 1u << 2  /* fail unless the MFMA kernel applies */
+  MKV_ATTN_FORCE_MFMA = 1u << 2, /* fail unless the MFMA kernel applies */
+  MKV_ATTN_PER_HEAD_LOADS = 1u << 3 /* planned MFMA path: one wave per KV head loads its
+                                       own rows, instead of the workgroup loading whole
+                                       token rows of every head (same results) */
 };
 
 typedef struct mkv_pool mkv_pool;

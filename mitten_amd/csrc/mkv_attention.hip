@@ -49,7 +49,8 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleSlack = 8.0f;  // log2 units: p <= 2^8 between rescales
 constexpr int kQChunkMfma = 16;
 constexpr int kQChunkValu = 8;
-constexpr int kRing = 3;               // MFMA loop: blocks loaded ahead + 1
+constexpr int kRing = 3;       // MFMA loop: blocks loaded ahead + 1
+constexpr int kCoopRing = 3;   // register stages of the cooperative kernel
 
 // Kernel-side geometry and per-call arguments shared by every variant.
 struct KArgs {
@@ -142,8 +143,10 @@ __device__ __forceinline__ void quad_transpose(uint32_t (&x)[4], int lane) {
   }
 }
 
-// Q^T operand of S^T = K.Q^T: lane holds Q[q0 + lane%16][32r + 8*(lane/16) .. +8],
-// zero for rows past the group.
+// Q^T operand of S^T = K.Q^T: lane holds Q[q0 + lane%16][32r + 8*(lane/16) .. +8].
+// Columns past the group repeat its last query; their results are never
+// stored. (No select on the loaded words, so nothing waits for the load
+// before the operand is used.)
 template <int D>
 __device__ __forceinline__ void mfma_load_q(const KArgs &a, int lane, int b, int h, int qc,
                                             bf16x8 (&qop)[D / 32]) {
@@ -153,11 +156,8 @@ __device__ __forceinline__ void mfma_load_q(const KArgs &a, int lane, int b, int
   const uint16_t *qp = reinterpret_cast<const uint16_t *>(a.q) +
                        (int64_t)(b * a.Hq + h * a.G + q0 + min(m16, nq - 1)) * D;
 #pragma unroll
-  for (int r = 0; r < D / 32; r++) {
-    u32x4 w = *reinterpret_cast<const u32x4 *>(qp + 32 * r + 8 * g4);
-    if (m16 >= nq) w = u32x4{0, 0, 0, 0};
-    qop[r] = __builtin_bit_cast(bf16x8, w);
-  }
+  for (int r = 0; r < D / 32; r++)
+    qop[r] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(qp + 32 * r + 8 * g4));
 }
 
 // One 16-token block whose first `nvalid` rows are context: scores, online
@@ -237,11 +237,15 @@ __device__ __forceinline__ void mfma_run(const KArgs &a, const Seg &sg, int lane
   const int64_t v_lane = (int64_t)(4 * g4 + rq) * a.row_bytes + head_off + 16 * a4;  // + 64 s
   const int last_blk = (sg.ctx - 1) / kPageSize, new_row = (sg.ctx - 1) % kPageSize;
   u32x4 kb[kRing][NR], vb[kRing][NR];
+  // Blocks past the stretch load one fixed 256-byte span (an L2 hit), so the
+  // loads are issued unconditionally and the compiler's static wait counts
+  // cover exactly the block about to be used.
   auto issue = [&](u32x4 (&kd)[NR], u32x4 (&vd)[NR], int jj) {
-    const int32_t blk = __builtin_amdgcn_readlane(idv, jj - sg.j0);
-    const uint8_t *kp = a.k_plane + (int64_t)blk * a.block_bytes + k_lane;
-    const uint8_t *vp = a.v_plane + (int64_t)blk * a.block_bytes + v_lane;
-    if (sg.nk && jj == last_blk) {  // the step's new row comes from the input
+    const bool live = jj < sg.j1;
+    const int32_t blk = __builtin_amdgcn_readlane(idv, live ? jj - sg.j0 : 0);
+    const uint8_t *kp = a.k_plane + (live ? (int64_t)blk * a.block_bytes + k_lane : 0);
+    const uint8_t *vp = a.v_plane + (live ? (int64_t)blk * a.block_bytes + v_lane : 0);
+    if (live && sg.nk && jj == last_blk) {  // the step's new row comes from the input
       if (m16 == new_row) kp = sg.nk + 16 * g4;
       if (4 * g4 + rq == new_row) vp = sg.nv + 16 * a4;
     }
@@ -251,14 +255,13 @@ __device__ __forceinline__ void mfma_run(const KArgs &a, const Seg &sg, int lane
     for (int s = 0; s < NR; s++) vd[s] = *reinterpret_cast<const u32x4 *>(vp + 64 * s);
   };
 #pragma unroll
-  for (int s = 0; s < kRing - 1; s++)
-    if (sg.j0 + s < sg.j1) issue(kb[s], vb[s], sg.j0 + s);
+  for (int s = 0; s < kRing - 1; s++) issue(kb[s], vb[s], sg.j0 + s);
   for (int j = sg.j0; j < sg.j1; j += kRing) {
 #pragma unroll
     for (int s = 0; s < kRing; s++) {
       const int jj = j + s;
       if (jj < sg.j1) {
-        if (jj + kRing - 1 < sg.j1) issue(kb[(s + kRing - 1) % kRing], vb[(s + kRing - 1) % kRing], jj + kRing - 1);
+        issue(kb[(s + kRing - 1) % kRing], vb[(s + kRing - 1) % kRing], jj + kRing - 1);
         const bool bad = (badmask >> (jj - sg.j0)) & 1;
         mfma_block<D>(kb[s], vb[s], min(kPageSize, sg.ctx - jj * kPageSize), bad, qop, a.sl2, lane, st);
       }
@@ -649,6 +652,20 @@ __global__ void __launch_bounds__(256) flatten_ids_kernel(PlanDev pd, const int3
   pd.flat_id[f] = id;
 }
 
+// Writes the step's new K/V rows of KV head h for the piece's items that are
+// the last block of their sequence (flattened items in lanes < n).
+template <int D>
+__device__ __forceinline__ void store_new_rows(const KArgs &a, int lane, int h, int32_t idv, int32_t seqv,
+                                               int32_t metav, int n, bool badv) {
+  uint64_t last = __ballot(lane < n && (metav & kMetaLast) && !badv);
+  while (last) {
+    const int k = __builtin_ctzll(last);
+    last &= last - 1;
+    store_new_row<D, 2>(a, lane, __builtin_amdgcn_readlane(seqv, k), h, __builtin_amdgcn_readlane(idv, k),
+                        (__builtin_amdgcn_readlane(metav, k) & kMetaValid) - 1);
+  }
+}
+
 // MFMA attention over one piece as a single block stream: the three-deep
 // load ring runs across sequence boundaries, and the next sequence's Q is
 // loaded while the current one is computed.
@@ -686,16 +703,22 @@ attn_stream_kernel(KArgs a, PlanDev pd) {
   const int64_t k_lane = (int64_t)m16 * a.row_bytes + head_off + 16 * g4;
   const int64_t v_lane = (int64_t)(4 * g4 + rq) * a.row_bytes + head_off + 16 * a4;
   u32x4 kb[kRing][NR], vb[kRing][NR];
+  // Items k >= n (past the piece) load one fixed 256-byte span instead, an
+  // L2 hit: every iteration then issues the same loads with no branch around
+  // them, so the compiler's static wait counts cover exactly the block about
+  // to be used rather than draining the whole ring.
   auto issue = [&](u32x4 (&kd)[NR], u32x4 (&vd)[NR], int k) {
-    const int32_t blk = __builtin_amdgcn_readlane(idv, k);
-    const int meta = __builtin_amdgcn_readlane(metav, k);
-    const uint8_t *kp = a.k_plane + (int64_t)blk * a.block_bytes + k_lane;
-    const uint8_t *vp = a.v_plane + (int64_t)blk * a.block_bytes + v_lane;
-    if (a.new_k && (meta & kMetaLast) && !((badmask >> k) & 1)) {
-      // The sequence's new row: write it into its slot and read it from the input.
+    const bool live = k < n;
+    const int kk = live ? k : n - 1;
+    const int32_t blk = __builtin_amdgcn_readlane(idv, kk);
+    const int meta = __builtin_amdgcn_readlane(metav, kk);
+    const uint8_t *kp = a.k_plane + (live ? (int64_t)blk * a.block_bytes + k_lane : 0);
+    const uint8_t *vp = a.v_plane + (live ? (int64_t)blk * a.block_bytes + v_lane : 0);
+    if (live && a.new_k && (meta & kMetaLast) && !((badmask >> k) & 1)) {
+      // The sequence's new row is read from the input (it is written into
+      // its slot after the loop).
       const int b = seq_at(k), row = (meta & kMetaValid) - 1;
       const int64_t src = ((int64_t)b * a.Hkv + h) * D * 2;
-      if (qc == 0) store_new_row<D, 2>(a, lane, b, h, blk, row);
       if (m16 == row) kp = a.new_k + src + 16 * g4;
       if (4 * g4 + rq == row) vp = a.new_v + src + 16 * a4;
     }
@@ -711,8 +734,7 @@ attn_stream_kernel(KArgs a, PlanDev pd) {
   int nxt = next_start(0);
   if (nxt < n) mfma_load_q<D>(a, lane, seq_at(nxt), h, qc, qnext);
 #pragma unroll
-  for (int s = 0; s < kRing - 1; s++)
-    if (s < n) issue(kb[s], vb[s], s);
+  for (int s = 0; s < kRing - 1; s++) issue(kb[s], vb[s], s);
 
   MState<D> st;
   auto reset = [&]() {
@@ -738,7 +760,7 @@ attn_stream_kernel(KArgs a, PlanDev pd) {
     for (int s = 0; s < kRing; s++) {
       const int k = j + s;
       if (k < n) {
-        if (k + kRing - 1 < n) issue(kb[(s + kRing - 1) % kRing], vb[(s + kRing - 1) % kRing], k + kRing - 1);
+        issue(kb[(s + kRing - 1) % kRing], vb[(s + kRing - 1) % kRing], k + kRing - 1);
         if (k > 0 && ((startmask >> k) & 1)) {  // a new sequence starts at item k
           finish(seg, seg_first);
           reset();
@@ -755,6 +777,7 @@ attn_stream_kernel(KArgs a, PlanDev pd) {
     }
   }
   finish(seg, seg_first);
+  if (a.new_k && qc == 0) store_new_rows<D>(a, lane, h, idv, seqv, metav, n, badv);
 }
 
 // One workgroup per (piece, group of <= 4 (KV head, query chunk) waves).
@@ -801,6 +824,144 @@ __global__ void __launch_bounds__(256) attn_planned_kernel(KArgs a, PlanDev pd) 
     const bool single = sb / pd.BP == (sb + nb - 1) / pd.BP;
     run_segment<D, BF16, MFMA>(a, sg, lane, single, (int64_t)(p + b) * a.Hq, 1);
   }
+}
+
+// Cooperative variant of the stream kernel for workgroups that hold every
+// KV head (num_kv_heads 1, 2 or 4 and <= 16 query heads per KV head):
+// the workgroup reads each block as whole 1 KiB runs (one per wave load
+// instruction, non-temporal), which the memory system serves markedly faster
+// than per-head 64-byte row pieces; the block passes through a
+// double-buffered LDS tile (one barrier per block) from which each wave reads
+// its head's MFMA operands.
+template <int D, int W, int R>
+__global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1)))
+attn_coop_kernel(KArgs a, PlanDev pd) {
+  constexpr int NR = D / 32;
+  constexpr int RB = W * D * 2;          // row bytes (all KV heads)
+  constexpr int BLK = 16 * RB;           // block bytes (K or V)
+  constexpr int CH = BLK / 1024 / W;     // 1 KiB loads per wave per block, K (and V)
+  constexpr int PAD = 16;
+  constexpr int TROW = RB + PAD;         // LDS row stride
+  constexpr int TILE = 16 * TROW;
+  static_assert(BLK % (1024 * W) == 0, "block must split into 1 KiB loads per wave");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2][2][TILE];  // [buffer][K|V]
+  const int lane = threadIdx.x & 63;
+  const int h = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave = KV head
+  const int m16 = lane & 15, g4 = lane >> 4, a4 = m16 >> 2, rq = m16 & 3;
+  const int p = blockIdx.x;
+  const int f0 = p * pd.BP;
+  const int n = min(pd.BP, pd.total_blocks - f0);
+  int32_t idv = -1, seqv = 0, metav = 0;
+  if (lane < n) {
+    idv = pd.flat_id[f0 + lane];
+    seqv = pd.flat_seq[f0 + lane];
+    metav = pd.flat_meta[f0 + lane];
+  }
+  const bool badv = lane < n && (idv < 0 || idv >= a.nblocks);
+  if (badv) idv = 0;
+  const uint64_t badmask = __ballot(badv);
+  const int prev_seq = __shfl_up(seqv, 1);
+  const uint64_t startmask = __ballot(lane < n && (lane == 0 || seqv != prev_seq));
+  auto seq_at = [&](int k) { return __builtin_amdgcn_readlane(seqv, k); };
+  auto next_start = [&](int k) {
+    const uint64_t m = k >= 63 ? 0 : (startmask >> (k + 1)) << (k + 1);
+    return m ? __builtin_ctzll(m) : 64;
+  };
+
+  // Wave h loads bytes [(i*W + h)*1024 + 16*lane, +16) of each block, i < CH.
+  u32x4 kb[R][CH], vb[R][CH];
+  // Items k >= n load block 0's first KiB instead (an L2 hit), so that every
+  // iteration issues the same loads and the compiler's static wait counts
+  // cover exactly the block about to be used.
+  auto issue = [&](u32x4 (&kd)[CH], u32x4 (&vd)[CH], int k) {
+    const bool live = k < n;
+    const int kk = live ? k : n - 1;
+    const int32_t blk = __builtin_amdgcn_readlane(idv, kk);
+    const int meta = __builtin_amdgcn_readlane(metav, kk);
+    const uint8_t *kbase = a.k_plane + (live ? (int64_t)blk * a.block_bytes : 0);
+    const uint8_t *vbase = a.v_plane + (live ? (int64_t)blk * a.block_bytes : 0);
+    const bool fresh = live && a.new_k && (meta & kMetaLast) && !((badmask >> k) & 1);
+    const int b = seq_at(kk), row_new = (meta & kMetaValid) - 1;
+#pragma unroll
+    for (int i = 0; i < CH; i++) {
+      const int off = live ? (i * W + h) * 1024 + 16 * lane : 16 * lane;
+      const uint8_t *kp = kbase + off, *vp = vbase + off;
+      if (fresh && off / RB == row_new) {  // the step's new row comes from the input
+        kp = a.new_k + (int64_t)b * RB + off % RB;
+        vp = a.new_v + (int64_t)b * RB + off % RB;
+      }
+      kd[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(kp));
+      vd[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(vp));
+    }
+  };
+
+  bf16x8 qcur[NR], qnext[NR];
+  int seg = seq_at(0);
+  mfma_load_q<D>(a, lane, seg, h, 0, qcur);
+  int nxt = next_start(0);
+  if (nxt < n) mfma_load_q<D>(a, lane, seq_at(nxt), h, 0, qnext);
+#pragma unroll
+  for (int s = 0; s < R - 1; s++) issue(kb[s], vb[s], s);
+
+  MState<D> st;
+  auto reset = [&]() {
+#pragma unroll
+    for (int s = 0; s < NR; s++) st.O[s][0] = st.O[s][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st.m = -INFINITY;
+    st.l = 0.0f;
+  };
+  auto finish = [&](int b, int first_item) {
+    st.l += __shfl_xor(st.l, 16);
+    st.l += __shfl_xor(st.l, 32);
+    Seg sg;
+    sg.b = b;
+    sg.h = h;
+    sg.qc = 0;
+    const bool single = __builtin_amdgcn_readlane(metav, first_item) & kMetaSingle;
+    mfma_store<D>(a, sg, lane, st, single, (int64_t)(p + b) * a.Hq, 1);
+  };
+  // LDS offsets of this lane's operands: K row m16 / V row 4*g4+rq, head h.
+  const int k_rd = m16 * TROW + h * D * 2 + 16 * g4;
+  const int v_rd = (4 * g4 + rq) * TROW + h * D * 2 + 16 * a4;
+  reset();
+  int seg_first = 0;
+  for (int j = 0; j < n; j += R) {
+#pragma unroll
+    for (int s = 0; s < R; s++) {
+      const int k = j + s;
+      if (k < n) {
+        issue(kb[(s + R - 1) % R], vb[(s + R - 1) % R], k + R - 1);
+        uint8_t *tk = lds[k & 1][0], *tv = lds[k & 1][1];
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+          const int off = (i * W + h) * 1024 + 16 * lane;
+          const int t = (off / RB) * TROW + off % RB;
+          *reinterpret_cast<u32x4 *>(tk + t) = kb[s][i];
+          *reinterpret_cast<u32x4 *>(tv + t) = vb[s][i];
+        }
+        __syncthreads();
+        if (k > 0 && ((startmask >> k) & 1)) {
+          finish(seg, seg_first);
+          reset();
+          seg = seq_at(k);
+          seg_first = k;
+#pragma unroll
+          for (int r = 0; r < NR; r++) qcur[r] = qnext[r];
+          nxt = next_start(k);
+          if (nxt < n) mfma_load_q<D>(a, lane, seq_at(nxt), h, 0, qnext);
+        }
+        u32x4 kq[NR], vq[NR];
+#pragma unroll
+        for (int r = 0; r < NR; r++) kq[r] = *reinterpret_cast<const u32x4 *>(tk + k_rd + 64 * r);
+#pragma unroll
+        for (int r = 0; r < NR; r++) vq[r] = *reinterpret_cast<const u32x4 *>(tv + v_rd + 64 * r);
+        const int meta = __builtin_amdgcn_readlane(metav, k);
+        mfma_block<D>(kq, vq, meta & kMetaValid, (badmask >> k) & 1, qcur, a.sl2, lane, st);
+      }
+    }
+  }
+  finish(seg, seg_first);
+  if (a.new_k) store_new_rows<D>(a, lane, h, idv, seqv, metav, n, badv);
 }
 
 // One wave per (sequence cut by piece boundaries, query head).
@@ -1236,12 +1397,31 @@ static int launch_planned(Pool *p, const Plan *pl, int32_t layer, const void *d_
       mpl->bound_indptr = d_block_indptr;
       mpl->bound_ids = d_block_ids;
     }
-    switch (g.D) {
-      case 64: hipLaunchKernelGGL(attn_stream_kernel<64>, grid, block, 0, hs, a, pd); break;
-      case 128: hipLaunchKernelGGL(attn_stream_kernel<128>, grid, block, 0, hs, a, pd); break;
-      default: hipLaunchKernelGGL(attn_stream_kernel<256>, grid, block, 0, hs, a, pd); break;
+    const bool coop = a.nqc == 1 && (g.Hkv == 1 || g.Hkv == 2 || g.Hkv == 4) &&
+                      !(flags & MKV_ATTN_PER_HEAD_LOADS);
+    if (coop) {
+      const dim3 cgrid((unsigned)pl->P), cblock(64 * g.Hkv);
+#define MKV_COOP(DD)                                                                              \
+  do {                                                                                            \
+    if (g.Hkv == 1) hipLaunchKernelGGL((attn_coop_kernel<DD, 1, kCoopRing>), cgrid, cblock, 0, hs, a, pd);    \
+    else if (g.Hkv == 2) hipLaunchKernelGGL((attn_coop_kernel<DD, 2, kCoopRing>), cgrid, cblock, 0, hs, a, pd); \
+    else hipLaunchKernelGGL((attn_coop_kernel<DD, 4, kCoopRing>), cgrid, cblock, 0, hs, a, pd);               \
+  } while (0)
+      switch (g.D) {
+        case 64: MKV_COOP(64); break;
+        case 128: MKV_COOP(128); break;
+        default: MKV_COOP(256); break;
+      }
+#undef MKV_COOP
+      MKV_CHECK_LAUNCH("attn_coop_kernel");
+    } else {
+      switch (g.D) {
+        case 64: hipLaunchKernelGGL(attn_stream_kernel<64>, grid, block, 0, hs, a, pd); break;
+        case 128: hipLaunchKernelGGL(attn_stream_kernel<128>, grid, block, 0, hs, a, pd); break;
+        default: hipLaunchKernelGGL(attn_stream_kernel<256>, grid, block, 0, hs, a, pd); break;
+      }
+      MKV_CHECK_LAUNCH("attn_stream_kernel");
     }
-    MKV_CHECK_LAUNCH("attn_stream_kernel");
   } else {
     MKV_DISPATCH(attn_planned_kernel, grid, block, hs, a, pd);
     MKV_CHECK_LAUNCH("attn_planned_kernel");

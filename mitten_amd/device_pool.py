@@ -35,7 +35,7 @@ MKV_ERR_NO_DEVICE = 5
 
 DEVERR_SLOT, DEVERR_BLOCK, DEVERR_TABLE, DEVERR_COPY, DEVERR_CTX = 1, 2, 4, 8, 16
 
-ATTN_ZERO_SINK, ATTN_FORCE_VALU, ATTN_FORCE_MFMA = 1, 2, 4
+ATTN_ZERO_SINK, ATTN_FORCE_VALU, ATTN_FORCE_MFMA, ATTN_PER_HEAD_LOADS = 1, 2, 4, 8
 
 DTYPES = {"f32": 0, "bf16": 1}
 PAGE_SIZE = 16
@@ -339,6 +339,8 @@ class DeviceKvPool:
             flags |= ATTN_FORCE_VALU
         elif kernel == "mfma":
             flags |= ATTN_FORCE_MFMA
+        elif kernel == "mfma-per-head":
+            flags |= ATTN_FORCE_MFMA | ATTN_PER_HEAD_LOADS
         elif kernel is not None:
             raise ValueError(f"unknown kernel {kernel!r}")
         return out, scale, flags

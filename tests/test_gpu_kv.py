@@ -19,6 +19,8 @@ SHAPES = {
     "qwen0.5b-f32": (3, 14, 2, 64, "f32"),
     "qwen7b-bf16": (2, 28, 4, 128, "bf16"),
     "gemma2b-bf16": (2, 8, 1, 256, "bf16"),
+    "qwen0.5b-bf16": (2, 14, 2, 64, "bf16"),
+    "llama8b-bf16": (1, 32, 8, 128, "bf16"),
 }
 
 
@@ -286,9 +288,16 @@ def _planned_case(shape, ctx, seed, pieces=0, kernel=None, zero_sink=False, fuse
 PLAN_CTX = [1, 2, 15, 16, 17, 33, 100, 129, 257, 500, 1000, 3, 64, 65, 700]
 
 
+# Planned-path kernels: "mfma" takes the cooperative whole-row loader where
+# the workgroup holds every KV head (Hkv <= 4, G <= 16) and the per-head
+# stream kernel otherwise (llama8b: Hkv = 8); "mfma-per-head" forces the latter.
+PLANNED_KERNELS = [("qwen0.5b-f32", None), ("qwen7b-bf16", "mfma"), ("qwen7b-bf16", "mfma-per-head"),
+                   ("qwen7b-bf16", "valu"), ("gemma2b-bf16", "mfma"), ("gemma2b-bf16", "mfma-per-head"),
+                   ("qwen0.5b-bf16", "mfma"), ("llama8b-bf16", "mfma")]
+
+
 @pytest.mark.parametrize("pieces", [0, 1, 7, 40, 300])
-@pytest.mark.parametrize("shape,kernel", [("qwen0.5b-f32", None), ("qwen7b-bf16", "mfma"),
-                                          ("qwen7b-bf16", "valu"), ("gemma2b-bf16", "mfma")])
+@pytest.mark.parametrize("shape,kernel", PLANNED_KERNELS)
 def test_planned_attention(shape, kernel, pieces):
     got, ref, dt, after, want, info = _planned_case(shape, PLAN_CTX, 60, pieces=pieces, kernel=kernel)
     assert_attention_close(got, ref, dt)
@@ -296,12 +305,38 @@ def test_planned_attention(shape, kernel, pieces):
 
 
 @pytest.mark.parametrize("pieces", [0, 5, 64])
-@pytest.mark.parametrize("shape,kernel", [("qwen0.5b-f32", None), ("qwen7b-bf16", "mfma"),
-                                          ("qwen7b-bf16", "valu"), ("gemma2b-bf16", "mfma")])
+@pytest.mark.parametrize("shape,kernel", PLANNED_KERNELS)
 def test_decode_step_fused_append(shape, kernel, pieces):
     got, ref, dt, after, want, info = _planned_case(shape, PLAN_CTX, 61, pieces=pieces, kernel=kernel, fused=True)
     assert np.array_equal(bits(after), bits(want)), "fused append is not bit-exact"
     assert_attention_close(got, ref, dt)
+
+
+@pytest.mark.parametrize("kernel", ["mfma", "mfma-per-head", "valu"])
+def test_planned_bad_block_id_reported(kernel):
+    """An id outside the pool is reported and its block skipped; the other
+    sequence of the batch is unaffected and nothing is written for it."""
+    desc = PoolDesc(1, 4, 28, 128, 10, "bf16")
+    host = normal(80, desc.shape, "bf16")
+    q = normal(81, (2, 28, 128), "bf16")
+    kn, vn = normal(82, (2, 4, 128), "bf16"), normal(83, (2, 4, 128), "bf16")
+    with DeviceKvPool(desc) as pool:
+        pool.write(host)
+        plan = pool.plan([20, 30])
+        o = pool.decode_step(0, plan, to_device(kn), to_device(vn), to_device(q), _i32([0, 2, 4]),
+                             _i32([1, 2, 3, 10]), kernel=kernel)
+        with pytest.raises(DeviceIndexError) as ei:
+            pool.check()
+        assert ei.value.bits & dp.DEVERR_BLOCK
+        got = to_host(o)
+        after = pool.read()
+        plan.close()
+    want = host.copy()
+    assert orc.append(odesc(desc), want, 0, kn[:1], vn[:1], np.array([2 * 16 + 3], np.int32)) == -1
+    assert np.array_equal(bits(after), bits(want))
+    ref = orc.decode_attention(odesc(desc), want, 0, widen(q[:1]), np.array([0, 2], np.int32),
+                               np.array([1, 2], np.int32), np.array([20], np.int32))
+    assert_attention_close(got[:1], ref, "bf16")
 
 
 @pytest.mark.parametrize("shape", ["qwen0.5b-f32", "qwen7b-bf16"])
