@@ -50,7 +50,8 @@ constexpr float kRescaleSlack = 8.0f;  // log2 units: p <= 2^8 between rescales
 constexpr int kQChunkMfma = 16;
 constexpr int kQChunkValu = 8;
 constexpr int kRing = 3;       // MFMA loop: blocks loaded ahead + 1
-constexpr int kCoopRing = 3;   // register stages of the cooperative kernel
+constexpr int kCoopRing = 3;   // register stages of the cooperative kernel (one less when
+                               // its slots carry four Q loads per lane)
 
 // Kernel-side geometry and per-call arguments shared by every variant.
 struct KArgs {
@@ -101,6 +102,12 @@ __device__ __forceinline__ void store_new_row(const KArgs &a, int lane, int b, i
     const u32x4 w = *reinterpret_cast<const u32x4 *>((kv ? a.new_v : a.new_k) + src + 16 * cc);
     *reinterpret_cast<u32x4 *>((kv ? a.v_plane_w : a.k_plane_w) + dst + 16 * cc) = w;
   }
+}
+
+// Byte offset of the block that this workgroup's spare ring loads (past the
+// end of its work) read: spreads them over the pool instead of one hot line.
+__device__ __forceinline__ int64_t dummy_offset(const KArgs &a) {
+  return (int64_t)(blockIdx.x % (uint32_t)min<int64_t>(a.nblocks, 1 << 30)) * a.block_bytes;
 }
 
 // One (sequence, KV head, query chunk) stretch of blocks [j0, j1) of a
@@ -237,14 +244,16 @@ __device__ __forceinline__ void mfma_run(const KArgs &a, const Seg &sg, int lane
   const int64_t v_lane = (int64_t)(4 * g4 + rq) * a.row_bytes + head_off + 16 * a4;  // + 64 s
   const int last_blk = (sg.ctx - 1) / kPageSize, new_row = (sg.ctx - 1) % kPageSize;
   u32x4 kb[kRing][NR], vb[kRing][NR];
-  // Blocks past the stretch load one fixed 256-byte span (an L2 hit), so the
-  // loads are issued unconditionally and the compiler's static wait counts
-  // cover exactly the block about to be used.
+  // Blocks past the stretch load the first 128 bytes of a block picked by the
+  // workgroup index instead (so workgroups do not all hit the same lines):
+  // the loads are issued unconditionally and the compiler's static wait
+  // counts cover exactly the block about to be used.
+  const int64_t spare = dummy_offset(a) + 16 * (lane & 7);
   auto issue = [&](u32x4 (&kd)[NR], u32x4 (&vd)[NR], int jj) {
     const bool live = jj < sg.j1;
     const int32_t blk = __builtin_amdgcn_readlane(idv, live ? jj - sg.j0 : 0);
-    const uint8_t *kp = a.k_plane + (live ? (int64_t)blk * a.block_bytes + k_lane : 0);
-    const uint8_t *vp = a.v_plane + (live ? (int64_t)blk * a.block_bytes + v_lane : 0);
+    const uint8_t *kp = a.k_plane + (live ? (int64_t)blk * a.block_bytes + k_lane : spare);
+    const uint8_t *vp = a.v_plane + (live ? (int64_t)blk * a.block_bytes + v_lane : spare);
     if (live && sg.nk && jj == last_blk) {  // the step's new row comes from the input
       if (m16 == new_row) kp = sg.nk + 16 * g4;
       if (4 * g4 + rq == new_row) vp = sg.nv + 16 * a4;
@@ -703,17 +712,18 @@ attn_stream_kernel(KArgs a, PlanDev pd) {
   const int64_t k_lane = (int64_t)m16 * a.row_bytes + head_off + 16 * g4;
   const int64_t v_lane = (int64_t)(4 * g4 + rq) * a.row_bytes + head_off + 16 * a4;
   u32x4 kb[kRing][NR], vb[kRing][NR];
-  // Items k >= n (past the piece) load one fixed 256-byte span instead, an
-  // L2 hit: every iteration then issues the same loads with no branch around
-  // them, so the compiler's static wait counts cover exactly the block about
-  // to be used rather than draining the whole ring.
+  // Items k >= n (past the piece) load the first 128 bytes of a block picked
+  // by the workgroup index instead: every iteration then issues the same loads
+  // with no branch around them, so the compiler's static wait counts cover
+  // exactly the block about to be used rather than draining the whole ring.
+  const int64_t spare = dummy_offset(a) + 16 * (lane & 7);
   auto issue = [&](u32x4 (&kd)[NR], u32x4 (&vd)[NR], int k) {
     const bool live = k < n;
     const int kk = live ? k : n - 1;
     const int32_t blk = __builtin_amdgcn_readlane(idv, kk);
     const int meta = __builtin_amdgcn_readlane(metav, kk);
-    const uint8_t *kp = a.k_plane + (live ? (int64_t)blk * a.block_bytes + k_lane : 0);
-    const uint8_t *vp = a.v_plane + (live ? (int64_t)blk * a.block_bytes + v_lane : 0);
+    const uint8_t *kp = a.k_plane + (live ? (int64_t)blk * a.block_bytes + k_lane : spare);
+    const uint8_t *vp = a.v_plane + (live ? (int64_t)blk * a.block_bytes + v_lane : spare);
     if (live && a.new_k && (meta & kMetaLast) && !((badmask >> k) & 1)) {
       // The sequence's new row is read from the input (it is written into
       // its slot after the loop).
@@ -755,27 +765,33 @@ attn_stream_kernel(KArgs a, PlanDev pd) {
   };
   reset();
   int seg_first = 0;
-  for (int j = 0; j < n; j += kRing) {
+  auto stage = [&](int s, int k) {
+    issue(kb[(s + kRing - 1) % kRing], vb[(s + kRing - 1) % kRing], k + kRing - 1);
+    if (k > 0 && ((startmask >> k) & 1)) {  // a new sequence starts at item k
+      finish(seg, seg_first);
+      reset();
+      seg = seq_at(k);
+      seg_first = k;
 #pragma unroll
-    for (int s = 0; s < kRing; s++) {
-      const int k = j + s;
-      if (k < n) {
-        issue(kb[(s + kRing - 1) % kRing], vb[(s + kRing - 1) % kRing], k + kRing - 1);
-        if (k > 0 && ((startmask >> k) & 1)) {  // a new sequence starts at item k
-          finish(seg, seg_first);
-          reset();
-          seg = seq_at(k);
-          seg_first = k;
-#pragma unroll
-          for (int r = 0; r < NR; r++) qcur[r] = qnext[r];
-          nxt = next_start(k);
-          if (nxt < n) mfma_load_q<D>(a, lane, seq_at(nxt), h, qc, qnext);
-        }
-        const int meta = __builtin_amdgcn_readlane(metav, k);
-        mfma_block<D>(kb[s], vb[s], meta & kMetaValid, (badmask >> k) & 1, qcur, a.sl2, lane, st);
-      }
+      for (int r = 0; r < NR; r++) qcur[r] = qnext[r];
+      nxt = next_start(k);
+      if (nxt < n) mfma_load_q<D>(a, lane, seq_at(nxt), h, qc, qnext);
     }
+    const int meta = __builtin_amdgcn_readlane(metav, k);
+    mfma_block<D>(kb[s], vb[s], meta & kMetaValid, (badmask >> k) & 1, qcur, a.sl2, lane, st);
+  };
+  // No branch around any stage of the main loop (a path that skipped one
+  // would make the compiler's wait counts drain the ring); the last
+  // n mod kRing items run after it.
+  const int nfull = n / kRing;
+  int k0 = 0;
+  for (int it = 0; it < nfull; it++, k0 += kRing) {
+#pragma unroll
+    for (int s = 0; s < kRing; s++) stage(s, k0 + s);
   }
+#pragma unroll
+  for (int s = 0; s < kRing - 1; s++)
+    if (k0 + s < n) stage(s, k0 + s);
   finish(seg, seg_first);
   if (a.new_k && qc == 0) store_new_rows<D>(a, lane, h, idv, seqv, metav, n, badv);
 }
@@ -826,31 +842,146 @@ __global__ void __launch_bounds__(256) attn_planned_kernel(KArgs a, PlanDev pd) 
   }
 }
 
+// ---- LDS-fed MFMA block (cooperative kernel) -------------------------------
+//
+// Same online-softmax step as mfma_block, but V^T comes straight from the
+// LDS tile through ds_read_tr16_b64 (gfx950 transpose read): within each group
+// of 16 lanes, lane i receives element (i mod 4) of the 8 bytes read by lane
+// 4j + i/4, for j = 0..3. Lane 4j + q of group g reads token row 4g + j at
+// dims 16n + 4q .. +3, so lane i of group g receives V[4g + j][16n + i] for
+// j = 0..3: the A operand of O^T[16n..+16][q] += V^T . P^T. O^T tile n holds
+// O[q = lane%16][16n + 4*(lane/16) + i] in O[n][i].
+template <int D>
+struct MStateT {
+  f32x4 O[D / 16];
+  float m, l;
+};
+
+typedef short i16x4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4s lds_i16x4;
+
+template <int D>
+__device__ __forceinline__ void mfma_block_t(const u32x4 (&kq)[D / 32], const uint8_t *tv,
+                                             const int (&v_rd)[D / 16], int nvalid, bool bad,
+                                             const bf16x8 (&qop)[D / 32], float sl2, int lane,
+                                             MStateT<D> &st) {
+  constexpr int NR = D / 32, NT = D / 16;
+  const int g4 = lane >> 4;
+  f32x4 S = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+    S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kq[r]), qop[r], S, 0, 0, 0);
+  // Lane holds S[token 4*g4 + i][q = lane%16]. Only a sequence's last block
+  // (or a rejected one) has rows past the context.
+  const bool partial = bad || nvalid < kPageSize;
+  float x[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) x[i] = S[i] * sl2;
+  if (partial) {
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      if (bad || 4 * g4 + i >= nvalid) x[i] = -INFINITY;
+  }
+  float mloc = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+  mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+  mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+  const bool need = mloc > st.m + kRescaleSlack;
+  if (__ballot(need)) {
+    const float mn = need ? mloc : st.m;
+    const float al = fast_exp2(st.m - mn);
+    st.l *= al;
+#pragma unroll
+    for (int n = 0; n < NT; n++) st.O[n] *= al;
+    st.m = mn;
+  }
+  float p[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) p[i] = fast_exp2(x[i] - st.m);
+  st.l += (p[0] + p[1]) + (p[2] + p[3]);
+  const uint32_t p01 = pack_bf16x2(p[0], p[1]), p23 = pack_bf16x2(p[2], p[3]);
+  const i16x4 pb = __builtin_bit_cast(i16x4, (uint64_t)p01 | ((uint64_t)p23 << 32));
+  // V rows past the context (or of a rejected block) are zeroed: stale slots
+  // may hold any bit pattern, and 0 * NaN would poison the sum.
+  uint32_t vm0 = ~0u, vm1 = ~0u;
+  if (partial) {
+    const int t0 = 4 * g4;
+    vm0 = (bad || t0 >= nvalid ? 0u : 0xffffu) | (bad || t0 + 1 >= nvalid ? 0u : 0xffff0000u);
+    vm1 = (bad || t0 + 2 >= nvalid ? 0u : 0xffffu) | (bad || t0 + 3 >= nvalid ? 0u : 0xffff0000u);
+  }
+#pragma unroll
+  for (int n = 0; n < NT; n++) {
+    const i16x4s raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(tv + v_rd[n]));
+    uint64_t w = __builtin_bit_cast(uint64_t, raw);
+    if (partial) w &= (uint64_t)vm0 | ((uint64_t)vm1 << 32);
+    st.O[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, w), pb, st.O[n], 0, 0, 0);
+  }
+}
+
+// Stores one (sequence, KV head) result of the LDS-fed path: the final bf16
+// rows, or f32 partial rows plus (m, l) for the split-K merge.
+template <int D>
+__device__ __forceinline__ void mfma_store_t(const KArgs &a, int b, int h, int lane, const MStateT<D> &st,
+                                             bool final, int64_t prow_base) {
+  const int m16 = lane & 15, g4 = lane >> 4;
+  if (m16 >= min(kQChunkMfma, a.G)) return;
+  const int hq = h * a.G + m16;
+  if (final) {
+    const float f = final_scale(st.m, st.l, a.zero_sink);
+    uint16_t *op = reinterpret_cast<uint16_t *>(a.o) + (int64_t)(b * a.Hq + hq) * D + 4 * g4;
+#pragma unroll
+    for (int n = 0; n < D / 16; n++) {
+      const uint2 w = make_uint2(pack_bf16x2(st.O[n][0] * f, st.O[n][1] * f),
+                                 pack_bf16x2(st.O[n][2] * f, st.O[n][3] * f));
+      *reinterpret_cast<uint2 *>(op + 16 * n) = w;
+    }
+  } else {
+    const int64_t prow = prow_base + hq;
+    float *wo = a.ws_o + prow * D + 4 * g4;
+#pragma unroll
+    for (int n = 0; n < D / 16; n++) *reinterpret_cast<f32x4 *>(wo + 16 * n) = st.O[n];
+    if (g4 == 0) *reinterpret_cast<float2 *>(a.ws_ml + 2 * prow) = make_float2(st.m, st.l);
+  }
+}
+
 // Cooperative variant of the stream kernel for workgroups that hold every
-// KV head (num_kv_heads 1, 2 or 4 and <= 16 query heads per KV head):
-// the workgroup reads each block as whole 1 KiB runs (one per wave load
-// instruction, non-temporal), which the memory system serves markedly faster
-// than per-head 64-byte row pieces; the block passes through a
-// double-buffered LDS tile (one barrier per block) from which each wave reads
-// its head's MFMA operands.
-template <int D, int W, int R>
+// KV head (num_kv_heads 1, 2 or 4 and at most 16 query heads per KV head).
+// The workgroup reads each block as whole token rows of all heads, every
+// wave load instruction one contiguous KiB (non-temporal), which the memory
+// system serves faster than per-head 64-byte row pieces. A block passes
+// through a double-buffered LDS tile (one barrier per block); each wave then
+// reads its head's MFMA operands from it. The Q rows of a sequence ride in
+// the same load ring as its first block in the piece and are kept in LDS, so
+// nothing waits for them at a sequence boundary.
+//
+// LDS layout: tile rows of RB = W*D*2 bytes with 16-byte chunk c of row r
+// stored at chunk c ^ swz(r) (swz permutes the row's low four chunk bits), so
+// the K reads (16 rows, one chunk each) and V reads (4 rows x 4 chunks) of a
+// 16-lane group hit distinct banks. Q rows (D*2 bytes, [Hq][D] order) use
+// chunk c ^ (row mod chunks-per-row).
+__device__ __forceinline__ int tile_swz(int row, int cpr) {
+  return (((row & 3) << 2) | ((row >> 2) & 3)) & (cpr - 1);
+}
+
+template <int D, int W, int QL, int R>
 __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1)))
 attn_coop_kernel(KArgs a, PlanDev pd) {
   constexpr int NR = D / 32;
-  constexpr int RB = W * D * 2;          // row bytes (all KV heads)
-  constexpr int BLK = 16 * RB;           // block bytes (K or V)
+  constexpr int RB = W * D * 2;          // tile row bytes (all KV heads)
+  constexpr int CPR = RB / 16;           // 16-byte chunks per tile row
+  constexpr int BLK = 16 * RB;           // K (or V) bytes of one block
   constexpr int CH = BLK / 1024 / W;     // 1 KiB loads per wave per block, K (and V)
-  constexpr int PAD = 16;
-  constexpr int TROW = RB + PAD;         // LDS row stride
-  constexpr int TILE = 16 * TROW;
+  constexpr int CPQ = D / 8;             // 16-byte chunks per Q row
+  constexpr int QCAP = QL * 64 * W * 16; // Q bytes the ring slots can carry
   static_assert(BLK % (1024 * W) == 0, "block must split into 1 KiB loads per wave");
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2][2][TILE];  // [buffer][K|V]
+  __shared__ __attribute__((aligned(16))) uint8_t tiles[2][2][BLK];  // [buffer][K|V]
+  __shared__ __attribute__((aligned(16))) uint8_t qtile[QCAP];
   const int lane = threadIdx.x & 63;
   const int h = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave = KV head
   const int m16 = lane & 15, g4 = lane >> 4, a4 = m16 >> 2, rq = m16 & 3;
   const int p = blockIdx.x;
   const int f0 = p * pd.BP;
   const int n = min(pd.BP, pd.total_blocks - f0);
+  const int qchunks = a.Hq * CPQ;        // Q chunks of one sequence (<= QCAP / 16)
   int32_t idv = -1, seqv = 0, metav = 0;
   if (lane < n) {
     idv = pd.flat_id[f0 + lane];
@@ -863,28 +994,28 @@ attn_coop_kernel(KArgs a, PlanDev pd) {
   const int prev_seq = __shfl_up(seqv, 1);
   const uint64_t startmask = __ballot(lane < n && (lane == 0 || seqv != prev_seq));
   auto seq_at = [&](int k) { return __builtin_amdgcn_readlane(seqv, k); };
-  auto next_start = [&](int k) {
-    const uint64_t m = k >= 63 ? 0 : (startmask >> (k + 1)) << (k + 1);
-    return m ? __builtin_ctzll(m) : 64;
-  };
 
-  // Wave h loads bytes [(i*W + h)*1024 + 16*lane, +16) of each block, i < CH.
-  u32x4 kb[R][CH], vb[R][CH];
-  // Items k >= n load block 0's first KiB instead (an L2 hit), so that every
-  // iteration issues the same loads and the compiler's static wait counts
-  // cover exactly the block about to be used.
-  auto issue = [&](u32x4 (&kd)[CH], u32x4 (&vd)[CH], int k) {
+  // Ring slot: wave h holds bytes [(i*W + h)*1024 + 16*lane, +16) of the
+  // block's K and V (i < CH), and Q chunks (i*W + h)*64 + lane (i < QL) of the
+  // sequence when the item starts one. Items k >= n load the first 128 bytes
+  // of a block picked by the workgroup index instead (so workgroups do not all
+  // hit the same lines), and Q of items that start no sequence a fixed span:
+  // every iteration issues the same loads, so the compiler's static wait
+  // counts cover exactly the block about to be used.
+  u32x4 kb[R][CH], vb[R][CH], qb[R][QL];
+  const int64_t spare = dummy_offset(a);
+  auto issue = [&](u32x4 (&kd)[CH], u32x4 (&vd)[CH], u32x4 (&qd)[QL], int k) {
     const bool live = k < n;
     const int kk = live ? k : n - 1;
     const int32_t blk = __builtin_amdgcn_readlane(idv, kk);
     const int meta = __builtin_amdgcn_readlane(metav, kk);
-    const uint8_t *kbase = a.k_plane + (live ? (int64_t)blk * a.block_bytes : 0);
-    const uint8_t *vbase = a.v_plane + (live ? (int64_t)blk * a.block_bytes : 0);
+    const uint8_t *kbase = a.k_plane + (live ? (int64_t)blk * a.block_bytes : spare);
+    const uint8_t *vbase = a.v_plane + (live ? (int64_t)blk * a.block_bytes : spare);
     const bool fresh = live && a.new_k && (meta & kMetaLast) && !((badmask >> k) & 1);
     const int b = seq_at(kk), row_new = (meta & kMetaValid) - 1;
 #pragma unroll
     for (int i = 0; i < CH; i++) {
-      const int off = live ? (i * W + h) * 1024 + 16 * lane : 16 * lane;
+      const int off = live ? (i * W + h) * 1024 + 16 * lane : 16 * (lane & 7);
       const uint8_t *kp = kbase + off, *vp = vbase + off;
       if (fresh && off / RB == row_new) {  // the step's new row comes from the input
         kp = a.new_k + (int64_t)b * RB + off % RB;
@@ -893,78 +1024,107 @@ attn_coop_kernel(KArgs a, PlanDev pd) {
       kd[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(kp));
       vd[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(vp));
     }
+    const bool qload = live && ((startmask >> k) & 1);
+    const uint8_t *qbase = static_cast<const uint8_t *>(a.q) + (qload ? (int64_t)b * a.Hq * D * 2 : 0);
+#pragma unroll
+    for (int i = 0; i < QL; i++) {
+      const int c = (i * W + h) * 64 + lane;
+      // (The fallback offset stays lane-varying: a uniform one invites the
+      // compiler to branch around the load, which costs a full wait.)
+      qd[i] = *reinterpret_cast<const u32x4 *>(qbase + 16 * (qload ? min(c, qchunks - 1) : (lane & 7)));
+    }
   };
 
-  bf16x8 qcur[NR], qnext[NR];
-  int seg = seq_at(0);
-  mfma_load_q<D>(a, lane, seg, h, 0, qcur);
-  int nxt = next_start(0);
-  if (nxt < n) mfma_load_q<D>(a, lane, seq_at(nxt), h, 0, qnext);
-#pragma unroll
-  for (int s = 0; s < R - 1; s++) issue(kb[s], vb[s], s);
-
-  MState<D> st;
+  MStateT<D> st;
   auto reset = [&]() {
 #pragma unroll
-    for (int s = 0; s < NR; s++) st.O[s][0] = st.O[s][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int n = 0; n < D / 16; n++) st.O[n] = f32x4{0.f, 0.f, 0.f, 0.f};
     st.m = -INFINITY;
     st.l = 0.0f;
   };
   auto finish = [&](int b, int first_item) {
     st.l += __shfl_xor(st.l, 16);
     st.l += __shfl_xor(st.l, 32);
-    Seg sg;
-    sg.b = b;
-    sg.h = h;
-    sg.qc = 0;
     const bool single = __builtin_amdgcn_readlane(metav, first_item) & kMetaSingle;
-    mfma_store<D>(a, sg, lane, st, single, (int64_t)(p + b) * a.Hq, 1);
+    mfma_store_t<D>(a, b, h, lane, st, single, (int64_t)(p + b) * a.Hq);
   };
-  // LDS offsets of this lane's operands: K row m16 / V row 4*g4+rq, head h.
-  const int k_rd = m16 * TROW + h * D * 2 + 16 * g4;
-  const int v_rd = (4 * g4 + rq) * TROW + h * D * 2 + 16 * a4;
-  reset();
-  int seg_first = 0;
-  for (int j = 0; j < n; j += R) {
+  // LDS byte offsets of this lane's operands: K (16 B, r < NR), V^T
+  // transpose reads (8 B, tile n < D/16: token row 4*g4 + (lane%16)/4, dims
+  // 16n + 4*(lane%4)), Q (16 B, r < NR).
+  int k_rd[NR], v_rd[D / 16], q_rd[NR];
+  const int qrow = h * a.G + min(m16, a.G - 1);
+  const int vrow = 4 * g4 + a4, vq4 = rq;
 #pragma unroll
-    for (int s = 0; s < R; s++) {
-      const int k = j + s;
-      if (k < n) {
-        issue(kb[(s + R - 1) % R], vb[(s + R - 1) % R], k + R - 1);
-        uint8_t *tk = lds[k & 1][0], *tv = lds[k & 1][1];
-#pragma unroll
-        for (int i = 0; i < CH; i++) {
-          const int off = (i * W + h) * 1024 + 16 * lane;
-          const int t = (off / RB) * TROW + off % RB;
-          *reinterpret_cast<u32x4 *>(tk + t) = kb[s][i];
-          *reinterpret_cast<u32x4 *>(tv + t) = vb[s][i];
-        }
-        __syncthreads();
-        if (k > 0 && ((startmask >> k) & 1)) {
-          finish(seg, seg_first);
-          reset();
-          seg = seq_at(k);
-          seg_first = k;
-#pragma unroll
-          for (int r = 0; r < NR; r++) qcur[r] = qnext[r];
-          nxt = next_start(k);
-          if (nxt < n) mfma_load_q<D>(a, lane, seq_at(nxt), h, 0, qnext);
-        }
-        u32x4 kq[NR], vq[NR];
-#pragma unroll
-        for (int r = 0; r < NR; r++) kq[r] = *reinterpret_cast<const u32x4 *>(tk + k_rd + 64 * r);
-#pragma unroll
-        for (int r = 0; r < NR; r++) vq[r] = *reinterpret_cast<const u32x4 *>(tv + v_rd + 64 * r);
-        const int meta = __builtin_amdgcn_readlane(metav, k);
-        mfma_block<D>(kq, vq, meta & kMetaValid, (badmask >> k) & 1, qcur, a.sl2, lane, st);
-      }
-    }
+  for (int r = 0; r < NR; r++) {
+    k_rd[r] = m16 * RB + (((h * D / 8 + g4 + 4 * r) ^ tile_swz(m16, CPR)) << 4);
+    q_rd[r] = qrow * D * 2 + (((4 * r + g4) ^ (qrow & (CPQ - 1))) << 4);
   }
+#pragma unroll
+  for (int n = 0; n < D / 16; n++)
+    v_rd[n] = vrow * RB + (((h * D / 8 + 2 * n + (vq4 >> 1)) ^ tile_swz(vrow, CPR)) << 4) + 8 * (vq4 & 1);
+  bf16x8 qop[NR];
+
+#pragma unroll
+  for (int s = 0; s < R - 1; s++) issue(kb[s], vb[s], qb[s], s);
+  reset();
+  int seg = seq_at(0), seg_first = 0;
+  // One item: load item k + R - 1 into the slot freed last, stage slot s
+  // (item k) in LDS, compute.
+  auto stage = [&](int s, int k) {
+    issue(kb[(s + R - 1) % R], vb[(s + R - 1) % R], qb[(s + R - 1) % R], k + R - 1);
+    uint8_t *tk = tiles[k & 1][0], *tv = tiles[k & 1][1];
+#pragma unroll
+    for (int i = 0; i < CH; i++) {
+      const int off = (i * W + h) * 1024 + 16 * lane;
+      const int row = off / RB, c = (off % RB) >> 4;
+      const int t = row * RB + ((c ^ tile_swz(row, CPR)) << 4);
+      *reinterpret_cast<u32x4 *>(tk + t) = kb[s][i];
+      *reinterpret_cast<u32x4 *>(tv + t) = vb[s][i];
+    }
+    __syncthreads();
+    if ((startmask >> k) & 1) {  // item k starts a sequence: its Q goes to LDS
+      if (k > 0) {
+        finish(seg, seg_first);
+        reset();
+        seg = seq_at(k);
+        seg_first = k;
+      }
+      // Every wave has passed the barrier above, so none still reads the
+      // previous sequence's Q.
+#pragma unroll
+      for (int i = 0; i < QL; i++) {
+        const int c = (i * W + h) * 64 + lane;
+        if (c < qchunks) {
+          const int row = c / CPQ, cc = c % CPQ;
+          *reinterpret_cast<u32x4 *>(qtile + row * D * 2 + ((cc ^ (row & (CPQ - 1))) << 4)) = qb[s][i];
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < NR; r++) qop[r] = *reinterpret_cast<const bf16x8 *>(qtile + q_rd[r]);
+    }
+    u32x4 kq[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) kq[r] = *reinterpret_cast<const u32x4 *>(tk + k_rd[r]);
+    const int meta = __builtin_amdgcn_readlane(metav, k);
+    mfma_block_t<D>(kq, tv, v_rd, meta & kMetaValid, (badmask >> k) & 1, qop, a.sl2, lane, st);
+  };
+  // The main loop has no branch around any stage: a path that skipped one
+  // would make the compiler's wait counts assume fewer loads in flight and
+  // drain the ring. The last n mod R items run after it.
+  const int nfull = n / R;
+  int k0 = 0;
+  for (int it = 0; it < nfull; it++, k0 += R) {
+#pragma unroll
+    for (int s = 0; s < R; s++) stage(s, k0 + s);
+  }
+#pragma unroll
+  for (int s = 0; s < R - 1; s++)
+    if (k0 + s < n) stage(s, k0 + s);
   finish(seg, seg_first);
   if (a.new_k) store_new_rows<D>(a, lane, h, idv, seqv, metav, n, badv);
 }
 
-// One wave per (sequence cut by piece boundaries, query head).
 template <int D, bool BF16>
 __global__ void __launch_bounds__(256) merge_planned_kernel(KArgs a, PlanDev pd) {
   const int lane = threadIdx.x & 63;
@@ -1397,15 +1557,26 @@ static int launch_planned(Pool *p, const Plan *pl, int32_t layer, const void *d_
       mpl->bound_indptr = d_block_indptr;
       mpl->bound_ids = d_block_ids;
     }
-    const bool coop = a.nqc == 1 && (g.Hkv == 1 || g.Hkv == 2 || g.Hkv == 4) &&
+    // Cooperative kernel: Q rows of one sequence (Hq * D * 2 bytes) must fit
+    // the QL loads per lane its ring slots carry.
+    const int qlanes = 64 * g.Hkv;
+    const int qchunks = g.Hq * g.D / 8;
+    const int ql = (qchunks + qlanes - 1) / qlanes;
+    const bool coop = a.nqc == 1 && (g.Hkv == 1 || g.Hkv == 2 || g.Hkv == 4) && ql <= 4 &&
                       !(flags & MKV_ATTN_PER_HEAD_LOADS);
     if (coop) {
       const dim3 cgrid((unsigned)pl->P), cblock(64 * g.Hkv);
-#define MKV_COOP(DD)                                                                              \
-  do {                                                                                            \
-    if (g.Hkv == 1) hipLaunchKernelGGL((attn_coop_kernel<DD, 1, kCoopRing>), cgrid, cblock, 0, hs, a, pd);    \
-    else if (g.Hkv == 2) hipLaunchKernelGGL((attn_coop_kernel<DD, 2, kCoopRing>), cgrid, cblock, 0, hs, a, pd); \
-    else hipLaunchKernelGGL((attn_coop_kernel<DD, 4, kCoopRing>), cgrid, cblock, 0, hs, a, pd);               \
+#define MKV_COOP_QL(DD, WW)                                                                              \
+  do {                                                                                                   \
+    if (ql == 1) hipLaunchKernelGGL((attn_coop_kernel<DD, WW, 1, kCoopRing>), cgrid, cblock, 0, hs, a, pd); \
+    else if (ql == 2) hipLaunchKernelGGL((attn_coop_kernel<DD, WW, 2, kCoopRing>), cgrid, cblock, 0, hs, a, pd); \
+    else hipLaunchKernelGGL((attn_coop_kernel<DD, WW, 4, kCoopRing - 1>), cgrid, cblock, 0, hs, a, pd);    \
+  } while (0)
+#define MKV_COOP(DD)                                   \
+  do {                                                 \
+    if (g.Hkv == 1) MKV_COOP_QL(DD, 1);                \
+    else if (g.Hkv == 2) MKV_COOP_QL(DD, 2);           \
+    else MKV_COOP_QL(DD, 4);                           \
   } while (0)
       switch (g.D) {
         case 64: MKV_COOP(64); break;
@@ -1413,6 +1584,7 @@ static int launch_planned(Pool *p, const Plan *pl, int32_t layer, const void *d_
         default: MKV_COOP(256); break;
       }
 #undef MKV_COOP
+#undef MKV_COOP_QL
       MKV_CHECK_LAUNCH("attn_coop_kernel");
     } else {
       switch (g.D) {
