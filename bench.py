@@ -49,7 +49,28 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-launch-events", action="store_true",
                     help="time the steps without per-launch HIP events (roofline fields null)")
+    ap.add_argument("--cpu-layers", type=int, default=5,
+                    help="layers of the batch in the CPU baseline sample")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only copy 1 GiB device to device (the known-size kernel that scales "
+                         "rocprofv3's FETCH_SIZE / WRITE_SIZE counters) and exit")
     return ap.parse_args()
+
+
+def copy_calibration():
+    """One 1 GiB device-to-device copy after a warm-up copy: the reference
+    dispatch whose FETCH_SIZE and WRITE_SIZE counters, against its known
+    2 x 1 GiB of traffic, give the scale factors of the HBM traffic figures."""
+    import torch
+
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": n}), flush=True)
 
 
 def profiled_traffic(config: str, mode: str):
@@ -79,34 +100,36 @@ def cpu_info():
     return model
 
 
-def cpu_baseline(cfg, batch, step_bytes):
+def cpu_baseline(cfg, batch, step_bytes, layers):
     """Reference-faithful CPU decode (contiguous f32 cache grown by a copy per
-    token, repeat_kv materialised, mask, softmax, matmuls) for one layer of
-    every sequence of the batch, scaled to a full step. The primary figure is
-    one thread, sequences one after another, as the reference executes
-    requests serially (inference-backend/src/burn_backend.rs:44-71); the same
-    sample threaded over sequences is reported beside it."""
+    token, repeat_kv materialised, mask, softmax, matmuls) for `layers` layers
+    of every sequence of the batch, scaled to a full step. The primary figure
+    is one thread, sequences one after another, as the reference executes
+    requests serially (inference-backend/src/burn_backend.rs:44-71); one layer
+    of the same sample threaded over sequences is reported beside it."""
     from oracle import oracle as orc
 
     ctx = batch.ctx_lens
+    layers = max(1, min(layers, cfg["num_layers"]))
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     orc.set_num_threads(1)
-    t1 = orc.ref_faithful_batch(ctx, cfg["num_kv_heads"], cfg["num_q_heads"], cfg["head_dim"], seed=1)
+    t1 = sum(orc.ref_faithful_batch(ctx, cfg["num_kv_heads"], cfg["num_q_heads"], cfg["head_dim"],
+                                    seed=1 + layer) for layer in range(layers))
     orc.set_num_threads(threads)
-    tn = orc.ref_faithful_batch(ctx, cfg["num_kv_heads"], cfg["num_q_heads"], cfg["head_dim"], seed=2)
-    step_1t, step_nt = t1 * cfg["num_layers"], tn * cfg["num_layers"]
+    tn = orc.ref_faithful_batch(ctx, cfg["num_kv_heads"], cfg["num_q_heads"], cfg["head_dim"], seed=100)
+    step_1t, step_nt = t1 / layers * cfg["num_layers"], tn * cfg["num_layers"]
     return {
         "value": round(step_bytes / step_1t / 1e9, 3),
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
-        "sample": (f"1 of {cfg['num_layers']} layers x all {batch.num_seqs} sequences, 1 thread, "
+        "sample": (f"{layers} of {cfg['num_layers']} layers x all {batch.num_seqs} sequences, 1 thread, "
                    f"{t1:.1f} s; scaled to a full step"),
         "tokens_per_s": round(batch.num_seqs / step_1t, 2),
         "ms_per_step": round(step_1t * 1e3, 1),
         "threaded": {"value": round(step_bytes / step_nt / 1e9, 3), "unit": "GB/s", "cores": threads,
                      "tokens_per_s": round(batch.num_seqs / step_nt, 2),
-                     "sample": f"same sample, {threads} threads over sequences, {tn:.1f} s"},
+                     "sample": f"1 layer of the sample, {threads} threads over sequences, {tn:.1f} s"},
         "cpu_model": cpu_info(),
         "host_cpus": os.cpu_count(),
     }
@@ -114,6 +137,9 @@ def cpu_baseline(cfg, batch, step_bytes):
 
 def main():
     args = parse()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: every box here has one MI355X and this path runs "
               f"on a single device (requested --gpus {args.gpus}).", file=sys.stderr)
@@ -244,7 +270,7 @@ def main():
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(cfg, batch, step_bytes)
+        result["cpu_baseline"] = cpu_baseline(cfg, batch, step_bytes, args.cpu_layers)
     plan.close()
     pool.close()
     print(json.dumps(result), flush=True)
