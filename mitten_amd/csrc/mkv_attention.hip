@@ -50,6 +50,8 @@ constexpr float kRescaleSlack = 8.0f;  // log2 units: p <= 2^8 between rescales
 constexpr int kQChunkMfma = 16;
 constexpr int kQChunkValu = 8;
 constexpr int kRing = 3;       // MFMA loop: blocks loaded ahead + 1
+constexpr int kBlockWeight = 8;    // plan: weight of one block in a piece ...
+constexpr int kSwitchWeight = 12;  // ... and of a sequence start inside it (about 1.5 blocks)
 constexpr int kCoopRing = 3;   // register stages of the cooperative kernel (one less when
                                // its slots carry four Q loads per lane)
 
@@ -624,12 +626,15 @@ __global__ void __launch_bounds__(256) merge_split_kernel(KArgs a, SplitArgs sp)
 struct PlanDev {
   const int32_t *ctx;         // [B] tokens attended
   const int32_t *seq_blk0;    // [B+1] first flattened block of each sequence
+  const int32_t *piece_f0;    // [P+1] first flattened block of each piece (<= 64 per piece)
   const int32_t *piece_seq;   // [P] sequence holding each piece's first block
+  const int32_t *seq_piece0;  // [B] first piece of each sequence
+  const int32_t *seq_npiece;  // [B] pieces a sequence spans
   const int32_t *merge_seqs;  // [n_merge] sequences cut by a piece boundary
   const int32_t *flat_seq;    // [total] sequence of each flattened block
   const int32_t *flat_meta;   // [total] kMetaValid | kMetaLast | kMetaSingle bits
   int32_t *flat_id;           // [total] block id (written per step from the tables)
-  int32_t B, P, BP, total_blocks, n_merge;
+  int32_t B, P, total_blocks, n_merge;
 };
 
 // flat_meta bits of a flattened block.
@@ -689,8 +694,8 @@ attn_stream_kernel(KArgs a, PlanDev pd) {
   const int h = hc / a.nqc, qc = hc % a.nqc;
   const int m16 = lane & 15, g4 = lane >> 4, a4 = m16 >> 2, rq = m16 & 3;
   const int p = blockIdx.x;
-  const int f0 = p * pd.BP;
-  const int n = min(pd.BP, pd.total_blocks - f0);  // 1..64 items
+  const int f0 = pd.piece_f0[p];
+  const int n = pd.piece_f0[p + 1] - f0;  // 1..64 items
   int32_t idv = -1, seqv = 0, metav = 0;
   if (lane < n) {
     idv = pd.flat_id[f0 + lane];
@@ -808,8 +813,8 @@ __global__ void __launch_bounds__(256) attn_planned_kernel(KArgs a, PlanDev pd) 
   sg.h = hc / a.nqc;
   sg.qc = hc % a.nqc;
   const int p = blockIdx.x;
-  int f = p * pd.BP;
-  const int f_end = min(f + pd.BP, pd.total_blocks);
+  int f = pd.piece_f0[p];
+  const int f_end = pd.piece_f0[p + 1];
   int b = pd.piece_seq[p];
   for (; f < f_end; ++b) {
     const int sb = pd.seq_blk0[b], nb = pd.seq_blk0[b + 1] - sb;
@@ -837,7 +842,7 @@ __global__ void __launch_bounds__(256) attn_planned_kernel(KArgs a, PlanDev pd) 
         if (sg.qc == 0) store_new_row<D, ES>(a, lane, b, sg.h, blk, (sg.ctx - 1) % kPageSize);
       }
     }
-    const bool single = sb / pd.BP == (sb + nb - 1) / pd.BP;
+    const bool single = pd.flat_meta[sb] & kMetaSingle;
     run_segment<D, BF16, MFMA>(a, sg, lane, single, (int64_t)(p + b) * a.Hq, 1);
   }
 }
@@ -979,8 +984,8 @@ attn_coop_kernel(KArgs a, PlanDev pd) {
   const int h = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave = KV head
   const int m16 = lane & 15, g4 = lane >> 4, a4 = m16 >> 2, rq = m16 & 3;
   const int p = blockIdx.x;
-  const int f0 = p * pd.BP;
-  const int n = min(pd.BP, pd.total_blocks - f0);
+  const int f0 = pd.piece_f0[p];
+  const int n = pd.piece_f0[p + 1] - f0;  // 1..64 items
   const int qchunks = a.Hq * CPQ;        // Q chunks of one sequence (<= QCAP / 16)
   int32_t idv = -1, seqv = 0, metav = 0;
   if (lane < n) {
@@ -1083,12 +1088,6 @@ attn_coop_kernel(KArgs a, PlanDev pd) {
     }
     __syncthreads();
     if ((startmask >> k) & 1) {  // item k starts a sequence: its Q goes to LDS
-      if (k > 0) {
-        finish(seg, seg_first);
-        reset();
-        seg = seq_at(k);
-        seg_first = k;
-      }
       // Every wave has passed the barrier above, so none still reads the
       // previous sequence's Q.
 #pragma unroll
@@ -1098,6 +1097,15 @@ attn_coop_kernel(KArgs a, PlanDev pd) {
           const int row = c / CPQ, cc = c % CPQ;
           *reinterpret_cast<u32x4 *>(qtile + row * D * 2 + ((cc ^ (row & (CPQ - 1))) << 4)) = qb[s][i];
         }
+      }
+      if (k > 0) {
+        // The previous sequence's result. Its stores go after the wait on
+        // this item's Q above: the wait's count assumes no stores, and
+        // would otherwise also wait for the loads issued this stage.
+        finish(seg, seg_first);
+        reset();
+        seg = seq_at(k);
+        seg_first = k;
       }
       __syncthreads();
 #pragma unroll
@@ -1133,9 +1141,8 @@ __global__ void __launch_bounds__(256) merge_planned_kernel(KArgs a, PlanDev pd)
   if (row >= (int64_t)pd.n_merge * a.Hq) return;
   const int b = pd.merge_seqs[row / a.Hq];
   const int hq = (int)(row % a.Hq);
-  const int sb = pd.seq_blk0[b], nb = pd.seq_blk0[b + 1] - sb;
-  const int first = sb / pd.BP, last = (sb + nb - 1) / pd.BP;
-  merge_rows<D, BF16>(a, lane, (int64_t)(first + b) * a.Hq + hq, a.Hq, last - first + 1,
+  const int first = pd.seq_piece0[b];
+  merge_rows<D, BF16>(a, lane, (int64_t)(first + b) * a.Hq + hq, a.Hq, pd.seq_npiece[b],
                       (int64_t)b * a.Hq + hq);
 }
 
@@ -1251,7 +1258,9 @@ struct Plan {
   Pool *pool = nullptr;
   int device = 0;
   int32_t B = 0, P = 0, BP = 0, total = 0, n_merge = 0;
-  int32_t *d_meta = nullptr;  // ctx[B] | seq_blk0[B+1] | piece_seq[P] | merge_seqs[n_merge]
+  int32_t *d_meta = nullptr;  // ctx[B] | seq_blk0[B+1] | piece_f0[P+1] | piece_seq[P] |
+                              // seq_piece0[B] | seq_npiece[B] | merge_seqs[n_merge] |
+                              // flat_seq[total] | flat_meta[total]
   size_t meta_cap = 0;        // ints
   int32_t *h_meta = nullptr;  // pinned staging
   size_t h_cap = 0;
@@ -1270,14 +1279,16 @@ static PlanDev plan_dev(const Plan *pl) {
   PlanDev d;
   d.ctx = pl->d_meta;
   d.seq_blk0 = d.ctx + pl->B;
-  d.piece_seq = d.seq_blk0 + pl->B + 1;
-  d.merge_seqs = d.piece_seq + pl->P;
+  d.piece_f0 = d.seq_blk0 + pl->B + 1;
+  d.piece_seq = d.piece_f0 + pl->P + 1;
+  d.seq_piece0 = d.piece_seq + pl->P;
+  d.seq_npiece = d.seq_piece0 + pl->B;
+  d.merge_seqs = d.seq_npiece + pl->B;
   d.flat_seq = d.merge_seqs + pl->n_merge;
   d.flat_meta = d.flat_seq + pl->total;
   d.flat_id = pl->d_flat_id;
   d.B = pl->B;
   d.P = pl->P;
-  d.BP = pl->BP;
   d.total_blocks = pl->total;
   d.n_merge = pl->n_merge;
   return d;
@@ -1411,12 +1422,9 @@ extern "C" int mkv_decode_plan_build(mkv_decode_plan *plan, const int32_t *h_ctx
   if (num_seqs < 1 || !h_ctx_lens) return set_error(MKV_ERR_INVALID_ARGUMENT, "need num_seqs >= 1 context lengths");
   if (pieces < 0) return set_error(MKV_ERR_INVALID_ARGUMENT, "pieces must be >= 0");
   int64_t total = 0;
-  int max_nb = 0;
   for (int32_t b = 0; b < num_seqs; b++) {
     if (h_ctx_lens[b] < 1) return set_error(MKV_ERR_INVALID_ARGUMENT, "ctx_len[%d] = %d < 1", b, h_ctx_lens[b]);
-    const int nb = (h_ctx_lens[b] + kPageSize - 1) / kPageSize;
-    total += nb;
-    max_nb = std::max(max_nb, nb);
+    total += (h_ctx_lens[b] + kPageSize - 1) / kPageSize;
   }
   if (total > INT32_MAX / 2) return set_error(MKV_ERR_INVALID_ARGUMENT, "batch too large");
   // Workgroup slots: ~8 waves per CU on 256 CUs, one wave per (KV head,
@@ -1425,12 +1433,59 @@ extern "C" int mkv_decode_plan_build(mkv_decode_plan *plan, const int32_t *h_ctx
   const int nqc = (G + kQChunkMfma - 1) / kQChunkMfma;
   int64_t P = pieces ? pieces : std::max<int64_t>(1, 2048 / std::max(1, g.Hkv * nqc));
   P = std::max<int64_t>(P, (total + 63) / 64);  // a piece is at most 64 blocks (one per lane)
-  int64_t BP = std::max<int64_t>(1, (total + P - 1) / P);
-  P = (total + BP - 1) / BP;
+  P = std::min<int64_t>(P, total);
+  std::vector<int32_t> blk0v(num_seqs + 1);
+  {
+    int64_t acc = 0;
+    for (int32_t b = 0; b < num_seqs; b++) {
+      blk0v[b] = (int32_t)acc;
+      acc += (h_ctx_lens[b] + kPageSize - 1) / kPageSize;
+    }
+    blk0v[num_seqs] = (int32_t)acc;
+  }
+  // Piece boundaries: a greedy fill of the flattened blocks under a weight
+  // cap, the smallest that gives at most P pieces. A block weighs
+  // kBlockWeight; a sequence that starts inside a piece (not at its first
+  // block) adds kSwitchWeight, what its predecessor's partial stores and the
+  // Q reload cost that piece (measured: about 1.5 blocks' time).
+  std::vector<int32_t> f0s;
+  auto cut = [&](int64_t cap) {
+    f0s.clear();
+    int64_t w = 0;
+    int cnt = 0;
+    int32_t b = 0;
+    for (int64_t f = 0; f < total; f++) {
+      while (blk0v[b + 1] <= f) b++;
+      int64_t wi = kBlockWeight + ((f == blk0v[b] && cnt > 0) ? kSwitchWeight : 0);
+      if (cnt > 0 && (cnt == 64 || w + wi > cap)) {
+        cnt = 0;
+        w = 0;
+        wi = kBlockWeight;
+      }
+      if (cnt == 0) f0s.push_back((int32_t)f);
+      w += wi;
+      cnt++;
+    }
+    f0s.push_back((int32_t)total);
+  };
+  {  // smallest cap giving at most P pieces (the count falls as the cap grows)
+    int64_t lo = (kBlockWeight * total + P - 1) / P, hi = 64 * (kBlockWeight + kSwitchWeight);
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) / 2;
+      cut(mid);
+      if ((int64_t)f0s.size() - 1 <= P) hi = mid;
+      else lo = mid + 1;
+    }
+    for (cut(lo); (int64_t)f0s.size() - 1 > P; cut(++lo)) {
+    }
+  }
+  P = (int64_t)f0s.size() - 1;
+  int64_t BP = 0;
+  for (int64_t q = 0; q < P; q++) BP = std::max<int64_t>(BP, f0s[q + 1] - f0s[q]);
   DeviceGuard guard(pl->pool->device);
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
-  std::vector<int32_t> merge;
-  const size_t n_ints = (size_t)num_seqs + (num_seqs + 1) + P + num_seqs + 2 * (size_t)total;
+  const size_t n_ints = (size_t)num_seqs + (num_seqs + 1) + (P + 1) + P + 3 * (size_t)num_seqs +
+                        2 * (size_t)total;
   // Staging: wait for the previous upload to leave the pinned buffer.
   if (pl->pending) {
     MKV_CHECK_HIP(hipEventSynchronize(pl->uploaded));
@@ -1443,34 +1498,38 @@ extern "C" int mkv_decode_plan_build(mkv_decode_plan *plan, const int32_t *h_ctx
     MKV_CHECK_HIP(hipHostMalloc(reinterpret_cast<void **>(&pl->h_meta), n_ints * 4));
     pl->h_cap = n_ints;
   }
-  int32_t *ctx = pl->h_meta, *blk0 = ctx + num_seqs, *pseq = blk0 + num_seqs + 1;
-  int64_t acc = 0;
-  for (int32_t b = 0; b < num_seqs; b++) {
-    ctx[b] = h_ctx_lens[b];
-    blk0[b] = (int32_t)acc;
-    acc += (h_ctx_lens[b] + kPageSize - 1) / kPageSize;
+  int32_t *ctx = pl->h_meta, *blk0 = ctx + num_seqs, *pf0 = blk0 + num_seqs + 1, *pseq = pf0 + P + 1;
+  int32_t *spiece0 = pseq + P, *snpiece = spiece0 + num_seqs, *mseq = snpiece + num_seqs;
+  for (int32_t b = 0; b < num_seqs; b++) ctx[b] = h_ctx_lens[b];
+  for (int32_t b = 0; b <= num_seqs; b++) blk0[b] = blk0v[b];
+  for (int64_t q = 0; q <= P; q++) pf0[q] = f0s[q];
+  for (int32_t b = 0, q = 0; q < P; q++) {
+    while (blk0[b + 1] <= pf0[q]) b++;
+    pseq[q] = b;
   }
-  blk0[num_seqs] = (int32_t)acc;
-  for (int32_t b = 0, piece = 0; piece < P; piece++) {
-    const int64_t f = piece * BP;
-    while (blk0[b + 1] <= f) b++;
-    pseq[piece] = b;
+  // Pieces of each sequence: first = the piece holding its first block.
+  for (int32_t b = 0, q = 0; b < num_seqs; b++) {
+    while (pf0[q + 1] <= blk0[b]) q++;
+    int32_t last = q;
+    while (pf0[last + 1] < blk0[b + 1]) last++;
+    spiece0[b] = q;
+    snpiece[b] = last - q + 1;
   }
-  int32_t *mseq = pseq + P;
   int n_merge = 0;
   for (int32_t b = 0; b < num_seqs; b++)
-    if (blk0[b] / BP != (blk0[b + 1] - 1) / BP) mseq[n_merge++] = b;
+    if (snpiece[b] > 1) mseq[n_merge++] = b;
   int32_t *fseq = mseq + n_merge, *fmeta = fseq + total;
   for (int32_t b = 0; b < num_seqs; b++) {
     const int nb = blk0[b + 1] - blk0[b];
-    const int single = blk0[b] / BP == (blk0[b + 1] - 1) / BP ? kMetaSingle : 0;
+    const int single = snpiece[b] == 1 ? kMetaSingle : 0;
     for (int j = 0; j < nb; j++) {
       const int last = j == nb - 1;
       fseq[blk0[b] + j] = b;
       fmeta[blk0[b] + j] = (last ? ctx[b] - kPageSize * j : kPageSize) | (last ? kMetaLast : 0) | single;
     }
   }
-  const size_t used = (size_t)num_seqs + (num_seqs + 1) + P + n_merge + 2 * (size_t)total;
+  const size_t used = (size_t)num_seqs + (num_seqs + 1) + (P + 1) + P + 2 * (size_t)num_seqs + n_merge +
+                      2 * (size_t)total;
   if (pl->meta_cap < used) {
     MKV_CHECK_HIP(hipStreamSynchronize(hs));  // earlier launches may read the old buffer
     if (pl->d_meta) MKV_CHECK_HIP(hipFree(pl->d_meta));
