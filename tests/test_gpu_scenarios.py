@@ -1,0 +1,299 @@
+"""End-to-end GPU scenarios at the shapes of the measurement configurations:
+the host block manager drives the device pool through the C ABI, and every
+phase is checked against the oracle (bit-exact for appends, copies and
+gathers; within the attention tolerances for decode attention).
+
+* C1, Qwen2.5-0.5B f32: bulk prompt append, then decode steps of
+  (append one token + gather + attention) over all 24 layers.
+* C4, radix sharing at Qwen-7B head shapes (2 of 28 layers): 256 sequences
+  fork one 4,100-token prefix (256 full blocks + a 4-token partial block),
+  copy-on-write of the shared partial block on the first append (255 copies,
+  the last holder writes in place), suffixes, decode steps, then 20% of the
+  sequences finish and the pool is compacted by batched block moves.
+* C5, pool pressure at Qwen-7B head shapes (1 of 28 layers): the
+  217,982-block pool of a 200 GB budget, 512 sequences with log-normal
+  lengths (median 2,048, sigma 1, capped at 32,768); per step 8 sequences
+  append a 512-token chunk and all others decode one token.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from mitten_amd import DeviceKvPool, PoolDesc
+from mitten_amd import workloads as wl
+from mitten_amd.host import BlockManager
+from oracle import oracle as orc
+from tests.helpers import assert_attention_close, bits, normal, odesc, to_device, to_host, widen
+
+pytestmark = pytest.mark.gpu
+
+
+def _i32(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a, np.int32)).cuda()
+
+
+def _tokens(seed, n):
+    return np.random.default_rng(seed).integers(0, 50_000, n).astype(np.uint32)
+
+
+def _ctx_indptr(ctx):
+    return np.concatenate([[0], np.cumsum(ctx)]).astype(np.int32)
+
+
+def _sub_batch(indptr, ids, ctx, rows):
+    """CSR tables of a subset of the batch's sequences."""
+    tabs = [ids[indptr[r]:indptr[r + 1]] for r in rows]
+    sub_ptr = np.concatenate([[0], np.cumsum([len(t) for t in tabs])]).astype(np.int32)
+    return sub_ptr, np.concatenate(tabs).astype(np.int32), np.asarray([ctx[r] for r in rows], np.int32)
+
+
+# --------------------------------------------------------------------- C1 ----
+
+def test_c1_prompt_append_then_decode_gather_attention():
+    c = wl.CONFIGS["qwen2.5-0.5b"]
+    L, Hq, Hkv, D = c["num_layers"], c["num_q_heads"], c["num_kv_heads"], c["head_dim"]
+    rng = wl.SplitMix64(wl.BASE_SEED + c["index"])
+    B, steps = c["batch"], 16
+    prompts = [rng.uniform_int(c["ctx_lo"], c["ctx_hi"]) for _ in range(B)]
+    num_blocks = sum((p + steps + 15) // 16 for p in prompts) + 4
+    desc = PoolDesc(L, Hkv, Hq, D, num_blocks, "f32")
+    od = odesc(desc)
+    bm = BlockManager(num_blocks)
+    want = np.zeros(desc.shape, np.float32)
+    with DeviceKvPool(desc) as pool:
+        pool.write(want)
+        # Bulk prompt append, all layers in one launch (admission order, LIFO pool).
+        slots = []
+        for s, p in enumerate(prompts):
+            assert bm.admit(s, _tokens(s, p)) == 0
+            sl, cow = bm.append(s, p)
+            assert cow == []
+            slots.append(sl)
+        slots = np.concatenate(slots).astype(np.int32)
+        k = normal(100, (L, slots.size, Hkv, D), "f32")
+        v = normal(101, (L, slots.size, Hkv, D), "f32")
+        pool.append_all_layers(to_device(k), to_device(v), _i32(slots))
+        for layer in range(L):
+            assert orc.append(od, want, layer, k[layer], v[layer], slots) == -1
+        pool.check()
+        assert np.array_equal(bits(pool.read()), bits(want))
+        for step in range(steps):
+            new = np.concatenate([bm.append(s, 1)[0] for s in range(B)]).astype(np.int32)
+            indptr, ids, ctx = bm.batch(list(range(B)))
+            assert np.array_equal(new, [ids[indptr[b] + (ctx[b] - 1) // 16] * 16 + (ctx[b] - 1) % 16
+                                        for b in range(B)])
+            plan = pool.plan(ctx)
+            d_ptr, d_ids, d_cptr = _i32(indptr), _i32(ids), _i32(_ctx_indptr(ctx))
+            check_layers = range(L) if step == steps - 1 else (0, L - 1)
+            for layer in range(L):
+                kn = normal(1000 + 31 * step + layer, (B, Hkv, D), "f32")
+                vn = normal(2000 + 31 * step + layer, (B, Hkv, D), "f32")
+                q = normal(3000 + 31 * step + layer, (B, Hq, D), "f32")
+                o = pool.decode_step(layer, plan, to_device(kn), to_device(vn), to_device(q), d_ptr, d_ids)
+                assert orc.append(od, want, layer, kn, vn, new) == -1
+                if layer in check_layers:
+                    gk, gv = pool.gather(layer, d_ptr, d_ids, d_cptr, int(ctx.max()))
+                    wk, wv = orc.gather(od, want, layer, indptr, ids, ctx)
+                    assert np.array_equal(bits(to_host(gk)), bits(wk))
+                    assert np.array_equal(bits(to_host(gv)), bits(wv))
+                    ref = orc.decode_attention(od, want, layer, q, indptr, ids, ctx)
+                    assert_attention_close(to_host(o), ref, "f32")
+            plan.close()
+        pool.check()
+        assert np.array_equal(bits(pool.read()), bits(want))
+    bm.check_invariants()
+
+
+# --------------------------------------------------------------------- C4 ----
+
+C4_SEQS, C4_PREFIX = 256, 4100
+
+
+def test_c4_radix_sharing_cow_decode_and_compaction():
+    L, Hq, Hkv, D = 2, 28, 4, 128  # Qwen-7B heads, 2 of 28 layers
+    rng = wl.SplitMix64(wl.BASE_SEED + 3)
+    suffix = [rng.uniform_int(16, 128) for _ in range(C4_SEQS)]
+    dec_steps = 3
+    prefix_blocks = (C4_PREFIX + 15) // 16
+    num_blocks = prefix_blocks + sum((4 + s + dec_steps + 15) // 16 + 1 for s in suffix) + 64
+    desc = PoolDesc(L, Hkv, Hq, D, num_blocks, "bf16")
+    od = odesc(desc)
+    bm = BlockManager(num_blocks)
+    want = np.zeros(desc.shape, np.uint16)
+    seqs = list(range(C4_SEQS))
+    with DeviceKvPool(desc) as pool:
+        pool.write(want)
+        # One prefill of the prefix, then every other sequence forks it.
+        assert bm.admit(0, _tokens(7, C4_PREFIX)) == 0
+        pslots, _ = bm.append(0, C4_PREFIX)
+        k = normal(200, (L, C4_PREFIX, Hkv, D), "bf16")
+        v = normal(201, (L, C4_PREFIX, Hkv, D), "bf16")
+        pool.append_all_layers(to_device(k), to_device(v), _i32(pslots))
+        for layer in range(L):
+            assert orc.append(od, want, layer, k[layer], v[layer], pslots) == -1
+        for s in seqs[1:]:
+            bm.fork(0, s)
+        shared = bm.table(0)
+        assert len(shared) == prefix_blocks and all(bm.refcount(b) == C4_SEQS for b in shared)
+        # First append of each sequence: the shared partial block is copied
+        # before the write, except by its last holder.
+        order = seqs[1:] + [0]
+        slots, src, dst = [], [], []
+        for s in order:
+            sl, cow = bm.append(s, suffix[s])
+            slots.append(sl)
+            for a, b in cow:
+                src.append(a)
+                dst.append(b)
+        assert len(src) == C4_SEQS - 1 and set(src) == {int(shared[-1])}
+        assert bm.table(0)[prefix_blocks - 1] == shared[-1]  # the last holder kept it
+        pool.copy_blocks(_i32(src), _i32(dst))
+        orc.copy_blocks(od, want, src, dst)
+        slots = np.concatenate(slots).astype(np.int32)
+        k = normal(202, (L, slots.size, Hkv, D), "bf16")
+        v = normal(203, (L, slots.size, Hkv, D), "bf16")
+        pool.append_all_layers(to_device(k), to_device(v), _i32(slots))
+        for layer in range(L):
+            assert orc.append(od, want, layer, k[layer], v[layer], slots) == -1
+        pool.check()
+        assert np.array_equal(bits(pool.read()), bits(want))
+        assert all(bm.refcount(b) == C4_SEQS for b in shared[:-1])
+        bm.check_invariants()
+        # Decode steps over all 256 sequences (the full prefix is read by each).
+        sample = list(range(0, C4_SEQS, 16))
+        for step in range(dec_steps):
+            new = []
+            for s in seqs:
+                sl, cow = bm.append(s, 1)
+                assert cow == []
+                new.append(sl)
+            new = np.concatenate(new).astype(np.int32)
+            indptr, ids, ctx = bm.batch(seqs)
+            plan = pool.plan(ctx)
+            d_ptr, d_ids = _i32(indptr), _i32(ids)
+            for layer in range(L):
+                kn = normal(300 + 7 * step + layer, (C4_SEQS, Hkv, D), "bf16")
+                vn = normal(400 + 7 * step + layer, (C4_SEQS, Hkv, D), "bf16")
+                q = normal(500 + 7 * step + layer, (C4_SEQS, Hq, D), "bf16")
+                o = pool.decode_step(layer, plan, to_device(kn), to_device(vn), to_device(q), d_ptr, d_ids)
+                assert orc.append(od, want, layer, kn, vn, new) == -1
+                sp, si, sc = _sub_batch(indptr, ids, ctx, sample)
+                ref = orc.decode_attention(od, want, layer, widen(q[sample]), sp, si, sc)
+                assert_attention_close(to_host(o)[sample], ref, "bf16")
+            plan.close()
+        pool.check()
+        assert np.array_equal(bits(pool.read()), bits(want))
+        # 20% of the sequences finish; compaction moves tail blocks into the holes.
+        done = seqs[::5]
+        live = [s for s in seqs if s not in done]
+        indptr, ids, ctx = bm.batch(live)
+        d_cptr = _i32(_ctx_indptr(ctx))
+        before = [to_host(t) for t in pool.gather(0, _i32(indptr), _i32(ids), d_cptr, int(ctx.max()))]
+        q = normal(600, (len(live), Hq, D), "bf16")
+        plan = pool.plan(ctx)
+        o_before = to_host(pool.decode_attention_planned(1, plan, to_device(q), _i32(indptr), _i32(ids)))
+        plan.close()
+        for s in done:
+            bm.release(s)
+        bm.check_invariants()
+        src, dst = bm.plan_compaction()
+        assert len(src) > 0 and set(src.tolist()).isdisjoint(dst.tolist())
+        pool.copy_blocks(_i32(src), _i32(dst))
+        orc.copy_blocks(od, want, src, dst)
+        bm.check_invariants()
+        indptr2, ids2, ctx2 = bm.batch(live)
+        assert np.array_equal(ctx2, ctx) and int(ids2.max()) < bm.live_blocks()
+        after = [to_host(t) for t in pool.gather(0, _i32(indptr2), _i32(ids2), d_cptr, int(ctx.max()))]
+        assert all(np.array_equal(bits(a), bits(b)) for a, b in zip(after, before))
+        plan = pool.plan(ctx2)
+        o_after = to_host(pool.decode_attention_planned(1, plan, to_device(q), _i32(indptr2), _i32(ids2)))
+        plan.close()
+        assert np.array_equal(bits(o_after), bits(o_before))  # same bytes, same order: same bits
+        pool.check()
+        assert np.array_equal(bits(pool.read()), bits(want))
+
+
+# --------------------------------------------------------------------- C5 ----
+
+C5_BLOCKS, C5_SEQS, C5_CHUNK, C5_CHUNK_SEQS = 217_982, 512, 512, 8
+
+
+def _lognormal_lengths(rng: wl.SplitMix64, n: int, median: int, sigma: float, cap: int):
+    out = []
+    for _ in range(n):
+        u1, u2 = rng.uniform01(), rng.uniform01()
+        z = math.sqrt(-2.0 * math.log(u1)) * math.cos(2.0 * math.pi * u2)  # Box-Muller
+        out.append(int(min(cap, max(1, round(median * math.exp(sigma * z))))))
+    return out
+
+
+def test_c5_pool_pressure_chunked_append_and_decode():
+    import torch
+
+    L, Hq, Hkv, D = 1, 28, 4, 128  # Qwen-7B heads, 1 of 28 layers
+    rng = wl.SplitMix64(wl.BASE_SEED + 4)
+    lengths = _lognormal_lengths(rng, C5_SEQS, 2048, 1.0, 32768)
+    desc = PoolDesc(L, Hkv, Hq, D, C5_BLOCKS, "bf16")
+    bm = BlockManager(C5_BLOCKS)
+    seqs = list(range(C5_SEQS))
+    for s in seqs:
+        bm.admit(s, _tokens(10_000 + s, lengths[s]))
+        bm.append(s, lengths[s])
+    assert bm.live_blocks() == sum((n + 15) // 16 for n in lengths)
+    with DeviceKvPool(desc) as pool:
+        view = pool.tensor()
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(5)
+        view.normal_(generator=gen)  # every slot holds N(0,1) K/V
+        torch.cuda.synchronize()
+
+        def blocks_of(table):
+            """Host copy of the given blocks of layer 0: [2, n, 16, Hkv, D] bf16 bits."""
+            t = view[0][:, torch.from_numpy(np.asarray(table, np.int64)).cuda()]
+            return to_host(t.contiguous())
+
+        for step in range(2):
+            chunk = seqs[step * C5_CHUNK_SEQS:(step + 1) * C5_CHUNK_SEQS]
+            slots = np.concatenate([bm.append(s, C5_CHUNK)[0] for s in chunk]).astype(np.int32)
+            kc = normal(700 + step, (slots.size, Hkv, D), "bf16")
+            vc = normal(800 + step, (slots.size, Hkv, D), "bf16")
+            pool.append(0, to_device(kc), to_device(vc), _i32(slots))
+            blk = torch.from_numpy((slots // 16).astype(np.int64)).cuda()
+            off = torch.from_numpy((slots % 16).astype(np.int64)).cuda()
+            assert np.array_equal(to_host(view[0, 0, blk, off]), kc)
+            assert np.array_equal(to_host(view[0, 1, blk, off]), vc)
+            dec = [s for s in seqs if s not in chunk]
+            new = np.concatenate([bm.append(s, 1)[0] for s in dec]).astype(np.int32)
+            indptr, ids, ctx = bm.batch(dec)
+            plan = pool.plan(ctx)
+            kn = normal(900 + step, (len(dec), Hkv, D), "bf16")
+            vn = normal(950 + step, (len(dec), Hkv, D), "bf16")
+            q = normal(990 + step, (len(dec), Hq, D), "bf16")
+            o = to_host(pool.decode_step(0, plan, to_device(kn), to_device(vn), to_device(q),
+                                         _i32(indptr), _i32(ids)))
+            plan.close()
+            pool.check()
+            blk = torch.from_numpy((new // 16).astype(np.int64)).cuda()
+            off = torch.from_numpy((new % 16).astype(np.int64)).cuda()
+            assert np.array_equal(to_host(view[0, 0, blk, off]), kn)  # fused append, bit-exact
+            assert np.array_equal(to_host(view[0, 1, blk, off]), vn)
+            # Attention of a sample (short, median and the longest sequences)
+            # against the oracle over those sequences' blocks.
+            order = np.argsort(ctx)
+            sample = sorted(set(order[:4].tolist() + order[len(order) // 2:len(order) // 2 + 4].tolist()
+                                + order[-8:].tolist()))
+            for r in sample:
+                table = ids[indptr[r]:indptr[r + 1]]
+                mini = blocks_of(table)[None]  # [1, 2, n, 16, Hkv, D]
+                md = orc.desc(1, Hkv, D, len(table), 2)
+                ref = orc.decode_attention(md, np.ascontiguousarray(mini), 0, widen(q[r:r + 1]),
+                                           np.array([0, len(table)], np.int32),
+                                           np.arange(len(table), dtype=np.int32), ctx[r:r + 1])
+                assert_attention_close(o[r:r + 1], ref, "bf16")
+        del view
+    bm.check_invariants()
