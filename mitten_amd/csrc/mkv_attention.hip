@@ -509,24 +509,26 @@ __device__ __forceinline__ void run_segment(const KArgs &a, const Seg &sg, int l
 template <int D, bool BF16>
 __device__ __forceinline__ void merge_rows(const KArgs &a, int lane, int64_t base, int64_t stride, int n,
                                            int64_t out_row) {
+  // Lane owns DPL contiguous dims (one vector load per partial row); all
+  // loads of up to SB partials are issued before their first use.
   constexpr int DPL = (D + 63) / 64;
   constexpr int SB = 16;
-  float acc[DPL];
-#pragma unroll
-  for (int k = 0; k < DPL; k++) acc[k] = 0.0f;
+  typedef float fvec __attribute__((ext_vector_type(DPL)));
+  const int d0 = lane * DPL;
+  const bool has = d0 < D;  // D = 32 leaves half the lanes idle
+  fvec acc = {};
   float M = -INFINITY, L = 0.0f;
   for (int s0 = 0; s0 < n; s0 += SB) {
     const int cnt = min(SB, n - s0);
     float2 ml = make_float2(-INFINITY, 0.0f);
     if (lane < cnt) ml = *reinterpret_cast<const float2 *>(a.ws_ml + 2 * (base + (int64_t)(s0 + lane) * stride));
-    float ov[SB][DPL];
+    fvec ov[SB];
 #pragma unroll
-    for (int i = 0; i < SB; i++)
-#pragma unroll
-      for (int k = 0; k < DPL; k++) {
-        const int d = lane + 64 * k;
-        ov[i][k] = (i < cnt && d < D) ? a.ws_o[(base + (int64_t)(s0 + i) * stride) * D + d] : 0.0f;
-      }
+    for (int i = 0; i < SB; i++) {
+      ov[i] = fvec{};
+      if (i < cnt && has)
+        ov[i] = *reinterpret_cast<const fvec *>(a.ws_o + (base + (int64_t)(s0 + i) * stride) * D + d0);
+    }
     float mb = ml.x;
 #pragma unroll
     for (int o = 8; o >= 1; o >>= 1) mb = fmaxf(mb, __shfl_xor(mb, o));
@@ -538,25 +540,29 @@ __device__ __forceinline__ void merge_rows(const KArgs &a, int lane, int64_t bas
 #pragma unroll
     for (int o = 8; o >= 1; o >>= 1) lw += __shfl_xor(lw, o);
     L = L * carry + __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, lw)));
-#pragma unroll
-    for (int k = 0; k < DPL; k++) acc[k] *= carry;
+    acc *= carry;
 #pragma unroll
     for (int i = 0; i < SB; i++) {
       const float wi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), i));
-#pragma unroll
-      for (int k = 0; k < DPL; k++) acc[k] = fmaf(wi, ov[i][k], acc[k]);
+      acc += wi * ov[i];
     }
     M = Mn;
   }
+  if (!has) return;
   const float f = final_scale(M, L, a.zero_sink);
+  if constexpr (BF16) {
+    uint16_t *op = reinterpret_cast<uint16_t *>(a.o) + out_row * D + d0;
+    if constexpr (DPL == 1) {
+      *op = (uint16_t)f32_to_bf16_bits(acc[0] * f);
+    } else {
+      uint32_t w[DPL / 2];
 #pragma unroll
-  for (int k = 0; k < DPL; k++) {
-    const int d = lane + 64 * k;
-    if (d >= D) break;
-    if constexpr (BF16)
-      reinterpret_cast<uint16_t *>(a.o)[out_row * D + d] = (uint16_t)f32_to_bf16_bits(acc[k] * f);
-    else
-      reinterpret_cast<float *>(a.o)[out_row * D + d] = acc[k] * f;
+      for (int k = 0; k < DPL / 2; k++) w[k] = pack_bf16x2(acc[2 * k] * f, acc[2 * k + 1] * f);
+      if constexpr (DPL == 2) *reinterpret_cast<uint32_t *>(op) = w[0];
+      else *reinterpret_cast<uint2 *>(op) = make_uint2(w[0], w[1]);
+    }
+  } else {
+    *reinterpret_cast<fvec *>(reinterpret_cast<float *>(a.o) + out_row * D + d0) = acc * f;
   }
 }
 
