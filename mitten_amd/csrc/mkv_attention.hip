@@ -1139,6 +1139,208 @@ attn_coop_kernel(KArgs a, PlanDev pd) {
   if (a.new_k) store_new_rows<D>(a, lane, h, idv, seqv, metav, n, badv);
 }
 
+// ===========================================================================
+// Extend (chunked prefill) attention: causal attention of each sequence's
+// newest q_len tokens over its whole cache (the chunk's own K/V already
+// appended), the seq_q > 1 path of inference-model-qwen/src/model.rs:410-416
+// with the causal mask of model.rs:542-555 (a key at position j is visible to
+// the query at position p iff j <= p).
+//
+// One workgroup per (16-token query tile, KV head, sequence); W >= G waves,
+// wave g computing query head h*G + g for the tile's 16 positions (the MFMA
+// column dimension). The workgroup streams the head's K/V blocks 0..(last
+// tile position)/16 through the same double-buffered, swizzled LDS tile as
+// the decode kernel (rows of one head: D*2 bytes), loaded cooperatively
+// three blocks deep; scores, online softmax and the V^T transpose reads are
+// those of the decode kernel, with the causal mask applied on blocks that
+// reach past the tile's first position.
+// ===========================================================================
+
+struct ExtArgs {
+  const int32_t *q_indptr;  // [B+1] query tokens of each sequence in q / o
+  const int32_t *ctx;       // [B] tokens in the cache, the chunk included
+  int32_t B, max_ctx;
+};
+
+template <int D, int W>
+__global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e) {
+  constexpr int NR = D / 32, NT = D / 16;
+  constexpr int RB = D * 2;                           // LDS tile row: one head's K or V row
+  constexpr int CPR = RB / 16;                        // 16-byte chunks per tile row
+  constexpr int TILE = 16 * RB;
+  constexpr int NCH = 2 * 16 * CPR;                   // chunks of K + V of one block
+  constexpr int LPL = (NCH + 64 * W - 1) / (64 * W);  // loads per lane per block
+  constexpr int R = 3;
+  __shared__ __attribute__((aligned(16))) uint8_t tiles[2][2][TILE];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int m16 = lane & 15, g4 = lane >> 4, a4 = m16 >> 2, rq = m16 & 3;
+  const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int q0 = e.q_indptr[b], nq = e.q_indptr[b + 1] - q0;
+  if (nq <= 0 || 16 * t >= nq) return;
+  const int ctx = e.ctx[b];
+  if (nq > ctx || ctx > e.max_ctx) {
+    if (threadIdx.x == 0 && t == 0) record_error(a.d_err, MKV_DEVERR_CTX);
+    return;
+  }
+  const int tab0 = a.indptr[b], nbt = (ctx + kPageSize - 1) / kPageSize;
+  if (tab0 < 0 || a.indptr[b + 1] - tab0 < nbt) {
+    if (threadIdx.x == 0 && t == 0) record_error(a.d_err, MKV_DEVERR_TABLE);
+    return;
+  }
+  const int32_t *table = a.ids + tab0;
+  const int qlo = ctx - nq + 16 * t;          // first query position of the tile
+  const int qhi = min(qlo + 15, ctx - 1);     // last valid one
+  const int n = qhi / kPageSize + 1;          // blocks holding keys 0..qhi
+  const bool computes = wave < a.G;
+  const int hq = h * a.G + min(wave, a.G - 1);
+  const int qp = qlo + m16;                   // this lane's query position (rows past nq: unused)
+  const int64_t spare = dummy_offset(a);
+
+  // Q^T operand: lane holds Q[row 16t + lane%16][32r + 8*(lane/16) .. +8].
+  bf16x8 qop[NR];
+  {
+    const int row = min(16 * t + m16, nq - 1);
+    const uint8_t *qp8 = static_cast<const uint8_t *>(a.q) + ((int64_t)(q0 + row) * a.Hq + hq) * D * 2;
+#pragma unroll
+    for (int r = 0; r < NR; r++)
+      qop[r] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(qp8 + 2 * (32 * r + 8 * g4)));
+  }
+
+  // Ring slot: lane loads chunks c = threadIdx.x + 64*W*i of block k (K rows
+  // then V rows of head h); items past n (and lanes past the block) read 128
+  // bytes of a block picked by the workgroup index, so every stage issues
+  // the same loads.
+  u32x4 ring[R][LPL];
+  bool badk[R];
+  auto issue = [&](u32x4 (&d)[LPL], bool &bad, int k) {
+    const bool live = k < n;
+    int32_t blk = live ? table[k] : 0;  // uniform: a scalar load
+    bad = live && (blk < 0 || blk >= a.nblocks);
+    if (bad) blk = 0;
+#pragma unroll
+    for (int i = 0; i < LPL; i++) {
+      const int c = (int)threadIdx.x + 64 * W * i;
+      const int kv = c / (16 * CPR), rem = c % (16 * CPR), row = rem / CPR, cc = rem % CPR;
+      const bool real = live && c < NCH;
+      const uint8_t *plane = kv ? a.v_plane : a.k_plane;
+      const int64_t off = real ? (int64_t)blk * a.block_bytes + (int64_t)row * a.row_bytes + h * RB + 16 * cc
+                               : spare + 16 * (lane & 7);
+      d[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>((real ? plane : a.k_plane) + off));
+    }
+  };
+
+  MStateT<D> st;
+#pragma unroll
+  for (int nn = 0; nn < NT; nn++) st.O[nn] = f32x4{0.f, 0.f, 0.f, 0.f};
+  st.m = -INFINITY;
+  st.l = 0.0f;
+  int k_rd[NR], v_rd[NT];
+  const int vrow = 4 * g4 + a4;
+#pragma unroll
+  for (int r = 0; r < NR; r++) k_rd[r] = m16 * RB + (((g4 + 4 * r) ^ tile_swz(m16, CPR)) << 4);
+#pragma unroll
+  for (int nn = 0; nn < NT; nn++)
+    v_rd[nn] = vrow * RB + (((2 * nn + (rq >> 1)) ^ tile_swz(vrow, CPR)) << 4) + 8 * (rq & 1);
+
+  auto stage = [&](int s, int k) {
+    issue(ring[(s + R - 1) % R], badk[(s + R - 1) % R], k + R - 1);
+    uint8_t *tk = tiles[k & 1][0], *tv = tiles[k & 1][1];
+#pragma unroll
+    for (int i = 0; i < LPL; i++) {
+      const int c = (int)threadIdx.x + 64 * W * i;
+      if (c < NCH) {
+        const int kv = c / (16 * CPR), rem = c % (16 * CPR), row = rem / CPR, cc = rem % CPR;
+        *reinterpret_cast<u32x4 *>(tiles[k & 1][kv] + row * RB + ((cc ^ tile_swz(row, CPR)) << 4)) = ring[s][i];
+      }
+    }
+    __syncthreads();
+    if (!computes) return;
+    if (badk[s] && lane == 0) record_error(a.d_err, MKV_DEVERR_BLOCK);
+    const bool bad = badk[s];
+    u32x4 kq[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) kq[r] = *reinterpret_cast<const u32x4 *>(tk + k_rd[r]);
+    f32x4 S = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < NR; r++)
+      S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kq[r]), qop[r], S, 0, 0, 0);
+    // Lane holds S[key 16k + 4*g4 + i][query position qlo + lane%16].
+    const int kp0 = kPageSize * k + 4 * g4;
+    const bool full = !bad && kPageSize * k + kPageSize - 1 <= qlo && kPageSize * k + kPageSize <= ctx;
+    float x[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) x[i] = S[i] * a.sl2;
+    if (!full) {
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        if (bad || kp0 + i > qp || kp0 + i >= ctx) x[i] = -INFINITY;
+    }
+    float mloc = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+    const bool need = mloc > st.m + kRescaleSlack;
+    if (__ballot(need)) {
+      const float mn = need ? mloc : st.m;
+      const float al = fast_exp2(st.m - mn);
+      st.l *= al;
+#pragma unroll
+      for (int nn = 0; nn < NT; nn++) st.O[nn] *= al;
+      st.m = mn;
+    }
+    float pr[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) pr[i] = fast_exp2(x[i] - st.m);
+    if (!full) {  // a fully masked column has m = -inf: keep its p at 0, not NaN
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        if (x[i] == -INFINITY) pr[i] = 0.0f;
+    }
+    st.l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+    const uint32_t p01 = pack_bf16x2(pr[0], pr[1]), p23 = pack_bf16x2(pr[2], pr[3]);
+    const i16x4 pb = __builtin_bit_cast(i16x4, (uint64_t)p01 | ((uint64_t)p23 << 32));
+    // V rows past the context or of a rejected block are zeroed (stale
+    // slots may hold any bit pattern); causally hidden rows have p = 0.
+    uint64_t vmask = ~0ull;
+    if (!full) {
+      const int t0 = kPageSize * k + 4 * g4;
+      vmask = (bad || t0 >= ctx ? 0ull : 0xffffull) | (bad || t0 + 1 >= ctx ? 0ull : 0xffff0000ull) |
+              (bad || t0 + 2 >= ctx ? 0ull : 0xffff00000000ull) |
+              (bad || t0 + 3 >= ctx ? 0ull : 0xffff000000000000ull);
+    }
+#pragma unroll
+    for (int nn = 0; nn < NT; nn++) {
+      const i16x4s raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(tv + v_rd[nn]));
+      const uint64_t w = __builtin_bit_cast(uint64_t, raw) & vmask;
+      st.O[nn] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, w), pb, st.O[nn], 0, 0, 0);
+    }
+  };
+
+#pragma unroll
+  for (int s = 0; s < R - 1; s++) issue(ring[s], badk[s], s);
+  const int nfull = n / R;
+  int k0 = 0;
+  for (int it = 0; it < nfull; it++, k0 += R) {
+#pragma unroll
+    for (int s = 0; s < R; s++) stage(s, k0 + s);
+  }
+#pragma unroll
+  for (int s = 0; s < R - 1; s++)
+    if (k0 + s < n) stage(s, k0 + s);
+
+  if (!computes) return;
+  st.l += __shfl_xor(st.l, 16);
+  st.l += __shfl_xor(st.l, 32);
+  const int row = 16 * t + m16;
+  if (row >= nq) return;
+  const float f = final_scale(st.m, st.l, a.zero_sink);
+  uint16_t *op = reinterpret_cast<uint16_t *>(a.o) + ((int64_t)(q0 + row) * a.Hq + hq) * D + 4 * g4;
+#pragma unroll
+  for (int nn = 0; nn < NT; nn++)
+    *reinterpret_cast<uint2 *>(op + 16 * nn) = make_uint2(pack_bf16x2(st.O[nn][0] * f, st.O[nn][1] * f),
+                                                          pack_bf16x2(st.O[nn][2] * f, st.O[nn][3] * f));
+}
+
 template <int D, bool BF16>
 __global__ void __launch_bounds__(256) merge_planned_kernel(KArgs a, PlanDev pd) {
   const int lane = threadIdx.x & 63;
@@ -1688,4 +1890,61 @@ extern "C" int mkv_decode_step(mkv_pool *pool, const mkv_decode_plan *plan, int3
   if (!d_k_new || !d_v_new) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL new K/V rows");
   return launch_planned(reinterpret_cast<Pool *>(pool), reinterpret_cast<const Plan *>(plan), layer,
                         d_k_new, d_v_new, d_q, d_o, d_block_indptr, d_block_ids, scale, flags, stream);
+}
+
+extern "C" int mkv_extend_attention(mkv_pool *pool, int32_t layer, const void *d_q, void *d_o,
+                                    const int32_t *d_q_indptr, const int32_t *d_block_indptr,
+                                    const int32_t *d_block_ids, const int32_t *d_ctx_lens, int32_t num_seqs,
+                                    int32_t max_q_len, int32_t max_ctx_len, float scale, uint32_t flags,
+                                    void *stream) {
+  if (!pool) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL pool");
+  Pool *p = reinterpret_cast<Pool *>(pool);
+  const Geom &g = p->g;
+  bool use_mfma = false;
+  int rc = check_common(p, layer, flags, scale, use_mfma);
+  if (rc) return rc;
+  if (!use_mfma)
+    return set_error(MKV_ERR_INVALID_ARGUMENT,
+                     "extend attention needs a bf16 pool with head_dim 64/128/256");
+  if (!d_q || !d_o || !d_q_indptr || !d_block_indptr || !d_block_ids || !d_ctx_lens)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL device pointer");
+  if (num_seqs < 0 || max_q_len < 0 || max_ctx_len < 0)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "negative sizes");
+  if (num_seqs == 0 || max_q_len == 0) return MKV_OK;
+  if (max_q_len > max_ctx_len)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "max_q_len %d > max_ctx_len %d", max_q_len, max_ctx_len);
+  const int G = g.Hq / g.Hkv;
+  if (G > 16) return set_error(MKV_ERR_INVALID_ARGUMENT, "extend attention supports <= 16 query heads per KV head");
+  if (!aligned16(d_q) || !aligned16(d_o)) return set_error(MKV_ERR_INVALID_ARGUMENT, "q and o must be 16-byte aligned");
+  const int64_t tiles = ((int64_t)max_q_len + 15) / 16;
+  if (tiles > INT32_MAX || num_seqs > 65535 || g.Hkv > 65535)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "grid too large");
+  DeviceGuard guard(p->device);
+  hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  KArgs a = make_kargs(p, layer, d_q, d_o, d_block_indptr, d_block_ids, scale, flags, true);
+  ExtArgs e;
+  e.q_indptr = d_q_indptr;
+  e.ctx = d_ctx_lens;
+  e.B = num_seqs;
+  e.max_ctx = max_ctx_len;
+  const int W = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : G <= 8 ? 8 : 16;
+  const dim3 grid((unsigned)tiles, (unsigned)g.Hkv, (unsigned)num_seqs), block(64 * W);
+#define MKV_EXT(DD)                                                                       \
+  do {                                                                                    \
+    switch (W) {                                                                          \
+      case 1: hipLaunchKernelGGL((attn_extend_kernel<DD, 1>), grid, block, 0, hs, a, e); break;  \
+      case 2: hipLaunchKernelGGL((attn_extend_kernel<DD, 2>), grid, block, 0, hs, a, e); break;  \
+      case 4: hipLaunchKernelGGL((attn_extend_kernel<DD, 4>), grid, block, 0, hs, a, e); break;  \
+      case 8: hipLaunchKernelGGL((attn_extend_kernel<DD, 8>), grid, block, 0, hs, a, e); break;  \
+      default: hipLaunchKernelGGL((attn_extend_kernel<DD, 16>), grid, block, 0, hs, a, e); break; \
+    }                                                                                     \
+  } while (0)
+  switch (g.D) {
+    case 64: MKV_EXT(64); break;
+    case 128: MKV_EXT(128); break;
+    default: MKV_EXT(256); break;
+  }
+#undef MKV_EXT
+  MKV_CHECK_LAUNCH("attn_extend_kernel");
+  return MKV_OK;
 }

@@ -313,6 +313,32 @@ class DeviceKvPool:
         return out
 
     # -- planned path -------------------------------------------------------------------------
+    def extend_attention(self, layer: int, q, q_indptr, block_indptr, block_ids, ctx_lens,
+                         max_q_len: int, max_ctx_len: int, out=None, scale: float | None = None,
+                         zero_sink: bool = False, stream=None):
+        """Causal attention of each sequence's newest tokens (chunked prefill):
+        q, out: [q_indptr[-1], Hq, D]; sequence b's n_b = q_indptr[b+1] - q_indptr[b]
+        queries sit at positions [ctx_b - n_b, ctx_b) and attend keys 0..p."""
+        torch = _torch()
+        d = self.desc
+        B = q_indptr.shape[0] - 1
+        self._i32(q_indptr, "q_indptr", B + 1)
+        self._i32(block_indptr, "block_indptr", B + 1)
+        self._i32(block_ids, "block_ids")
+        self._i32(ctx_lens, "ctx_lens", B)
+        T = q.shape[0]
+        self._check_tensor(q, (T, d.num_q_heads, d.head_dim), "q")
+        if out is None:
+            out = torch.empty_like(q)
+        self._check_tensor(out, (T, d.num_q_heads, d.head_dim), "out")
+        if scale is None:
+            scale = float(np.float32(d.head_dim ** -0.5))
+        flags = ATTN_ZERO_SINK if zero_sink else 0
+        _raise(self._lib.mkv_extend_attention(
+            self._h, layer, _dptr(q), _dptr(out), _dptr(q_indptr), _dptr(block_indptr), _dptr(block_ids),
+            _dptr(ctx_lens), B, max_q_len, max_ctx_len, scale, flags, _stream_handle(stream)))
+        return out
+
     def plan(self, ctx_lens, pieces: int = 0, stream=None) -> "DecodePlan":
         """Work plan of one decode step from host context lengths (tokens
         attended per sequence, including the token appended this step)."""

@@ -187,6 +187,37 @@ def decode_attention(d: PoolDesc, pool: np.ndarray, layer: int, q: np.ndarray, i
     return o
 
 
+def extend_attention(d: PoolDesc, pool: np.ndarray, layer: int, q: np.ndarray, q_indptr, indptr, indices,
+                     ctx_len, scale: float | None = None, zero_sink: bool = False,
+                     precision: str = "f32") -> np.ndarray:
+    """Causal attention of each sequence's newest tokens, the seq_q > 1 path of
+    inference-model-qwen/src/model.rs:410-416 with the mask of model.rs:542-555:
+    query i of sequence b sits at position p = ctx_b - n_b + i and attends keys
+    0..p (the mask's -1e10 makes every later key's weight exactly 0 in f32).
+    That is, each query is a decode query over the first p + 1 tokens of its
+    sequence's table, which is how it is computed here (one virtual sequence
+    per query token). q: [sum n_b, Hq, D] f32 values."""
+    q_indptr = np.asarray(q_indptr, np.int64)
+    indptr = np.asarray(indptr, np.int64)
+    indices = np.asarray(indices, np.int32)
+    ctx_len = np.asarray(ctx_len, np.int64)
+    v_ptr, v_ids, v_ctx = [0], [], []
+    for b in range(ctx_len.size):
+        nb = int(q_indptr[b + 1] - q_indptr[b])
+        table = indices[indptr[b]:indptr[b + 1]]
+        for i in range(nb):
+            p = int(ctx_len[b]) - nb + i
+            need = p // d.page_size + 1
+            v_ids.append(table[:need])
+            v_ptr.append(v_ptr[-1] + need)
+            v_ctx.append(p + 1)
+    if not v_ctx:
+        return np.empty((0,) + q.shape[1:], np.float32 if precision == "f32" else np.float64)
+    return decode_attention(d, pool, layer, q, np.asarray(v_ptr, np.int32), np.concatenate(v_ids),
+                            np.asarray(v_ctx, np.int32), scale=scale, zero_sink=zero_sink,
+                            precision=precision)
+
+
 def ref_faithful_batch(ctx, Hkv: int, Hq: int, D: int, seed: int = 1) -> float:
     """Seconds for one reference-faithful decode step (one layer) of every
     sequence; ctx[b] counts the appended token."""

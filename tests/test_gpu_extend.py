@@ -1,0 +1,115 @@
+"""GPU parity of extend (chunked prefill) attention through the C ABI:
+each sequence's newest tokens attend causally over the whole cache,
+against the oracle (bf16 row-relative 2e-2), plus the identities the
+oracle tests pin (the chunk's last query equals decode attention) and the
+error paths."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from mitten_amd import BackendError, DeviceIndexError, DeviceKvPool, PoolDesc
+from mitten_amd import device_pool as dp
+from mitten_amd import workloads as wl
+from oracle import oracle as orc
+from tests.helpers import assert_attention_close, bits, normal, odesc, to_device, to_host, widen
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = {
+    # name: (Hq, Hkv, D): query heads per KV head G = 7, 8, 7, 4, 16, 1
+    "qwen7b": (28, 4, 128),
+    "gemma2b": (8, 1, 256),
+    "qwen0.5b": (14, 2, 64),
+    "llama8b": (32, 8, 128),
+    "g16": (64, 4, 128),
+    "mha": (4, 4, 64),
+}
+
+
+def _i32(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a, np.int32)).cuda()
+
+
+def _case(shape, ctx, nq, seed, zero_sink=False, layer=1):
+    Hq, Hkv, D = SHAPES[shape]
+    rng = wl.SplitMix64(seed)
+    batch = wl.decode_batch_from_contexts([c - 1 for c in ctx], rng, extra_blocks=2)
+    desc = PoolDesc(2, Hkv, Hq, D, batch.num_blocks, "bf16")
+    host = normal(seed + 1, desc.shape, "bf16")
+    q_indptr = np.concatenate([[0], np.cumsum(nq)]).astype(np.int32)
+    q = normal(seed + 2, (int(q_indptr[-1]), Hq, D), "bf16")
+    with DeviceKvPool(desc) as pool:
+        pool.write(host)
+        o = pool.extend_attention(layer, to_device(q), _i32(q_indptr), _i32(batch.block_indptr),
+                                  _i32(batch.block_ids), _i32(batch.ctx_lens), max(nq), max(ctx),
+                                  zero_sink=zero_sink)
+        pool.check()
+        got = to_host(o)
+        dec = None
+        if not zero_sink:  # the last query of each chunk is a decode query over the whole context
+            last = q_indptr[1:] - 1
+            dec = to_host(pool.decode_attention(layer, to_device(q[last]), _i32(batch.block_indptr),
+                                                _i32(batch.block_ids), _i32(batch.ctx_lens), max(ctx)))
+    ref = orc.extend_attention(odesc(desc), host, layer, widen(q), q_indptr, batch.block_indptr,
+                               batch.block_ids, batch.ctx_lens, zero_sink=zero_sink)
+    return got, ref, dec, q_indptr
+
+
+CTX = [1, 16, 17, 40, 200, 530, 97]
+NQ = [1, 16, 5, 40, 33, 512, 1]  # whole prompts, chunks after a prefix, a single token
+
+
+@pytest.mark.parametrize("shape", list(SHAPES))
+def test_extend_attention_matches_oracle(shape):
+    got, ref, dec, q_indptr = _case(shape, CTX, NQ, 90)
+    assert_attention_close(got, ref, "bf16")
+    last = q_indptr[1:] - 1
+    assert_attention_close(dec, ref[last], "bf16")
+
+
+def test_extend_attention_zero_sink():
+    got, ref, _, _ = _case("qwen7b", [1, 20, 300], [1, 20, 64], 91, zero_sink=True)
+    assert_attention_close(got, ref, "bf16")
+
+
+def test_extend_long_context_chunk():
+    """A 512-token chunk at the end of an 8k context (the pool-pressure
+    configuration's chunked prefill)."""
+    got, ref, _, _ = _case("qwen7b", [8192, 700], [512, 64], 92)
+    assert_attention_close(got, ref, "bf16")
+
+
+def test_extend_errors_are_reported():
+    Hq, Hkv, D = SHAPES["qwen7b"]
+    desc = PoolDesc(1, Hkv, Hq, D, 10, "bf16")
+    with DeviceKvPool(desc) as pool:
+        pool.write(normal(93, desc.shape, "bf16"))
+        q = to_device(normal(94, (4, Hq, D), "bf16"))
+        qi = _i32([0, 2, 4])
+        # block id outside the pool
+        pool.extend_attention(0, q, qi, _i32([0, 2, 4]), _i32([1, 2, 3, 10]), _i32([20, 30]), 2, 30)
+        with pytest.raises(DeviceIndexError) as ei:
+            pool.check()
+        assert ei.value.bits & dp.DEVERR_BLOCK
+        # table too short for the context
+        pool.extend_attention(0, q, qi, _i32([0, 1, 3]), _i32([1, 2, 3]), _i32([20, 30]), 2, 30)
+        with pytest.raises(DeviceIndexError) as ei:
+            pool.check()
+        assert ei.value.bits & dp.DEVERR_TABLE
+        # context beyond max_ctx_len
+        pool.extend_attention(0, q, qi, _i32([0, 2, 4]), _i32([1, 2, 3, 4]), _i32([20, 30]), 2, 25)
+        with pytest.raises(DeviceIndexError) as ei:
+            pool.check()
+        assert ei.value.bits & dp.DEVERR_CTX
+        with pytest.raises(BackendError):  # max_q_len > max_ctx_len
+            pool.extend_attention(0, q, qi, _i32([0, 2, 4]), _i32([1, 2, 3, 4]), _i32([20, 30]), 40, 30)
+    f32 = PoolDesc(1, 2, 14, 64, 4, "f32")
+    with DeviceKvPool(f32) as pool:
+        import torch
+
+        q = torch.zeros((2, 14, 64), dtype=torch.float32, device="cuda")
+        with pytest.raises(BackendError):  # needs a bf16 pool
+            pool.extend_attention(0, q, _i32([0, 2]), _i32([0, 1]), _i32([0]), _i32([2]), 2, 2)

@@ -13,7 +13,8 @@ gathers; within the attention tolerances for decode attention).
 * C5, pool pressure at Qwen-7B head shapes (1 of 28 layers): the
   217,982-block pool of a 200 GB budget, 512 sequences with log-normal
   lengths (median 2,048, sigma 1, capped at 32,768); per step 8 sequences
-  append a 512-token chunk and all others decode one token.
+  append a 512-token chunk and attend over it causally (extend attention),
+  and all others decode one token.
 """
 from __future__ import annotations
 
@@ -267,6 +268,24 @@ def test_c5_pool_pressure_chunked_append_and_decode():
             off = torch.from_numpy((slots % 16).astype(np.int64)).cuda()
             assert np.array_equal(to_host(view[0, 0, blk, off]), kc)
             assert np.array_equal(to_host(view[0, 1, blk, off]), vc)
+            # The chunks' causal attention over their whole caches (extend).
+            cptr, cids, cctx = bm.batch(chunk)
+            qc = normal(850 + step, (len(chunk) * C5_CHUNK, Hq, D), "bf16")
+            q_indptr = np.arange(len(chunk) + 1, dtype=np.int32) * C5_CHUNK
+            oc = to_host(pool.extend_attention(0, to_device(qc), _i32(q_indptr), _i32(cptr), _i32(cids),
+                                               _i32(cctx), C5_CHUNK, int(cctx.max())))
+            for r in (0, len(chunk) - 1):  # two chunk sequences, first / middle / last queries
+                table = cids[cptr[r]:cptr[r + 1]]
+                mini = np.ascontiguousarray(blocks_of(table)[None])
+                md = orc.desc(1, Hkv, D, len(table), 2)
+                rows = [0, 1, C5_CHUNK // 2, C5_CHUNK - 1]
+                pos = [int(cctx[r]) - C5_CHUNK + i for i in rows]
+                need = [p // 16 + 1 for p in pos]
+                vptr = np.concatenate([[0], np.cumsum(need)]).astype(np.int32)
+                vids = np.concatenate([np.arange(k, dtype=np.int32) for k in need])
+                ref = orc.decode_attention(md, mini, 0, widen(qc[[r * C5_CHUNK + i for i in rows]]), vptr, vids,
+                                           np.asarray([p + 1 for p in pos], np.int32))
+                assert_attention_close(oc[[r * C5_CHUNK + i for i in rows]], ref, "bf16")
             dec = [s for s in seqs if s not in chunk]
             new = np.concatenate([bm.append(s, 1)[0] for s in dec]).astype(np.int32)
             indptr, ids, ctx = bm.batch(dec)

@@ -384,3 +384,95 @@ def _np_attention_headmap(pool, q, indptr, ids, ctx, Hkv, scale):
             s = K[h % Hkv] @ q[b, h] * scale
             out[b, h] = scipy.special.softmax(s) @ V[h % Hkv]
     return out
+
+
+# ------------------------------------------------ extend (chunked prefill) ----
+
+
+def _np_causal_mask(seq, total):
+    """generate_causal_mask (inference-model-qwen/src/model.rs:542-555): row i
+    (cur_pos = total - seq + i) gets -1e10 for every column j > cur_pos."""
+    m = np.zeros((seq, total))
+    for i in range(seq):
+        m[i, total - seq + i + 1:] = -1e10
+    return m
+
+
+def _np_extend(pool, layer, q, q_indptr, indptr, ids, ctx, Hkv, scale, shift=0):
+    """float64 restatement of the reference's prefill attention, matrix form:
+    S = Q.K^T * scale + mask, softmax over keys, P.V (model.rs:410-416).
+    `shift` moves the mask's diagonal (only for planting a mistake)."""
+    T, Hq, D = q.shape
+    rep = Hq // Hkv
+    out = np.zeros((T, Hq, D))
+    p64 = _widen(pool).astype(np.float64)
+    for b in range(len(ctx)):
+        n = ctx[b]
+        lo, hi = q_indptr[b], q_indptr[b + 1]
+        tab = ids[indptr[b]:indptr[b + 1]]
+        t = np.arange(n)
+        K = np.repeat(p64[layer, 0, tab[t // 16], t % 16].transpose(1, 0, 2), rep, axis=0)
+        V = np.repeat(p64[layer, 1, tab[t // 16], t % 16].transpose(1, 0, 2), rep, axis=0)
+        mask = _np_causal_mask(hi - lo, n)
+        if shift:
+            mask = np.roll(mask, shift, axis=1)
+            mask[:, :shift] = 0.0 if shift > 0 else mask[:, :shift]
+        s = np.einsum("thd,hkd->htk", q[lo:hi].astype(np.float64), K) * scale + mask[None]
+        out[lo:hi] = np.einsum("htk,hkd->thd", scipy.special.softmax(s, axis=-1), V)
+    return out
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,es", CASES)
+def test_extend_attention_against_masked_matrix_restatement(Hq, Hkv, D, es):
+    ctx = [1, 16, 40, 75, 33]
+    nq = [1, 16, 17, 5, 33]  # whole prompt (prefix 0), chunks after a prefix
+    nblocks = sum((c + 15) // 16 for c in ctx) + 2
+    d, pool = _pool(2, Hkv, D, nblocks, es, 40)
+    indptr, ids = _tables(ctx, nblocks, 41)
+    q_indptr = np.concatenate([[0], np.cumsum(nq)]).astype(np.int32)
+    q = np.random.default_rng(42).standard_normal((int(q_indptr[-1]), Hq, D), dtype=np.float32)
+    scale = float(np.float32(D ** -0.5))
+    want = _np_extend(pool, 1, q, q_indptr, indptr, ids, ctx, Hkv, scale)
+    got = orc.extend_attention(d, pool, 1, q, q_indptr, indptr, ids, ctx)
+    assert np.max(np.abs(got - want)) < 2e-6
+    got64 = orc.extend_attention(d, pool, 1, q, q_indptr, indptr, ids, ctx, precision="f64")
+    assert np.max(np.abs(got64 - want)) < 1e-12
+
+
+def test_extend_attention_identities():
+    Hq, Hkv, D = 4, 2, 32
+    ctx, nq = [37, 20], [9, 20]
+    d, pool = _pool(1, Hkv, D, 8, 4, 43)
+    indptr, ids = _tables(ctx, 8, 44)
+    q_indptr = np.array([0, 9, 29], np.int32)
+    q = np.random.default_rng(45).standard_normal((29, Hq, D), dtype=np.float32)
+    o = orc.extend_attention(d, pool, 0, q, q_indptr, indptr, ids, ctx)
+    # The chunk's last query is a plain decode query over the whole context.
+    dec = orc.decode_attention(d, pool, 0, q[[8, 28]], indptr, ids, ctx)
+    assert np.array_equal(o[[8, 28]], dec)
+    # The first query of a whole prompt (position 0) sees one key: O = v_0.
+    for h in range(Hq):
+        assert np.allclose(o[9, h], pool[0, 1, ids[indptr[1]], 0, h // (Hq // Hkv)], atol=1e-7)
+
+
+def test_extend_checks_detect_planted_mistakes():
+    """A diagonal off by one either way, or no mask at all, moves the result
+    far outside the f32 tolerance."""
+    Hq, Hkv, D = 4, 2, 32
+    ctx, nq = [50], [20]
+    d, pool = _pool(1, Hkv, D, 5, 4, 46)
+    indptr, ids = _tables(ctx, 5, 47)
+    q_indptr = np.array([0, 20], np.int32)
+    q = np.random.default_rng(48).standard_normal((20, Hq, D), dtype=np.float32)
+    scale = float(np.float32(D ** -0.5))
+    good = orc.extend_attention(d, pool, 0, q, q_indptr, indptr, ids, ctx)
+    assert np.max(np.abs(good - _np_extend(pool, 0, q, q_indptr, indptr, ids, ctx, Hkv, scale))) < 2e-6
+    every_query_sees_all = _np_attention(pool, 0, q, np.arange(21, dtype=np.int32) * len(ids),
+                                         np.tile(ids, 20), [50] * 20, Hkv, scale)
+    wrong = {
+        "diagonal one later": _np_extend(pool, 0, q, q_indptr, indptr, ids, ctx, Hkv, scale, shift=1),
+        "diagonal one earlier": _np_extend(pool, 0, q, q_indptr, indptr, ids, ctx, Hkv, scale, shift=-1),
+        "no causal mask": every_query_sees_all,
+    }
+    for name, w in wrong.items():
+        assert np.max(np.abs(good - w)) > 1e-3, name
