@@ -10,6 +10,7 @@
  *   copy_blocks       copy-on-write block copies and batched block moves
  *   decode_attention  GQA/MQA paged decode attention straight from the pool
  *   extend_attention  causal attention of a chunk of new tokens (chunked prefill)
+ *   qk_norm_rope_append  q/k RMSNorm + partial RoPE, fused with the K/V append
  *
  * Pool layout in HBM (design/rust-inference-engine-design.md:1380-1387):
  *   [num_layers][2 (K then V)][num_blocks][page_size][num_kv_heads][head_dim]
@@ -77,6 +78,12 @@ enum {
   MKV_ATTN_PER_HEAD_LOADS = 1u << 3 /* planned MFMA path: one wave per KV head loads its
                                        own rows, instead of the workgroup loading whole
                                        token rows of every head (same results) */
+};
+
+/* qk_norm_rope_append flags. */
+enum {
+  MKV_PREP_PLAIN_Q = 1u << 0, /* d_q is [n][num_q_heads][head_dim] (no gate half) */
+  MKV_PREP_NO_NORM = 1u << 1  /* skip the RMSNorm (RoPE and append only) */
 };
 
 typedef struct mkv_pool mkv_pool;
@@ -229,6 +236,32 @@ MKV_API int mkv_extend_attention(mkv_pool *pool, int32_t layer, const void *d_q,
                                  const int32_t *d_block_ids, const int32_t *d_ctx_lens, int32_t num_seqs,
                                  int32_t max_q_len, int32_t max_ctx_len, float scale, uint32_t flags,
                                  void *stream);
+
+/* ---- fused pre-attention step --------------------------------------------- */
+
+/* For each token t of one layer: RMSNorm of every q head and k head,
+ *   x * (mean(x^2) + eps)^-1/2 * (1 + w)   (w = d_q_norm_w or d_k_norm_w, [head_dim] f32),
+ * then NeoX RoPE on dims [0, rotary_dim) at position d_positions[t]: for
+ * i < rotary_dim/2, angle a = pos * d_inv_freq[i],
+ *   x[i] -> x[i]*cos a - x[i+half]*sin a,  x[i+half] -> x[i+half]*cos a + x[i]*sin a,
+ * dims >= rotary_dim unchanged. The prepared k row and the unchanged v row are
+ * appended at slot d_slot_mapping[t] (as mkv_append); the prepared q rows go
+ * to d_q_out [num_tokens][num_q_heads][head_dim]. All in the pool dtype,
+ * computed in f32 with one rounding per output element.
+ * d_q: [num_tokens][num_q_heads][2][head_dim] (q then gate, the q_proj output)
+ * or, with MKV_PREP_PLAIN_Q, [num_tokens][num_q_heads][head_dim].
+ * d_k, d_v: [num_tokens][num_kv_heads][head_dim]. d_inv_freq: [rotary_dim/2]
+ * f32, the reference's 1 / theta^(2i/rotary_dim). rotary_dim must be a
+ * multiple of 2*max(1, head_dim/64); head_dim 32/64/128/256.
+ * With MKV_PREP_NO_NORM the weights may be NULL and eps is ignored.
+ * Replaces, for one layer, inference-model-qwen/src/model.rs:371-392:
+ * the q slice of the gated q_proj (:371-374), RmsNorm::forward4 (:104-108),
+ * apply_rope (:508-540) on q and k, and the cache append (:390-392). */
+MKV_API int mkv_qk_norm_rope_append(mkv_pool *pool, int32_t layer, const void *d_q, const void *d_k,
+                                    const void *d_v, const float *d_q_norm_w, const float *d_k_norm_w,
+                                    const float *d_inv_freq, int32_t rotary_dim, float eps,
+                                    const int32_t *d_positions, const int32_t *d_slot_mapping,
+                                    int32_t num_tokens, void *d_q_out, uint32_t flags, void *stream);
 
 /* ---- host-side validation (pure CPU; no device access) ------------------- */
 

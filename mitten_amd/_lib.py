@@ -54,6 +54,7 @@ DEVICE_SIGNATURES = {
     "mkv_decode_attention_planned": (c_int, [P, P, i32, P, P, P, P, f32, u32, P]),
     "mkv_decode_step": (c_int, [P, P, i32, P, P, P, P, P, P, f32, u32, P]),
     "mkv_extend_attention": (c_int, [P, i32, P, P, P, P, P, P, i32, i32, i32, f32, u32, P]),
+    "mkv_qk_norm_rope_append": (c_int, [P, i32, P, P, P, P, P, P, i32, f32, P, P, i32, P, u32, P]),
     "mkv_validate_slots": (c_int, [DESC_P, I32P, i32]),
     "mkv_validate_block_tables": (c_int, [DESC_P, I32P, I32P, I32P, i32, i32]),
     "mkv_validate_copy_pairs": (c_int, [DESC_P, I32P, I32P, i32]),

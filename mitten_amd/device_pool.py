@@ -36,6 +36,7 @@ MKV_ERR_NO_DEVICE = 5
 DEVERR_SLOT, DEVERR_BLOCK, DEVERR_TABLE, DEVERR_COPY, DEVERR_CTX = 1, 2, 4, 8, 16
 
 ATTN_ZERO_SINK, ATTN_FORCE_VALU, ATTN_FORCE_MFMA, ATTN_PER_HEAD_LOADS = 1, 2, 4, 8
+PREP_PLAIN_Q, PREP_NO_NORM = 1, 2
 
 DTYPES = {"f32": 0, "bf16": 1}
 PAGE_SIZE = 16
@@ -104,6 +105,15 @@ class PoolDesc:
     @property
     def shape(self):
         return (self.num_layers, 2, self.num_blocks, self.page_size, self.num_kv_heads, self.head_dim)
+
+
+def rope_inv_freq(rotary_dim: int, theta: float) -> np.ndarray:
+    """The reference's RoPE frequency table, f32 throughout:
+    1 / (theta as f32)^(2i / rotary_dim) for i < rotary_dim / 2
+    (inference-model-qwen/src/model.rs:512-514)."""
+    i = np.arange(rotary_dim // 2, dtype=np.float32)
+    expo = (np.float32(2.0) * i) / np.float32(rotary_dim)
+    return (np.float32(1.0) / np.power(np.float32(theta), expo)).astype(np.float32)
 
 
 def required_bytes(desc: PoolDesc) -> int:
@@ -337,6 +347,46 @@ class DeviceKvPool:
         _raise(self._lib.mkv_extend_attention(
             self._h, layer, _dptr(q), _dptr(out), _dptr(q_indptr), _dptr(block_indptr), _dptr(block_ids),
             _dptr(ctx_lens), B, max_q_len, max_ctx_len, scale, flags, _stream_handle(stream)))
+        return out
+
+    def qk_norm_rope_append(self, layer: int, q, k, v, positions, slot_mapping, q_norm_w=None,
+                            k_norm_w=None, inv_freq=None, eps: float = 1e-6, gated: bool = True,
+                            out=None, stream=None):
+        """Fused pre-attention step of one layer (inference-model-qwen/src/model.rs:371-392):
+        RMSNorm(1 + w) of the q and k heads, NeoX RoPE on the first 2*len(inv_freq)
+        dims at `positions`, k and v appended at `slot_mapping`; returns the prepared
+        q [n, Hq, D]. q is [n, Hq, 2, D] (q then gate) when `gated`, else [n, Hq, D].
+        Weights None skips the norm; inv_freq None skips RoPE."""
+        torch = _torch()
+        d = self.desc
+        n = slot_mapping.shape[0]
+        self._i32(slot_mapping, "slot_mapping", n)
+        self._i32(positions, "positions", n)
+        qshape = (n, d.num_q_heads, 2, d.head_dim) if gated else (n, d.num_q_heads, d.head_dim)
+        self._check_tensor(q, qshape, "q")
+        self._check_tensor(k, (n, d.num_kv_heads, d.head_dim), "k")
+        self._check_tensor(v, (n, d.num_kv_heads, d.head_dim), "v")
+        flags = 0 if gated else PREP_PLAIN_Q
+        if (q_norm_w is None) != (k_norm_w is None):
+            raise BackendError(MKV_ERR_INVALID_ARGUMENT, "give both norm weights or neither")
+        if q_norm_w is None:
+            flags |= PREP_NO_NORM
+        else:
+            self._check_tensor(q_norm_w, (d.head_dim,), "q_norm_w", dtype=torch.float32)
+            self._check_tensor(k_norm_w, (d.head_dim,), "k_norm_w", dtype=torch.float32)
+        rd = 0
+        if inv_freq is not None:
+            self._check_tensor(inv_freq, None, "inv_freq", dtype=torch.float32)
+            rd = 2 * inv_freq.shape[0]
+        if out is None:
+            out = torch.empty((n, d.num_q_heads, d.head_dim), dtype=self.torch_dtype, device=q.device)
+        self._check_tensor(out, (n, d.num_q_heads, d.head_dim), "out")
+        nul = ctypes.c_void_p(0)
+        _raise(self._lib.mkv_qk_norm_rope_append(
+            self._h, layer, _dptr(q), _dptr(k), _dptr(v),
+            nul if q_norm_w is None else _dptr(q_norm_w), nul if k_norm_w is None else _dptr(k_norm_w),
+            nul if inv_freq is None else _dptr(inv_freq), rd, eps, _dptr(positions), _dptr(slot_mapping),
+            n, _dptr(out), flags, _stream_handle(stream)))
         return out
 
     def plan(self, ctx_lens, pieces: int = 0, stream=None) -> "DecodePlan":

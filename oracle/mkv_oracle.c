@@ -24,6 +24,11 @@
  *   orc_decode_attention inference-model-qwen/src/model.rs:394-416 (GQA repeat,
  *                        q.k^T * scaling, additive causal mask, softmax, .v),
  *                        scaling = head_dim^-0.5 (model.rs:298)
+ *   orc_norm_rope_rows   inference-model-qwen/src/model.rs:104-108 (RmsNorm::forward4:
+ *                        x * (mean(x^2) + eps)^-1/2 * (w + 1)) followed by
+ *                        model.rs:508-540 (apply_rope, NeoX half-rotation of
+ *                        dims [0, rotary_dim), the rest passed through), as
+ *                        GatedAttention::forward applies them (model.rs:380-384)
  *   orc_ref_faithful_*   the same attention, executed the way the reference
  *                        executes it (contiguous cache grown by a copy per
  *                        token, repeat_kv materialised, mask built per call);
@@ -195,6 +200,35 @@ ORC_API int orc_copy_blocks(const orc_pool_desc *d, uint8_t *pool, const int32_t
         memmove(pool + plane_off(d, l, kv, dst[i]), pool + plane_off(d, l, kv, src[i]), bb);
   }
   return 0;
+}
+
+/* RMSNorm then partial NeoX RoPE, in place, on `rows` rows of D f32 values
+ * (model.rs:104-108, 508-540). Row r sits at position pos[r]. w == NULL skips
+ * the norm. All arithmetic f32 in the reference's order: the mean of squares,
+ * + eps, sqrt, reciprocal, x * that, then * (w + 1); then for i < half =
+ * rotary_dim/2, a = (float)pos * inv_freq[i],
+ *   x[i] * cos a - x[i+half] * sin a,  x[i+half] * cos a + x[i] * sin a.
+ * (Built with -std=c11: no contraction into FMAs.) */
+ORC_API void orc_norm_rope_rows(float *x, int64_t rows, int32_t D, const float *w, float eps,
+                                const float *inv_freq, int32_t rotary_dim, const int32_t *pos) {
+  const int half = rotary_dim / 2;
+  for (int64_t r = 0; r < rows; r++) {
+    float *row = x + r * D;
+    if (w) {
+      float ss = 0.0f;
+      for (int i = 0; i < D; i++) ss += row[i] * row[i];
+      const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+      for (int i = 0; i < D; i++) row[i] = (row[i] * inv) * (w[i] + 1.0f);
+    }
+    const float p = (float)pos[r];
+    for (int i = 0; i < half; i++) {
+      const float a = p * inv_freq[i];
+      const float c = cosf(a), sn = sinf(a);
+      const float x1 = row[i], x2 = row[i + half];
+      row[i] = x1 * c - x2 * sn;
+      row[i + half] = x2 * c + x1 * sn;
+    }
+  }
 }
 
 /* Element load from the pool as f32 (bf16 is widened exactly). */

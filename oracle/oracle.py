@@ -58,6 +58,7 @@ def lib():
             "orc_append": (i64, [dp, P, ctypes.c_int, P, P, P, i64]),
             "orc_gather": (ctypes.c_int, [dp, P, ctypes.c_int, P, P, P, i32, P, P]),
             "orc_copy_blocks": (ctypes.c_int, [dp, P, P, P, i64]),
+            "orc_norm_rope_rows": (None, [P, i64, i32, P, f32, P, i32, P]),
             "orc_decode_attention_f32": (ctypes.c_int, [dp, P, ctypes.c_int, P, i32, i32, P, P, P,
                                                         f32, ctypes.c_int, P]),
             "orc_decode_attention_f64": (ctypes.c_int, [dp, P, ctypes.c_int, P, i32, i32, P, P, P,
@@ -159,6 +160,50 @@ def copy_blocks(d: PoolDesc, pool: np.ndarray, src, dst) -> None:
     dst = np.ascontiguousarray(dst, np.int32)
     if lib().orc_copy_blocks(ctypes.byref(d), _p(pool), _p(src), _p(dst), src.size) != 0:
         raise ValueError("orc_copy_blocks: block id out of range")
+
+
+def norm_rope_rows(x: np.ndarray, w, eps: float, inv_freq, pos) -> np.ndarray:
+    """RMSNorm(1 + w) then partial NeoX RoPE of each row (model.rs:104-108,
+    508-540); x: [..., D] f32 values, pos: one position per row of x[..., 0]
+    (broadcast over the middle axes by the caller). w None skips the norm,
+    inv_freq None (or empty) skips RoPE. Returns a new f32 array."""
+    y = np.array(x, dtype=np.float32, order="C", copy=True)
+    D = y.shape[-1]
+    rows = y.size // D
+    pos = np.ascontiguousarray(pos, np.int32).reshape(-1)
+    if pos.size != rows:
+        raise ValueError("one position per row")
+    wv = None if w is None else np.ascontiguousarray(w, np.float32)
+    f = np.zeros(0, np.float32) if inv_freq is None else np.ascontiguousarray(inv_freq, np.float32)
+    lib().orc_norm_rope_rows(_p(y), rows, D, None if wv is None else _p(wv), float(np.float32(eps)),
+                             _p(f) if f.size else None, 2 * f.size, _p(pos))
+    return y
+
+
+def qk_norm_rope_append(d: PoolDesc, pool: np.ndarray, layer: int, q: np.ndarray, k: np.ndarray,
+                        v: np.ndarray, q_w, k_w, inv_freq, eps: float, positions, slots) -> np.ndarray:
+    """The fused pre-attention step of GatedAttention::forward
+    (inference-model-qwen/src/model.rs:371-392) on one layer: q [n, Hq, 2, D]
+    (q then gate) or [n, Hq, D], k, v [n, Hkv, D] as f32 values; q and k heads
+    are normed and rotated at their token's position, k (rounded to the pool
+    dtype) and v are appended at `slots` in place; returns q in the pool
+    dtype's storage (np.uint16 bf16 bits or f32)."""
+    q = np.asarray(q, np.float32)
+    if q.ndim == 4:
+        q = q[:, :, 0, :]
+    n, Hq, D = q.shape
+    Hkv = k.shape[1]
+    pos = np.asarray(positions, np.int32)
+    qo = norm_rope_rows(q, q_w, eps, inv_freq, np.repeat(pos, Hq))
+    ko = norm_rope_rows(np.asarray(k, np.float32), k_w, eps, inv_freq, np.repeat(pos, Hkv))
+    if d.elem_bytes == 2:
+        qo, ko, vs = f32_to_bf16(qo), f32_to_bf16(ko), f32_to_bf16(np.asarray(v, np.float32))
+    else:
+        vs = np.ascontiguousarray(v, np.float32)
+    bad = append(d, pool, layer, np.ascontiguousarray(ko), np.ascontiguousarray(vs), slots)
+    if bad >= 0:
+        raise ValueError(f"slot of token {bad} outside the pool")
+    return qo
 
 
 def decode_attention(d: PoolDesc, pool: np.ndarray, layer: int, q: np.ndarray, indptr, indices,
