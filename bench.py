@@ -14,6 +14,10 @@ oracle's reference-faithful restatement of the reference's CPU attention,
 timed on a bounded sample on this host).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+`--op prep` measures the fused pre-attention kernel instead (q/k RMSNorm +
+NeoX RoPE + K/V append, mkv_qk_norm_rope_append) on a prefill chunk of
+`--tokens` tokens at the same head geometry, and prints its own JSON line.
 """
 from __future__ import annotations
 
@@ -51,6 +55,10 @@ def parse():
                     help="time the steps without per-launch HIP events (roofline fields null)")
     ap.add_argument("--cpu-layers", type=int, default=5,
                     help="layers of the batch in the CPU baseline sample")
+    ap.add_argument("--op", choices=["decode", "prep"], default="decode",
+                    help="decode: the decode step (headline); prep: the fused q/k-norm + RoPE + "
+                         "append kernel on a prefill chunk")
+    ap.add_argument("--tokens", type=int, default=16384, help="--op prep: tokens in the chunk")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 1 GiB device to device (the known-size kernel that scales "
                          "rocprofv3's FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -135,6 +143,99 @@ def cpu_baseline(cfg, batch, step_bytes, layers):
     }
 
 
+def bench_prep(args):
+    """The fused pre-attention kernel on one prefill chunk: `--tokens` tokens
+    of one layer, q as the gated q_proj output [n, Hq, 2, D], RMSNorm(1 + w)
+    on q and k, RoPE over the whole head (theta 1e6), k and v appended at the
+    slots of freshly allocated blocks drawn from a seeded permutation of the
+    pool. One launch per step; HIP events on the launch stream."""
+    import torch
+
+    from mitten_amd import DeviceKvPool, PoolDesc
+    from mitten_amd import workloads as wl
+    from mitten_amd.device_pool import rope_inv_freq
+
+    cfg = wl.CONFIGS[args.config]
+    Hq, Hkv, D, dt = cfg["num_q_heads"], cfg["num_kv_heads"], cfg["head_dim"], cfg["dtype"]
+    n, rd = args.tokens, D
+    nblocks = (n + 15) // 16 * 2
+    desc = PoolDesc(1, Hkv, Hq, D, nblocks, dt)
+    dev = torch.device("cuda:0")
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    rng = wl.SplitMix64(wl.BASE_SEED + 17)
+    perm = wl.permutation(nblocks, rng)
+    pos = np.arange(n, dtype=np.int64)
+    slots = (perm[pos // 16].astype(np.int64) * 16 + pos % 16).astype(np.int32)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(wl.BASE_SEED + 17)
+    q = torch.randn((n, Hq, 2, D), generator=gen, device=dev, dtype=torch.float32).to(tdt)
+    k = torch.randn((n, Hkv, D), generator=gen, device=dev, dtype=torch.float32).to(tdt)
+    v = torch.randn((n, Hkv, D), generator=gen, device=dev, dtype=torch.float32).to(tdt)
+    wq = (torch.rand(D, generator=gen, device=dev) - 0.5) * 0.2
+    wk = (torch.rand(D, generator=gen, device=dev) - 0.5) * 0.2
+    freq = torch.from_numpy(rope_inv_freq(rd, 1e6)).to(dev)
+    i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(dev)
+    pos_d, slots_d = i32(pos), i32(slots)
+    out = torch.empty((n, Hq, D), dtype=tdt, device=dev)
+    stream = torch.cuda.current_stream()
+    launch_bytes = wl.algorithmic_bytes_prep(n, Hq, Hkv, D, desc.elem_bytes, rd, True)
+    with DeviceKvPool(desc) as pool:
+        def step():
+            pool.qk_norm_rope_append(0, q, k, v, pos_d, slots_d, wq, wk, freq, eps=1e-6, out=out,
+                                     stream=stream)
+
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        pool.check()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(args.steps):
+            step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        pool.check()
+    launch_s = e0.elapsed_time(e1) / 1e3 / args.steps
+    gbs = launch_bytes / launch_s / 1e9
+    # CPU baseline: the oracle's restatement on a 2048-token sample.
+    from oracle import oracle as orc
+
+    sample = min(n, 2048)
+    qh = np.random.default_rng(0).standard_normal((sample, Hq, D)).astype(np.float32)
+    kh = np.random.default_rng(1).standard_normal((sample, Hkv, D)).astype(np.float32)
+    wh = np.zeros(D, np.float32)
+    fh = rope_inv_freq(rd, 1e6)
+    c0 = time.perf_counter()
+    reps = 0
+    while time.perf_counter() - c0 < 2.0 or reps == 0:
+        orc.norm_rope_rows(qh, wh, 1e-6, fh, np.repeat(pos[:sample], Hq))
+        orc.norm_rope_rows(kh, wh, 1e-6, fh, np.repeat(pos[:sample], Hkv))
+        reps += 1
+    cpu_s = (time.perf_counter() - c0) / reps
+    cpu_gbs = wl.algorithmic_bytes_prep(sample, Hq, Hkv, D, desc.elem_bytes, rd, True) / cpu_s / 1e9
+    print(json.dumps({
+        "metric": "fused q/k RMSNorm + RoPE + K/V append achieved HBM GB/s",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(launch_s * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": dt,
+        "data": "synthetic: N(0,1) q/k/v from a seed; slots of a seeded block permutation",
+        "config": {"workload": f"{args.config}-shaped prefill chunk, fused pre-attention step",
+                   "tokens": n, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "rotary_dim": rd,
+                   "q_layout": "gated [n, Hq, 2, D]", "norm": "RMSNorm(1 + w), eps 1e-6"},
+        "tokens_per_s": round(n / launch_s, 1),
+        "wall_ms_per_step": round(elapsed / args.steps * 1e3, 4),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "mkv_qk_norm_rope_append", "bytes_per_launch": launch_bytes,
+                     "avg_launch_us": round(launch_s * 1e6, 2)},
+        "cpu_baseline": {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                         "sample": f"oracle norm + RoPE of {sample} tokens' q and k rows, f32, "
+                                   f"{reps} repetitions"},
+    }), flush=True)
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -144,6 +245,9 @@ def main():
         print(f"bench.py measures one GPU: every box here has one MI355X and this path runs "
               f"on a single device (requested --gpus {args.gpus}).", file=sys.stderr)
         sys.exit(2)
+    if args.op == "prep":
+        bench_prep(args)
+        return
     import torch
 
     from mitten_amd import DeviceKvPool, PoolDesc

@@ -144,3 +144,12 @@ def algorithmic_bytes_append(num_tokens: int, num_kv_heads: int, head_dim: int,
                              elem_bytes: int) -> int:
     """K and V rows read and written + slot ids."""
     return 4 * num_tokens * num_kv_heads * head_dim * elem_bytes + 4 * num_tokens
+
+
+def algorithmic_bytes_prep(num_tokens: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                           elem_bytes: int, rotary_dim: int, norm: bool) -> int:
+    """Fused pre-attention step: q rows read (the q half of the gated
+    projection) and written, k and v rows read and written, positions and
+    slot ids, plus the norm weights and the frequency table."""
+    rows = num_tokens * (2 * num_q_heads + 4 * num_kv_heads) * head_dim * elem_bytes
+    return rows + 8 * num_tokens + (8 * head_dim if norm else 0) + 2 * rotary_dim
