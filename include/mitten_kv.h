@@ -11,6 +11,8 @@
  *   decode_attention  GQA/MQA paged decode attention straight from the pool
  *   extend_attention  causal attention of a chunk of new tokens (chunked prefill)
  *   qk_norm_rope_append  q/k RMSNorm + partial RoPE, fused with the K/V append
+ *   wire_export / wire_import  blocks to / from a checksummed byte payload
+ *                     (offload to host or disk, handoff between pools)
  *
  * Pool layout in HBM (design/rust-inference-engine-design.md:1380-1387):
  *   [num_layers][2 (K then V)][num_blocks][page_size][num_kv_heads][head_dim]
@@ -66,7 +68,8 @@ enum {
   MKV_DEVERR_BLOCK = 1u << 1,       /* gather/attention: block id outside the pool */
   MKV_DEVERR_TABLE = 1u << 2,       /* block table shorter than ceil(ctx/page_size) */
   MKV_DEVERR_COPY = 1u << 3,        /* copy_blocks: src or dst outside the pool */
-  MKV_DEVERR_CTX = 1u << 4          /* context length < 1 or > the max_ctx_len given */
+  MKV_DEVERR_CTX = 1u << 4,         /* context length < 1 or > the max_ctx_len given */
+  MKV_DEVERR_CHECKSUM = 1u << 5     /* wire import: a block's payload checksum differs */
 };
 
 /* decode_attention flags. */
@@ -262,6 +265,67 @@ MKV_API int mkv_qk_norm_rope_append(mkv_pool *pool, int32_t layer, const void *d
                                     const float *d_inv_freq, int32_t rotary_dim, float eps,
                                     const int32_t *d_positions, const int32_t *d_slot_mapping,
                                     int32_t num_tokens, void *d_q_out, uint32_t flags, void *stream);
+
+/* ---- KV block wire format --------------------------------------------------- */
+
+/* Blocks leave and enter a pool as a payload of
+ *   [num_blocks][num_layers][2 (K, V)][page_size][num_kv_heads][head_dim]
+ * (pool dtype, block-major: one block's state is contiguous) with one u64
+ * checksum per block: over the block's payload as little-endian u64 words
+ * w_0 .. w_{m-1},
+ *   sum64 = sum_j mix(w_j + (j + 1) * 0x9E3779B97F4A7C15)  (mod 2^64),
+ *   mix(z): z = (z ^ z>>30) * 0xBF58476D1CE4E5B9; z = (z ^ z>>27) * 0x94D049BB133111EB; z ^ z>>31.
+ * A file or message is: mkv_wire_header (64 bytes) | num_blocks checksums
+ * (u64) | zero padding | payload at header.payload_offset (a multiple of
+ * 4096). All fields little-endian.
+ * The reference hands pages between workers as indices into one pool
+ * (KvHandoff { request_id, kv_pages, cached_len },
+ * design/phase2b-deliverable.md:272-289) and plans per-layer KV files for
+ * SSD offload (KvOffloadManager, design/phase1-deliverable.md:253-339); this
+ * is the byte form of both: a handoff carries all layers of a request's
+ * pages, an offload chunk one layer (num_layers = 1). */
+#define MKV_WIRE_MAGIC 0x57564B4Du /* "MKVW" */
+#define MKV_WIRE_VERSION 1u
+
+typedef struct mkv_wire_header {
+  uint32_t magic;          /* MKV_WIRE_MAGIC */
+  uint16_t version;        /* MKV_WIRE_VERSION */
+  uint16_t dtype;          /* MKV_DTYPE_* */
+  int32_t page_size;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t layer_begin;     /* first layer carried */
+  int32_t num_layers;      /* layers carried */
+  int32_t num_blocks;
+  int64_t cached_len;      /* tokens the blocks hold (KvHandoff.cached_len) */
+  uint64_t block_bytes;    /* payload bytes per block */
+  uint64_t payload_offset; /* byte offset of the payload from the header's start */
+  uint64_t reserved;       /* 0 */
+} mkv_wire_header;
+
+/* Copy layers [layer_begin, layer_begin + num_layers) of blocks
+ * d_block_ids[0..num_blocks) into d_payload (num_blocks * block_bytes) and
+ * their checksums into d_checksums[num_blocks]. An id outside the pool is
+ * skipped and reported (MKV_DEVERR_BLOCK). At most 65535 blocks per call.
+ * No reference counterpart (see above); the read side of a handoff or an
+ * offload write-back. */
+MKV_API int mkv_wire_export(mkv_pool *pool, const int32_t *d_block_ids, int32_t num_blocks,
+                            int32_t layer_begin, int32_t num_layers, void *d_payload, uint64_t *d_checksums,
+                            void *stream);
+/* Copy d_payload into blocks d_block_ids (distinct; see
+ * mkv_validate_copy_pairs) and write the checksums of the payload as
+ * received to d_checksums. With d_expected non-NULL, a block whose checksum
+ * differs sets MKV_DEVERR_CHECKSUM (its bytes are still written: import into
+ * fresh blocks and release them if mkv_pool_check reports it). */
+MKV_API int mkv_wire_import(mkv_pool *pool, const int32_t *d_block_ids, int32_t num_blocks,
+                            int32_t layer_begin, int32_t num_layers, const void *d_payload,
+                            const uint64_t *d_expected, uint64_t *d_checksums, void *stream);
+/* Fill a header for a payload of this pool (pure CPU). */
+MKV_API int mkv_wire_header_init(const mkv_pool_desc *desc, int32_t layer_begin, int32_t num_layers,
+                                 int32_t num_blocks, int64_t cached_len, mkv_wire_header *out);
+/* MKV_OK if the header is a version this library reads and its geometry
+ * fits the pool (pure CPU). */
+MKV_API int mkv_wire_header_check(const mkv_pool_desc *desc, const mkv_wire_header *header);
 
 /* ---- host-side validation (pure CPU; no device access) ------------------- */
 

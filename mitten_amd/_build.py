@@ -20,7 +20,7 @@ INCLUDE = os.path.join(REPO, "include")
 DEVICE_LIB = os.path.join(LIBDIR, "libmitten_kv.so")
 HOST_LIB = os.path.join(LIBDIR, "libmitten_kvhost.so")
 
-DEVICE_SOURCES = ["mkv_pool.hip", "mkv_attention.hip", "mkv_prep.hip"]
+DEVICE_SOURCES = ["mkv_pool.hip", "mkv_attention.hip", "mkv_prep.hip", "mkv_wire.hip"]
 HOST_SOURCES = ["host/kv_host.cpp"]
 
 ARCH = "gfx950"

@@ -31,7 +31,26 @@ class PoolDescC(ctypes.Structure):
     ]
 
 
+class WireHeaderC(ctypes.Structure):
+    _fields_ = [
+        ("magic", ctypes.c_uint32),
+        ("version", ctypes.c_uint16),
+        ("dtype", ctypes.c_uint16),
+        ("page_size", i32),
+        ("num_kv_heads", i32),
+        ("head_dim", i32),
+        ("layer_begin", i32),
+        ("num_layers", i32),
+        ("num_blocks", i32),
+        ("cached_len", i64),
+        ("block_bytes", u64),
+        ("payload_offset", u64),
+        ("reserved", u64),
+    ]
+
+
 DESC_P = ctypes.POINTER(PoolDescC)
+WIRE_P = ctypes.POINTER(WireHeaderC)
 I32P = ctypes.POINTER(i32)
 
 DEVICE_SIGNATURES = {
@@ -55,6 +74,10 @@ DEVICE_SIGNATURES = {
     "mkv_decode_step": (c_int, [P, P, i32, P, P, P, P, P, P, f32, u32, P]),
     "mkv_extend_attention": (c_int, [P, i32, P, P, P, P, P, P, i32, i32, i32, f32, u32, P]),
     "mkv_qk_norm_rope_append": (c_int, [P, i32, P, P, P, P, P, P, i32, f32, P, P, i32, P, u32, P]),
+    "mkv_wire_export": (c_int, [P, P, i32, i32, i32, P, P, P]),
+    "mkv_wire_import": (c_int, [P, P, i32, i32, i32, P, P, P, P]),
+    "mkv_wire_header_init": (c_int, [DESC_P, i32, i32, i32, i64, WIRE_P]),
+    "mkv_wire_header_check": (c_int, [DESC_P, WIRE_P]),
     "mkv_validate_slots": (c_int, [DESC_P, I32P, i32]),
     "mkv_validate_block_tables": (c_int, [DESC_P, I32P, I32P, I32P, i32, i32]),
     "mkv_validate_copy_pairs": (c_int, [DESC_P, I32P, I32P, i32]),

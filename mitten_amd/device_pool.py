@@ -33,7 +33,7 @@ MKV_ERR_HIP = 3
 MKV_ERR_DEVICE_INDEX = 4
 MKV_ERR_NO_DEVICE = 5
 
-DEVERR_SLOT, DEVERR_BLOCK, DEVERR_TABLE, DEVERR_COPY, DEVERR_CTX = 1, 2, 4, 8, 16
+DEVERR_SLOT, DEVERR_BLOCK, DEVERR_TABLE, DEVERR_COPY, DEVERR_CTX, DEVERR_CHECKSUM = 1, 2, 4, 8, 16, 32
 
 ATTN_ZERO_SINK, ATTN_FORCE_VALU, ATTN_FORCE_MFMA, ATTN_PER_HEAD_LOADS = 1, 2, 4, 8
 PREP_PLAIN_Q, PREP_NO_NORM = 1, 2
@@ -388,6 +388,51 @@ class DeviceKvPool:
             nul if inv_freq is None else _dptr(inv_freq), rd, eps, _dptr(positions), _dptr(slot_mapping),
             n, _dptr(out), flags, _stream_handle(stream)))
         return out
+
+    def wire_block_bytes(self, num_layers: int | None = None) -> int:
+        """Payload bytes of one block carrying `num_layers` layers (all by default)."""
+        nl = self.desc.num_layers if num_layers is None else num_layers
+        return nl * self.desc.block_bytes * 2
+
+    def wire_export(self, block_ids, layer_begin: int = 0, num_layers: int | None = None, payload=None,
+                    checksums=None, stream=None):
+        """Blocks -> (payload uint8 [n * block_bytes], checksums int64 [n]):
+        layers [layer_begin, layer_begin + num_layers) of each block, K and V,
+        block-major, with the per-block sum64 checksum (mkv_wire_export)."""
+        torch = _torch()
+        n = block_ids.shape[0]
+        nl = self.desc.num_layers - layer_begin if num_layers is None else num_layers
+        self._i32(block_ids, "block_ids", n)
+        nbytes = n * self.wire_block_bytes(nl)
+        if payload is None:
+            payload = torch.empty(nbytes, dtype=torch.uint8, device=block_ids.device)
+        if checksums is None:
+            checksums = torch.empty(n, dtype=torch.int64, device=block_ids.device)
+        self._check_tensor(payload, (nbytes,), "payload", dtype=torch.uint8)
+        self._check_tensor(checksums, (n,), "checksums", dtype=torch.int64)
+        _raise(self._lib.mkv_wire_export(self._h, _dptr(block_ids), n, layer_begin, nl, _dptr(payload),
+                                         _dptr(checksums), _stream_handle(stream)))
+        return payload, checksums
+
+    def wire_import(self, block_ids, payload, layer_begin: int = 0, num_layers: int | None = None,
+                    expected=None, checksums=None, stream=None):
+        """payload -> blocks `block_ids` (mkv_wire_import); returns the checksums
+        of the payload as received. With `expected`, a mismatch is reported by
+        check() as DeviceIndexError with DEVERR_CHECKSUM."""
+        torch = _torch()
+        n = block_ids.shape[0]
+        nl = self.desc.num_layers - layer_begin if num_layers is None else num_layers
+        self._i32(block_ids, "block_ids", n)
+        self._check_tensor(payload, (n * self.wire_block_bytes(nl),), "payload", dtype=torch.uint8)
+        if expected is not None:
+            self._check_tensor(expected, (n,), "expected", dtype=torch.int64)
+        if checksums is None:
+            checksums = torch.empty(n, dtype=torch.int64, device=block_ids.device)
+        self._check_tensor(checksums, (n,), "checksums", dtype=torch.int64)
+        _raise(self._lib.mkv_wire_import(self._h, _dptr(block_ids), n, layer_begin, nl, _dptr(payload),
+                                         ctypes.c_void_p(0) if expected is None else _dptr(expected),
+                                         _dptr(checksums), _stream_handle(stream)))
+        return checksums
 
     def plan(self, ctx_lens, pieces: int = 0, stream=None) -> "DecodePlan":
         """Work plan of one decode step from host context lengths (tokens

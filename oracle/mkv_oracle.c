@@ -29,6 +29,13 @@
  *                        model.rs:508-540 (apply_rope, NeoX half-rotation of
  *                        dims [0, rotary_dim), the rest passed through), as
  *                        GatedAttention::forward applies them (model.rs:380-384)
+ *   orc_wire_*           no reference implementation (the reference hands pages
+ *                        between workers as indices, design/phase2b-deliverable.md:
+ *                        272-289, and sketches per-layer SSD KV files,
+ *                        design/phase1-deliverable.md:253-339); the closed form of
+ *                        the byte format declared in include/mitten_kv.h:
+ *                        payload [n][layers][K,V][page][heads][dim], per-block
+ *                        sum64 checksum
  *   orc_ref_faithful_*   the same attention, executed the way the reference
  *                        executes it (contiguous cache grown by a copy per
  *                        token, repeat_kv materialised, mask built per call);
@@ -229,6 +236,55 @@ ORC_API void orc_norm_rope_rows(float *x, int64_t rows, int32_t D, const float *
       row[i + half] = x2 * c + x1 * sn;
     }
   }
+}
+
+/* sum64 of one block's payload: sum over little-endian u64 words w_j of
+ * mix(w_j + (j + 1) * golden), mix the splitmix64 output function, mod 2^64.
+ * splitmix64_next(&s) with s = w_j + j * golden adds golden and mixes: the
+ * same value. */
+static uint64_t wire_sum64(const uint8_t *p, int64_t nbytes) {
+  uint64_t acc = 0;
+  for (int64_t j = 0; j < nbytes / 8; j++) {
+    uint64_t w;
+    memcpy(&w, p + 8 * j, 8);
+    uint64_t s = w + (uint64_t)j * 0x9E3779B97F4A7C15ull;
+    acc += splitmix64_next(&s);
+  }
+  return acc;
+}
+
+ORC_API void orc_wire_checksums(const uint8_t *payload, int64_t n, int64_t block_bytes, uint64_t *out) {
+  for (int64_t i = 0; i < n; i++) out[i] = wire_sum64(payload + i * block_bytes, block_bytes);
+}
+
+/* Export: payload[i][l][kv] = pool[layer_begin + l][kv][ids[i]] (one whole
+ * block plane, page_size rows), checksums per block. Returns -1, or the index
+ * of the first id outside the pool (nothing written for it). */
+ORC_API int64_t orc_wire_export(const orc_pool_desc *d, const uint8_t *pool, const int32_t *ids, int64_t n,
+                                int layer_begin, int num_layers, uint8_t *payload, uint64_t *sums) {
+  const int64_t bb = block_bytes(d), per = (int64_t)num_layers * 2 * bb;
+  for (int64_t i = 0; i < n; i++) {
+    if (ids[i] < 0 || ids[i] >= d->num_blocks) return i;
+    for (int l = 0; l < num_layers; l++)
+      for (int kv = 0; kv < 2; kv++)
+        memcpy(payload + i * per + ((int64_t)l * 2 + kv) * bb, pool + plane_off(d, layer_begin + l, kv, ids[i]), bb);
+    sums[i] = wire_sum64(payload + i * per, per);
+  }
+  return -1;
+}
+
+/* Import: the inverse scatter; sums of the payload as received. */
+ORC_API int64_t orc_wire_import(const orc_pool_desc *d, uint8_t *pool, const int32_t *ids, int64_t n,
+                                int layer_begin, int num_layers, const uint8_t *payload, uint64_t *sums) {
+  const int64_t bb = block_bytes(d), per = (int64_t)num_layers * 2 * bb;
+  for (int64_t i = 0; i < n; i++) {
+    if (ids[i] < 0 || ids[i] >= d->num_blocks) return i;
+    for (int l = 0; l < num_layers; l++)
+      for (int kv = 0; kv < 2; kv++)
+        memcpy(pool + plane_off(d, layer_begin + l, kv, ids[i]), payload + i * per + ((int64_t)l * 2 + kv) * bb, bb);
+    sums[i] = wire_sum64(payload + i * per, per);
+  }
+  return -1;
 }
 
 /* Element load from the pool as f32 (bf16 is widened exactly). */

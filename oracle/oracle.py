@@ -59,6 +59,9 @@ def lib():
             "orc_gather": (ctypes.c_int, [dp, P, ctypes.c_int, P, P, P, i32, P, P]),
             "orc_copy_blocks": (ctypes.c_int, [dp, P, P, P, i64]),
             "orc_norm_rope_rows": (None, [P, i64, i32, P, f32, P, i32, P]),
+            "orc_wire_checksums": (None, [P, i64, i64, P]),
+            "orc_wire_export": (i64, [dp, P, P, i64, ctypes.c_int, ctypes.c_int, P, P]),
+            "orc_wire_import": (i64, [dp, P, P, i64, ctypes.c_int, ctypes.c_int, P, P]),
             "orc_decode_attention_f32": (ctypes.c_int, [dp, P, ctypes.c_int, P, i32, i32, P, P, P,
                                                         f32, ctypes.c_int, P]),
             "orc_decode_attention_f64": (ctypes.c_int, [dp, P, ctypes.c_int, P, i32, i32, P, P, P,
@@ -204,6 +207,40 @@ def qk_norm_rope_append(d: PoolDesc, pool: np.ndarray, layer: int, q: np.ndarray
     if bad >= 0:
         raise ValueError(f"slot of token {bad} outside the pool")
     return qo
+
+
+def wire_checksums(payload: np.ndarray, n: int, block_bytes: int) -> np.ndarray:
+    """sum64 of each block of a payload (include/mitten_kv.h), as int64 bit patterns."""
+    p = np.ascontiguousarray(payload).view(np.uint8)
+    out = np.empty(n, np.uint64)
+    lib().orc_wire_checksums(_p(p), n, block_bytes, _p(out))
+    return out.view(np.int64)
+
+
+def wire_export(d: PoolDesc, pool: np.ndarray, ids, layer_begin: int, num_layers: int):
+    """(payload uint8 [n * num_layers * 2 * block_bytes], checksums int64 [n])."""
+    ids = np.ascontiguousarray(ids, np.int32)
+    per = num_layers * 2 * d.page_size * d.num_kv_heads * d.head_dim * d.elem_bytes
+    payload = np.empty(ids.size * per, np.uint8)
+    sums = np.empty(ids.size, np.uint64)
+    bad = lib().orc_wire_export(ctypes.byref(d), _p(pool), _p(ids), ids.size, layer_begin, num_layers,
+                                _p(payload), _p(sums))
+    if bad >= 0:
+        raise ValueError(f"block id {ids[bad]} outside the pool")
+    return payload, sums.view(np.int64)
+
+
+def wire_import(d: PoolDesc, pool: np.ndarray, ids, layer_begin: int, num_layers: int,
+                payload: np.ndarray) -> np.ndarray:
+    """In-place scatter of a payload into blocks `ids`; returns its checksums."""
+    ids = np.ascontiguousarray(ids, np.int32)
+    p = np.ascontiguousarray(payload).view(np.uint8)
+    sums = np.empty(ids.size, np.uint64)
+    bad = lib().orc_wire_import(ctypes.byref(d), _p(pool), _p(ids), ids.size, layer_begin, num_layers,
+                                _p(p), _p(sums))
+    if bad >= 0:
+        raise ValueError(f"block id {ids[bad]} outside the pool")
+    return sums.view(np.int64)
 
 
 def decode_attention(d: PoolDesc, pool: np.ndarray, layer: int, q: np.ndarray, indptr, indices,
