@@ -18,6 +18,8 @@ timed on a bounded sample on this host).
 `--op prep` measures the fused pre-attention kernel instead (q/k RMSNorm +
 NeoX RoPE + K/V append, mkv_qk_norm_rope_append) on a prefill chunk of
 `--tokens` tokens at the same head geometry, and prints its own JSON line.
+`--op wire` measures the KV block wire format: export of `--handoff-blocks`
+blocks (all layers) to a payload and its import into other blocks.
 """
 from __future__ import annotations
 
@@ -55,9 +57,12 @@ def parse():
                     help="time the steps without per-launch HIP events (roofline fields null)")
     ap.add_argument("--cpu-layers", type=int, default=5,
                     help="layers of the batch in the CPU baseline sample")
-    ap.add_argument("--op", choices=["decode", "prep"], default="decode",
+    ap.add_argument("--op", choices=["decode", "prep", "wire"], default="decode",
                     help="decode: the decode step (headline); prep: the fused q/k-norm + RoPE + "
-                         "append kernel on a prefill chunk")
+                         "append kernel on a prefill chunk; wire: KV block export + import of a "
+                         "handoff")
+    ap.add_argument("--handoff-blocks", type=int, default=2048,
+                    help="--op wire: blocks handed off (all layers)")
     ap.add_argument("--tokens", type=int, default=16384, help="--op prep: tokens in the chunk")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 1 GiB device to device (the known-size kernel that scales "
@@ -236,6 +241,100 @@ def bench_prep(args):
     }), flush=True)
 
 
+def bench_wire(args):
+    """A handoff of `--handoff-blocks` blocks of the config's pool (every
+    layer, K and V): mkv_wire_export of blocks drawn from a seeded
+    permutation into one payload with per-block checksums, then
+    mkv_wire_import of that payload into other blocks with verification.
+    One step = export + import; HIP events around each launch pair."""
+    import torch
+
+    from mitten_amd import DeviceKvPool, PoolDesc
+    from mitten_amd import workloads as wl
+
+    cfg = wl.CONFIGS[args.config]
+    L, Hq, Hkv, D, dt = (cfg["num_layers"], cfg["num_q_heads"], cfg["num_kv_heads"], cfg["head_dim"],
+                         cfg["dtype"])
+    n = args.handoff_blocks
+    nblocks = 2 * n + 64
+    desc = PoolDesc(L, Hkv, Hq, D, nblocks, dt)
+    dev = torch.device("cuda:0")
+    rng = wl.SplitMix64(wl.BASE_SEED + 23)
+    perm = wl.permutation(nblocks, rng)
+    i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(dev)
+    src, dst = i32(perm[:n]), i32(perm[n:2 * n])
+    stream = torch.cuda.current_stream()
+    with DeviceKvPool(desc) as pool:
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(wl.BASE_SEED + 23)
+        view = pool.tensor()
+        for layer in range(L):
+            view[layer].normal_(generator=gen)
+        del view
+        bb = pool.wire_block_bytes()
+        payload = torch.empty(n * bb, dtype=torch.uint8, device=dev)
+        sums = torch.empty(n, dtype=torch.int64, device=dev)
+        got = torch.empty(n, dtype=torch.int64, device=dev)
+
+        def step(ev=None):
+            if ev:
+                ev[0].record(stream)
+            pool.wire_export(src, payload=payload, checksums=sums, stream=stream)
+            if ev:
+                ev[1].record(stream)
+            pool.wire_import(dst, payload, expected=sums, checksums=got, stream=stream)
+            if ev:
+                ev[2].record(stream)
+
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        pool.check()
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+        t0 = time.perf_counter()
+        for s_ in range(args.steps):
+            step(evs[s_])
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        pool.check()
+        exp_s = float(np.mean([e[0].elapsed_time(e[1]) for e in evs])) / 1e3
+        imp_s = float(np.mean([e[1].elapsed_time(e[2]) for e in evs])) / 1e3
+        # CPU baseline: the oracle's export of a 64-block sample of the same pool.
+        from oracle import oracle as orc
+
+        sample = min(n, 64)
+        host = pool.read()
+        od = orc.desc(L, Hkv, D, nblocks, desc.elem_bytes)
+        ids_h = perm[:sample].astype(np.int32)
+        c0 = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - c0 < 2.0 or reps == 0:
+            orc.wire_export(od, host, ids_h, 0, L)
+            reps += 1
+        cpu_s = (time.perf_counter() - c0) / reps
+    bytes_one = 2 * n * bb + 4 * n + 8 * n  # payload read + written, ids, checksums
+    exp_gbs, imp_gbs = bytes_one / exp_s / 1e9, bytes_one / imp_s / 1e9
+    step_gbs = 2 * bytes_one / (elapsed / args.steps) / 1e9
+    print(json.dumps({
+        "metric": "KV block wire export + import achieved HBM GB/s",
+        "value": round(step_gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(elapsed / args.steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": dt,
+        "data": "synthetic: N(0,1) K/V in every block; block ids from a seeded permutation",
+        "config": {"workload": f"{args.config}-shaped handoff of {n} blocks (all {L} layers, K and V)",
+                   "blocks": n, "block_payload_bytes": bb, "payload_bytes": n * bb},
+        "export": {"avg_launch_us": round(exp_s * 1e6, 2), "GB_s": round(exp_gbs, 2)},
+        "import": {"avg_launch_us": round(imp_s * 1e6, 2), "GB_s": round(imp_gbs, 2),
+                   "note": "includes the checksum compare launch"},
+        "roofline": {"bound": "hbm", "achieved": round(exp_gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(exp_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "mkv_wire_export (zero + wire_kernel<true>)", "bytes_per_launch": bytes_one,
+                     "avg_launch_us": round(exp_s * 1e6, 2)},
+        "cpu_baseline": {"value": round(2 * sample * bb / cpu_s / 1e9, 3), "unit": "GB/s", "cores": 1,
+                         "kind": "port", "sample": f"oracle wire_export of {sample} blocks, {reps} repetitions"},
+    }), flush=True)
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -247,6 +346,9 @@ def main():
         sys.exit(2)
     if args.op == "prep":
         bench_prep(args)
+        return
+    if args.op == "wire":
+        bench_wire(args)
         return
     import torch
 

@@ -22,6 +22,8 @@
 
 namespace mkv {
 
+typedef uint32_t w32x4 __attribute__((ext_vector_type(4)));
+
 constexpr uint64_t kWireGolden = 0x9E3779B97F4A7C15ull;
 constexpr int kWireUnroll = 8;  // 16-byte chunks per thread: 32 KiB per workgroup
 
@@ -56,24 +58,24 @@ __global__ void __launch_bounds__(256) wire_kernel(WireArgs a) {
     return;
   }
   const uint32_t c0 = blockIdx.x * (256u * kWireUnroll) + tid;
-  uint4 *pay = reinterpret_cast<uint4 *>(a.payload + (int64_t)i * a.chunks * 16);
+  w32x4 *pay = reinterpret_cast<w32x4 *>(a.payload + (int64_t)i * a.chunks * 16);
   int64_t poff[kWireUnroll];
-  uint4 r[kWireUnroll];
+  w32x4 r[kWireUnroll];
 #pragma unroll
-  for (int u = 0; u < kWireUnroll; u++) {  // all loads first
+  for (int u = 0; u < kWireUnroll; u++) {  // all loads first; nontemporal: the data is not reused
     const uint32_t c = min(c0 + u * 256u, a.chunks - 1);  // lanes past the end reload the last chunk
     const uint32_t p = c / a.plane_chunks, o = c - p * a.plane_chunks;
     poff[u] = (int64_t)(a.layer0 * 2 + (int)p) * a.plane_bytes + (int64_t)b * a.block_bytes + (int64_t)o * 16;
-    r[u] = EXPORT ? *reinterpret_cast<const uint4 *>(a.pool + poff[u]) : pay[c];
+    r[u] = EXPORT ? __builtin_nontemporal_load(reinterpret_cast<const w32x4 *>(a.pool + poff[u])) : __builtin_nontemporal_load(&pay[c]);
   }
   unsigned long long acc = 0;
 #pragma unroll
   for (int u = 0; u < kWireUnroll; u++) {
     const uint32_t c = c0 + u * 256u;
     if (c < a.chunks) {
-      if (EXPORT) pay[c] = r[u];
-      else *reinterpret_cast<uint4 *>(a.pool + poff[u]) = r[u];
-      const uint64_t lo = ((uint64_t)r[u].y << 32) | r[u].x, hi = ((uint64_t)r[u].w << 32) | r[u].z;
+      if (EXPORT) __builtin_nontemporal_store(r[u], &pay[c]);
+      else __builtin_nontemporal_store(r[u], reinterpret_cast<w32x4 *>(a.pool + poff[u]));
+      const uint64_t lo = ((uint64_t)r[u][1] << 32) | r[u][0], hi = ((uint64_t)r[u][3] << 32) | r[u][2];
       acc += wire_mix(lo, 2ull * c) + wire_mix(hi, 2ull * c + 1);
     }
   }
