@@ -20,6 +20,9 @@ NeoX RoPE + K/V append, mkv_qk_norm_rope_append) on a prefill chunk of
 `--tokens` tokens at the same head geometry, and prints its own JSON line.
 `--op wire` measures the KV block wire format: export of `--handoff-blocks`
 blocks (all layers) to a payload and its import into other blocks.
+`--op gather` measures the block-table gather of the decode batch's contexts
+(one layer per launch); `--op copy` measures copy_blocks (COW copies and
+compaction moves) of `--copy-pairs` block pairs over all layers.
 """
 from __future__ import annotations
 
@@ -57,10 +60,12 @@ def parse():
                     help="time the steps without per-launch HIP events (roofline fields null)")
     ap.add_argument("--cpu-layers", type=int, default=5,
                     help="layers of the batch in the CPU baseline sample")
-    ap.add_argument("--op", choices=["decode", "prep", "wire"], default="decode",
+    ap.add_argument("--op", choices=["decode", "prep", "wire", "gather", "copy"], default="decode",
                     help="decode: the decode step (headline); prep: the fused q/k-norm + RoPE + "
                          "append kernel on a prefill chunk; wire: KV block export + import of a "
-                         "handoff")
+                         "handoff; gather: block-table gather of the decode batch, one layer; "
+                         "copy: copy_blocks of --copy-pairs block pairs, all layers")
+    ap.add_argument("--copy-pairs", type=int, default=4096, help="--op copy: block pairs")
     ap.add_argument("--handoff-blocks", type=int, default=2048,
                     help="--op wire: blocks handed off (all layers)")
     ap.add_argument("--tokens", type=int, default=16384, help="--op prep: tokens in the chunk")
@@ -335,6 +340,90 @@ def bench_wire(args):
     }), flush=True)
 
 
+def bench_move(args):
+    """gather: the decode batch's block-table gather, one layer per launch,
+    cycling over the layers (K and V of every context token read once through
+    the block table and written contiguously). copy: copy_blocks of
+    `--copy-pairs` (src, dst) pairs drawn from a seeded permutation of the
+    pool, every layer, K and V. HIP events on the launch stream around each
+    launch."""
+    import torch
+
+    from mitten_amd import DeviceKvPool, PoolDesc
+    from mitten_amd import workloads as wl
+
+    cfg = wl.CONFIGS[args.config]
+    batch = wl.config_batch(args.config)
+    L, Hq, Hkv, D, dt = (cfg["num_layers"], cfg["num_q_heads"], cfg["num_kv_heads"], cfg["head_dim"],
+                         cfg["dtype"])
+    desc = PoolDesc(L, Hkv, Hq, D, batch.num_blocks, dt)
+    dev = torch.device("cuda:0")
+    i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(dev)
+    stream = torch.cuda.current_stream()
+    row = Hkv * D * desc.elem_bytes
+    with DeviceKvPool(desc) as pool:
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(batch.seed)
+        view = pool.tensor()
+        for layer in range(L):
+            view[layer].normal_(generator=gen)
+        del view
+        if args.op == "gather":
+            ctx = batch.ctx_lens.astype(np.int64)
+            cptr = np.concatenate([[0], np.cumsum(ctx)]).astype(np.int32)
+            tokens = int(cptr[-1])
+            indptr, ids, ctx_indptr = i32(batch.block_indptr), i32(batch.block_ids), i32(cptr)
+            n = tokens * Hkv * D
+            tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+            out_k = torch.empty(n, dtype=tdt, device=dev)
+            out_v = torch.empty(n, dtype=tdt, device=dev)
+            launch_bytes = 4 * tokens * row + 4 * int(batch.block_ids.size) + 8 * (batch.num_seqs + 1)
+
+            def launch(i):
+                pool.gather(i % L, indptr, ids, ctx_indptr, int(ctx.max()), out_k=out_k, out_v=out_v,
+                            total_tokens=tokens, stream=stream)
+            kernel, what = "mkv_gather", (f"{args.config} decode batch: {batch.num_seqs} sequences, "
+                                          f"{tokens} context tokens, one layer per launch")
+        else:
+            rng = wl.SplitMix64(batch.seed + 5)
+            perm = wl.permutation(batch.num_blocks, rng)
+            npairs = args.copy_pairs
+            src, dst = i32(perm[:npairs]), i32(perm[npairs:2 * npairs])
+            launch_bytes = 2 * npairs * L * 2 * desc.block_bytes + 8 * npairs
+
+            def launch(i):
+                pool.copy_blocks(src, dst, stream=stream)
+            kernel, what = "mkv_copy_blocks", f"{args.config} pool: {npairs} block pairs, all {L} layers, K and V"
+        for i in range(args.warmup):
+            launch(i)
+        torch.cuda.synchronize()
+        pool.check()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(args.steps)]
+        t0 = time.perf_counter()
+        for i, (a, b) in enumerate(evs):
+            a.record(stream)
+            launch(i)
+            b.record(stream)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        pool.check()
+    launch_s = float(np.mean([a.elapsed_time(b) for a, b in evs])) / 1e3
+    gbs = launch_bytes / launch_s / 1e9
+    print(json.dumps({
+        "metric": f"{kernel} achieved HBM GB/s",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(elapsed / args.steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": dt,
+        "data": "synthetic: N(0,1) K/V in every block; block tables / pairs from a seeded permutation",
+        "config": {"workload": what, "op": args.op},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "kernel": kernel,
+                     "bytes_per_launch": launch_bytes, "avg_launch_us": round(launch_s * 1e6, 2)},
+        "cpu_baseline": None,
+    }), flush=True)
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -349,6 +438,9 @@ def main():
         return
     if args.op == "wire":
         bench_wire(args)
+        return
+    if args.op in ("gather", "copy"):
+        bench_move(args)
         return
     import torch
 

@@ -13,6 +13,8 @@
 
 namespace mkv {
 
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
 static thread_local std::string g_last_error;
 
 int set_error(int code, const char *fmt, ...) {
@@ -97,7 +99,12 @@ append_kernel(uint8_t *__restrict__ pool, int32_t layer0, const uint4 *__restric
   }
 }
 
-// grid.x = block index within a sequence, grid.y = sequence.
+// grid.x = block index within a sequence, grid.y = sequence. A workgroup
+// moves one block's rows of K and V: every thread issues all its 16-byte
+// loads (K chunks, then V chunks) before its stores; loads and stores are
+// nontemporal (nothing is reused).
+constexpr int kGatherPer = 8;  // 16-byte chunks per thread and pass
+
 __global__ void __launch_bounds__(256)
 gather_kernel(const uint8_t *__restrict__ pool, int32_t layer, const int32_t *__restrict__ indptr,
               const int32_t *__restrict__ ids, const int32_t *__restrict__ ctx_indptr,
@@ -124,45 +131,67 @@ gather_kernel(const uint8_t *__restrict__ pool, int32_t layer, const int32_t *__
     return;
   }
   const int nt = (int)min<int64_t>(kPageSize, n - t0);
-  const int cph = (g.D * g.es) >> 4;  // 16-byte chunks per head row
-  const int total = nt * g.Hkv * cph;
-  for (int kv = 0; kv < 2; kv++) {
-    const uint4 *src = reinterpret_cast<const uint4 *>(
-        pool + ((int64_t)layer * 2 + kv) * g.plane_bytes + (int64_t)blk * g.block_bytes);
-    uint8_t *out = kv ? out_v : out_k;
-    for (int c = tid; c < total; c += blockDim.x) {
-      const int t = c / (g.Hkv * cph);
-      const int h = (c / cph) % g.Hkv;
-      const int cc = c % cph;
+  const uint32_t cph = (uint32_t)(g.D * g.es) >> 4;  // 16-byte chunks per head row
+  const uint32_t per_kv = (uint32_t)nt * g.Hkv * cph;  // chunks of K (or V) in this block
+  const uint32_t total = 2 * per_kv;
+  const uint8_t *kplane = pool + (int64_t)layer * 2 * g.plane_bytes + (int64_t)blk * g.block_bytes;
+  for (uint32_t base = tid; base < total; base += 256u * kGatherPer) {
+    u32x4v r[kGatherPer];
+#pragma unroll
+    for (int u = 0; u < kGatherPer; u++) {  // all loads first (clamped past the end, not stored)
+      const uint32_t c = min(base + u * 256u, total - 1);
+      const uint32_t kv = c >= per_kv, cc = c - kv * per_kv;
+      r[u] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4v *>(kplane + kv * g.plane_bytes + (int64_t)cc * 16));
+    }
+#pragma unroll
+    for (int u = 0; u < kGatherPer; u++) {
+      const uint32_t c = base + u * 256u;
+      if (c >= total) break;
+      const uint32_t kv = c >= per_kv, cc = c - kv * per_kv;
+      const uint32_t t = cc / (g.Hkv * cph), h = (cc / cph) % g.Hkv, w = cc % cph;
       const int64_t elem = (c0 * g.Hkv + (int64_t)h * n + t0 + t) * g.D;
-      reinterpret_cast<uint4 *>(out + elem * g.es)[cc] = src[c];
+      __builtin_nontemporal_store(r[u], reinterpret_cast<u32x4v *>((kv ? out_v : out_k) + elem * g.es) + w);
     }
   }
 }
 
-// grid.x = pair, grid.y = plane (layer * 2 + kv).
+// grid.x = pair, grid.y = group of kCopyPlanes planes (layer * 2 + kv). A
+// workgroup copies kCopyPlanes whole block planes: all loads first, then the
+// stores, nontemporal.
+constexpr int kCopyPlanes = 2;
+constexpr int kCopyPer = 8;  // 16-byte chunks per thread and pass
+
 __global__ void __launch_bounds__(256)
 copy_blocks_kernel(uint8_t *__restrict__ pool, const int32_t *__restrict__ src,
                    const int32_t *__restrict__ dst, Geom g, uint32_t *__restrict__ d_err) {
-  const int i = blockIdx.x, plane = blockIdx.y, tid = threadIdx.x;
+  const int i = blockIdx.x, tid = threadIdx.x;
   const int32_t s = src[i], d = dst[i];
   if (s < 0 || s >= g.nblocks || d < 0 || d >= g.nblocks) {
-    if (plane == 0 && tid == 0) record_error(d_err, MKV_DEVERR_COPY);
+    if (blockIdx.y == 0 && tid == 0) record_error(d_err, MKV_DEVERR_COPY);
     return;
   }
-  const uint4 *sp = reinterpret_cast<const uint4 *>(pool + plane * g.plane_bytes + s * g.block_bytes);
-  uint4 *dp = reinterpret_cast<uint4 *>(pool + plane * g.plane_bytes + d * g.block_bytes);
-  const int n = (int)(g.block_bytes >> 4);
-  const int bd = blockDim.x;
-  // Issue four loads before the four stores so each lane keeps 64 B in flight.
-  for (int base = tid; base < n; base += 4 * bd) {
-    uint4 r[4];
+  const int p0 = blockIdx.y * kCopyPlanes;
+  const int planes = min(kCopyPlanes, 2 * g.L - p0);
+  const uint32_t per_plane = (uint32_t)(g.block_bytes >> 4);
+  const uint32_t total = planes * per_plane;
+  const uint8_t *sp = pool + p0 * g.plane_bytes + s * g.block_bytes;
+  uint8_t *dp = pool + p0 * g.plane_bytes + d * g.block_bytes;
+  for (uint32_t base = tid; base < total; base += 256u * kCopyPer) {
+    u32x4v r[kCopyPer];
 #pragma unroll
-    for (int u = 0; u < 4; u++)
-      if (base + u * bd < n) r[u] = sp[base + u * bd];
+    for (int u = 0; u < kCopyPer; u++) {
+      const uint32_t c = min(base + u * 256u, total - 1);
+      const uint32_t pl = c / per_plane, cc = c - pl * per_plane;
+      r[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4v *>(sp + pl * g.plane_bytes) + cc);
+    }
 #pragma unroll
-    for (int u = 0; u < 4; u++)
-      if (base + u * bd < n) dp[base + u * bd] = r[u];
+    for (int u = 0; u < kCopyPer; u++) {
+      const uint32_t c = base + u * 256u;
+      if (c >= total) break;
+      const uint32_t pl = c / per_plane, cc = c - pl * per_plane;
+      __builtin_nontemporal_store(r[u], reinterpret_cast<u32x4v *>(dp + pl * g.plane_bytes) + cc);
+    }
   }
 }
 
@@ -342,7 +371,7 @@ extern "C" int mkv_copy_blocks(mkv_pool *pool, const int32_t *d_src_blocks,
     return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL device pointer");
   if (2 * p->g.L > 65535) return set_error(MKV_ERR_INVALID_ARGUMENT, "too many layers");
   DeviceGuard guard(p->device);
-  hipLaunchKernelGGL(copy_blocks_kernel, dim3(num_pairs, 2 * p->g.L), dim3(256), 0,
+  hipLaunchKernelGGL(copy_blocks_kernel, dim3(num_pairs, (2 * p->g.L + kCopyPlanes - 1) / kCopyPlanes), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), p->data, d_src_blocks, d_dst_blocks,
                      p->g, p->d_err);
   MKV_CHECK_LAUNCH("copy_blocks_kernel");
