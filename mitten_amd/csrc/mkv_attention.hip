@@ -1160,7 +1160,24 @@ struct ExtArgs {
   const int32_t *q_indptr;  // [B+1] query tokens of each sequence in q / o
   const int32_t *ctx;       // [B] tokens in the cache, the chunk included
   int32_t B, max_ctx;
+  int32_t tiles, per_xcd;   // query tiles per sequence; logical workgroups per XCD
 };
+
+// Workgroups are dealt to the 8 XCDs round-robin by linear index. The
+// launch has 8 * per_xcd workgroups; workgroup L becomes logical index
+// (L % 8) * per_xcd + L / 8, so each XCD receives a contiguous run of
+// logical indices: the query tiles of one (sequence, KV head) share that
+// XCD's L2 while they stream the same K/V. Logical index = tile + tiles *
+// (head + Hkv * sequence); false for the padding past the last one.
+__device__ __forceinline__ bool ext_tile(const ExtArgs &e, int Hkv, int &t, int &h, int &b) {
+  const int L = blockIdx.x;
+  const int logical = (L & 7) * e.per_xcd + (L >> 3);
+  if (logical >= e.tiles * Hkv * e.B) return false;
+  t = logical % e.tiles;
+  h = (logical / e.tiles) % Hkv;
+  b = logical / (e.tiles * Hkv);
+  return true;
+}
 
 template <int D, int W>
 __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e) {
@@ -1170,12 +1187,14 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
   constexpr int TILE = 16 * RB;
   constexpr int NCH = 2 * 16 * CPR;                   // chunks of K + V of one block
   constexpr int LPL = (NCH + 64 * W - 1) / (64 * W);  // loads per lane per block
-  constexpr int R = 3;
+  constexpr int R = 4;  // even: stage s of an unrolled round uses LDS buffer s & 1
+  static_assert(R % 2 == 0, "the LDS buffer index must be static per stage");
   __shared__ __attribute__((aligned(16))) uint8_t tiles[2][2][TILE];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int m16 = lane & 15, g4 = lane >> 4, a4 = m16 >> 2, rq = m16 & 3;
-  const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  int t, h, b;
+  if (!ext_tile(e, a.Hkv, t, h, b)) return;
   const int q0 = e.q_indptr[b], nq = e.q_indptr[b + 1] - q0;
   if (nq <= 0 || 16 * t >= nq) return;
   const int ctx = e.ctx[b];
@@ -1188,7 +1207,11 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
     if (threadIdx.x == 0 && t == 0) record_error(a.d_err, MKV_DEVERR_TABLE);
     return;
   }
-  const int32_t *table = a.ids + tab0;
+  // The table is read through the constant address space: scalar loads,
+  // whose wait does not drain the vector-load ring (a vector load of a block
+  // id needs vmcnt(0) before its readfirstlane).
+  typedef const __attribute__((address_space(4))) int32_t const_i32;
+  const const_i32 *table = (const const_i32 *)(a.ids + tab0);
   const int qlo = ctx - nq + 16 * t;          // first query position of the tile
   const int qhi = min(qlo + 15, ctx - 1);     // last valid one
   const int n = qhi / kPageSize + 1;          // blocks holding keys 0..qhi
@@ -1245,13 +1268,15 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
 
   auto stage = [&](int s, int k) {
     issue(ring[(s + R - 1) % R], badk[(s + R - 1) % R], k + R - 1);
-    uint8_t *tk = tiles[k & 1][0], *tv = tiles[k & 1][1];
+    // k = (multiple of R) + s: buffer s & 1 alternates like k & 1 and is a
+    // compile-time constant here (immediate LDS offsets).
+    uint8_t *tk = tiles[s & 1][0], *tv = tiles[s & 1][1];
 #pragma unroll
     for (int i = 0; i < LPL; i++) {
       const int c = (int)threadIdx.x + 64 * W * i;
       if (c < NCH) {
         const int kv = c / (16 * CPR), rem = c % (16 * CPR), row = rem / CPR, cc = rem % CPR;
-        *reinterpret_cast<u32x4 *>(tiles[k & 1][kv] + row * RB + ((cc ^ tile_swz(row, CPR)) << 4)) = ring[s][i];
+        *reinterpret_cast<u32x4 *>(tiles[s & 1][kv] + row * RB + ((cc ^ tile_swz(row, CPR)) << 4)) = ring[s][i];
       }
     }
     __syncthreads();
@@ -1276,11 +1301,15 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
       for (int i = 0; i < 4; i++)
         if (bad || kp0 + i > qp || kp0 + i >= ctx) x[i] = -INFINITY;
     }
+    // Rescale only when some score passes the running max by the slack:
+    // checked on the lane's own 4 scores first, so the column-wide max (two
+    // cross-lane steps) is computed only on the rare blocks that need it.
+    // Same result as always computing it.
     float mloc = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-    const bool need = mloc > st.m + kRescaleSlack;
-    if (__ballot(need)) {
+    if (__ballot(mloc > st.m + kRescaleSlack)) {
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+      const bool need = mloc > st.m + kRescaleSlack;
       const float mn = need ? mloc : st.m;
       const float al = fast_exp2(st.m - mn);
       st.l *= al;
@@ -1301,13 +1330,13 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
     const i16x4 pb = __builtin_bit_cast(i16x4, (uint64_t)p01 | ((uint64_t)p23 << 32));
     // V rows past the context or of a rejected block are zeroed (stale
     // slots may hold any bit pattern); causally hidden rows have p = 0.
-    uint64_t vmask = ~0ull;
-    if (!full) {
-      const int t0 = kPageSize * k + 4 * g4;
-      vmask = (bad || t0 >= ctx ? 0ull : 0xffffull) | (bad || t0 + 1 >= ctx ? 0ull : 0xffff0000ull) |
-              (bad || t0 + 2 >= ctx ? 0ull : 0xffff00000000ull) |
-              (bad || t0 + 3 >= ctx ? 0ull : 0xffff000000000000ull);
-    }
+    // (One code path with an all-ones mask for full blocks: a separate
+    // unmasked path raised the register count past two workgroups per CU.)
+    const int t0 = kPageSize * k + 4 * g4;
+    const uint64_t vmask = full ? ~0ull
+                                : (bad || t0 >= ctx ? 0ull : 0xffffull) | (bad || t0 + 1 >= ctx ? 0ull : 0xffff0000ull) |
+                                      (bad || t0 + 2 >= ctx ? 0ull : 0xffff00000000ull) |
+                                      (bad || t0 + 3 >= ctx ? 0ull : 0xffff000000000000ull);
 #pragma unroll
     for (int nn = 0; nn < NT; nn++) {
       const i16x4s raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(tv + v_rd[nn]));
@@ -1917,8 +1946,7 @@ extern "C" int mkv_extend_attention(mkv_pool *pool, int32_t layer, const void *d
   if (G > 16) return set_error(MKV_ERR_INVALID_ARGUMENT, "extend attention supports <= 16 query heads per KV head");
   if (!aligned16(d_q) || !aligned16(d_o)) return set_error(MKV_ERR_INVALID_ARGUMENT, "q and o must be 16-byte aligned");
   const int64_t tiles = ((int64_t)max_q_len + 15) / 16;
-  if (tiles > INT32_MAX || num_seqs > 65535 || g.Hkv > 65535)
-    return set_error(MKV_ERR_INVALID_ARGUMENT, "grid too large");
+  if (tiles * g.Hkv * num_seqs + 8 > INT32_MAX) return set_error(MKV_ERR_INVALID_ARGUMENT, "grid too large");
   DeviceGuard guard(p->device);
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
   KArgs a = make_kargs(p, layer, d_q, d_o, d_block_indptr, d_block_ids, scale, flags, true);
@@ -1927,8 +1955,12 @@ extern "C" int mkv_extend_attention(mkv_pool *pool, int32_t layer, const void *d
   e.ctx = d_ctx_lens;
   e.B = num_seqs;
   e.max_ctx = max_ctx_len;
+  // Linear workgroup index -> (tile, KV head, sequence), grouped by XCD.
+  const int64_t total = tiles * g.Hkv * num_seqs;
+  e.tiles = (int32_t)tiles;
+  e.per_xcd = (int32_t)((total + 7) / 8);
   const int W = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : G <= 8 ? 8 : 16;
-  const dim3 grid((unsigned)tiles, (unsigned)g.Hkv, (unsigned)num_seqs), block(64 * W);
+  const dim3 grid((unsigned)(8 * (int64_t)e.per_xcd)), block(64 * W);
 #define MKV_EXT(DD)                                                                       \
   do {                                                                                    \
     switch (W) {                                                                          \
