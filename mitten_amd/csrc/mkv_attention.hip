@@ -1258,6 +1258,8 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
   for (int nn = 0; nn < NT; nn++) st.O[nn] = f32x4{0.f, 0.f, 0.f, 0.f};
   st.m = -INFINITY;
   st.l = 0.0f;
+  const float inv_sl2 = 1.0f / a.sl2;
+  float thr = -INFINITY;  // raw-score rescale threshold
   int k_rd[NR], v_rd[NT];
   const int vrow = 4 * g4 + a4;
 #pragma unroll
@@ -1276,7 +1278,12 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
       const int c = (int)threadIdx.x + 64 * W * i;
       if (c < NCH) {
         const int kv = c / (16 * CPR), rem = c % (16 * CPR), row = rem / CPR, cc = rem % CPR;
-        *reinterpret_cast<u32x4 *>(tiles[s & 1][kv] + row * RB + ((cc ^ tile_swz(row, CPR)) << 4)) = ring[s][i];
+        // V rows past the context or of a rejected block are stored as
+        // zeros (stale slots may hold any bit pattern, and p = 0 times NaN
+        // would poison O); K rows there are masked in the scores instead.
+        u32x4 val = ring[s][i];
+        if (kv && (badk[s] || kPageSize * k + row >= ctx)) val = u32x4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4 *>(tiles[s & 1][kv] + row * RB + ((cc ^ tile_swz(row, CPR)) << 4)) = val;
       }
     }
     __syncthreads();
@@ -1293,55 +1300,50 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
     // Lane holds S[key 16k + 4*g4 + i][query position qlo + lane%16].
     const int kp0 = kPageSize * k + 4 * g4;
     const bool full = !bad && kPageSize * k + kPageSize - 1 <= qlo && kPageSize * k + kPageSize <= ctx;
-    float x[4];
+    // Raw scores (masked ones -inf); the running max st.m is in scaled
+    // (log2) units and thr = (st.m + slack) / (scale * log2 e) in raw ones.
+    float sr[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) x[i] = S[i] * a.sl2;
+    for (int i = 0; i < 4; i++) sr[i] = S[i];
     if (!full) {
 #pragma unroll
       for (int i = 0; i < 4; i++)
-        if (bad || kp0 + i > qp || kp0 + i >= ctx) x[i] = -INFINITY;
+        if (bad || kp0 + i > qp || kp0 + i >= ctx) sr[i] = -INFINITY;
     }
     // Rescale only when some score passes the running max by the slack:
     // checked on the lane's own 4 scores first, so the column-wide max (two
     // cross-lane steps) is computed only on the rare blocks that need it.
-    // Same result as always computing it.
-    float mloc = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-    if (__ballot(mloc > st.m + kRescaleSlack)) {
+    float mloc = fmaxf(fmaxf(sr[0], sr[1]), fmaxf(sr[2], sr[3]));
+    if (__ballot(mloc > thr)) {
       mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
       mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-      const bool need = mloc > st.m + kRescaleSlack;
-      const float mn = need ? mloc : st.m;
+      const float ms = mloc * a.sl2;
+      const bool need = ms > st.m + kRescaleSlack;
+      const float mn = need ? ms : st.m;
       const float al = fast_exp2(st.m - mn);
       st.l *= al;
 #pragma unroll
       for (int nn = 0; nn < NT; nn++) st.O[nn] *= al;
       st.m = mn;
+      thr = (mn + kRescaleSlack) * inv_sl2;
     }
     float pr[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) pr[i] = fast_exp2(x[i] - st.m);
+    for (int i = 0; i < 4; i++) pr[i] = fast_exp2(fmaf(sr[i], a.sl2, -st.m));
     if (!full) {  // a fully masked column has m = -inf: keep its p at 0, not NaN
 #pragma unroll
       for (int i = 0; i < 4; i++)
-        if (x[i] == -INFINITY) pr[i] = 0.0f;
+        if (sr[i] == -INFINITY) pr[i] = 0.0f;
     }
     st.l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
     const uint32_t p01 = pack_bf16x2(pr[0], pr[1]), p23 = pack_bf16x2(pr[2], pr[3]);
     const i16x4 pb = __builtin_bit_cast(i16x4, (uint64_t)p01 | ((uint64_t)p23 << 32));
-    // V rows past the context or of a rejected block are zeroed (stale
-    // slots may hold any bit pattern); causally hidden rows have p = 0.
-    // (One code path with an all-ones mask for full blocks: a separate
-    // unmasked path raised the register count past two workgroups per CU.)
-    const int t0 = kPageSize * k + 4 * g4;
-    const uint64_t vmask = full ? ~0ull
-                                : (bad || t0 >= ctx ? 0ull : 0xffffull) | (bad || t0 + 1 >= ctx ? 0ull : 0xffff0000ull) |
-                                      (bad || t0 + 2 >= ctx ? 0ull : 0xffff00000000ull) |
-                                      (bad || t0 + 3 >= ctx ? 0ull : 0xffff000000000000ull);
+    // O^T += V^T . P^T (V rows past the context were zeroed in LDS; causally
+    // hidden rows have p = 0).
 #pragma unroll
     for (int nn = 0; nn < NT; nn++) {
       const i16x4s raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(tv + v_rd[nn]));
-      const uint64_t w = __builtin_bit_cast(uint64_t, raw) & vmask;
-      st.O[nn] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, w), pb, st.O[nn], 0, 0, 0);
+      st.O[nn] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, raw), pb, st.O[nn], 0, 0, 0);
     }
   };
 
