@@ -185,11 +185,13 @@ __device__ __forceinline__ void mfma_block(const u32x4 (&kq)[D / 32], const u32x
   float x[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) x[i] = (!bad && 4 * g4 + i < nvalid) ? S[i] * sl2 : -INFINITY;
+  // The column-wide max (two cross-lane steps) only when a lane's own
+  // scores pass the running max by the slack: the same rescale decisions.
   float mloc = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-  mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-  mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-  const bool need = mloc > st.m + kRescaleSlack;
-  if (__ballot(need)) {
+  if (__ballot(mloc > st.m + kRescaleSlack)) {
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+    const bool need = mloc > st.m + kRescaleSlack;
     const float mn = need ? mloc : st.m;
     const float al = fast_exp2(st.m - mn);
     st.l *= al;
@@ -893,11 +895,13 @@ __device__ __forceinline__ void mfma_block_t(const u32x4 (&kq)[D / 32], const ui
     for (int i = 0; i < 4; i++)
       if (bad || 4 * g4 + i >= nvalid) x[i] = -INFINITY;
   }
+  // The column-wide max (two cross-lane steps) only when a lane's own
+  // scores pass the running max by the slack: the same rescale decisions.
   float mloc = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-  mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-  mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-  const bool need = mloc > st.m + kRescaleSlack;
-  if (__ballot(need)) {
+  if (__ballot(mloc > st.m + kRescaleSlack)) {
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+    const bool need = mloc > st.m + kRescaleSlack;
     const float mn = need ? mloc : st.m;
     const float al = fast_exp2(st.m - mn);
     st.l *= al;
