@@ -22,7 +22,9 @@ NeoX RoPE + K/V append, mkv_qk_norm_rope_append) on a prefill chunk of
 blocks (all layers) to a payload and its import into other blocks.
 `--op gather` measures the block-table gather of the decode batch's contexts
 (one layer per launch); `--op copy` measures copy_blocks (COW copies and
-compaction moves) of `--copy-pairs` block pairs over all layers.
+compaction moves) of `--copy-pairs` block pairs over all layers; `--op
+extend` measures chunked-prefill attention (TFLOP/s against the bf16 MFMA
+peak).
 """
 from __future__ import annotations
 
@@ -60,11 +62,16 @@ def parse():
                     help="time the steps without per-launch HIP events (roofline fields null)")
     ap.add_argument("--cpu-layers", type=int, default=5,
                     help="layers of the batch in the CPU baseline sample")
-    ap.add_argument("--op", choices=["decode", "prep", "wire", "gather", "copy"], default="decode",
+    ap.add_argument("--op", choices=["decode", "prep", "wire", "gather", "copy", "extend"], default="decode",
                     help="decode: the decode step (headline); prep: the fused q/k-norm + RoPE + "
                          "append kernel on a prefill chunk; wire: KV block export + import of a "
                          "handoff; gather: block-table gather of the decode batch, one layer; "
-                         "copy: copy_blocks of --copy-pairs block pairs, all layers")
+                         "copy: copy_blocks of --copy-pairs block pairs, all layers; extend: chunked-"
+                         "prefill attention of --extend-seqs chunks of --tokens-per-chunk after "
+                         "--prefix tokens")
+    ap.add_argument("--extend-seqs", type=int, default=8, help="--op extend: sequences")
+    ap.add_argument("--tokens-per-chunk", type=int, default=512, help="--op extend: chunk length")
+    ap.add_argument("--prefix", type=int, default=4096, help="--op extend: cached tokens before the chunk")
     ap.add_argument("--copy-pairs", type=int, default=4096, help="--op copy: block pairs")
     ap.add_argument("--handoff-blocks", type=int, default=2048,
                     help="--op wire: blocks handed off (all layers)")
@@ -424,6 +431,81 @@ def bench_move(args):
     }), flush=True)
 
 
+PEAK_BF16_TFLOPS = 2500.0  # dense bf16 MFMA, MI355X
+
+
+def bench_extend(args):
+    """Chunked-prefill attention of one layer at the config's head geometry:
+    `--extend-seqs` sequences, each a chunk of `--tokens-per-chunk` new
+    tokens after `--prefix` cached ones (the chunk's K/V already in the pool;
+    block tables from a seeded permutation). FLOPs are the causal ones: a
+    query at position p attends p + 1 keys, 4 * head_dim per (query head,
+    key) for QK^T and PV."""
+    import torch
+
+    from mitten_amd import DeviceKvPool, PoolDesc
+    from mitten_amd import workloads as wl
+
+    cfg = wl.CONFIGS[args.config]
+    Hq, Hkv, D = cfg["num_q_heads"], cfg["num_kv_heads"], cfg["head_dim"]
+    B, n, prefix = args.extend_seqs, args.tokens_per_chunk, args.prefix
+    ctx = [prefix + n] * B
+    rng = wl.SplitMix64(wl.BASE_SEED + 31)
+    batch = wl.decode_batch_from_contexts([c - 1 for c in ctx], rng)
+    desc = PoolDesc(1, Hkv, Hq, D, batch.num_blocks, "bf16")
+    dev = torch.device("cuda:0")
+    i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(dev)
+    stream = torch.cuda.current_stream()
+    with DeviceKvPool(desc) as pool:
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(wl.BASE_SEED + 31)
+        view = pool.tensor()
+        view[0].normal_(generator=gen)
+        del view
+        q = torch.randn((B * n, Hq, D), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
+        out = torch.empty_like(q)
+        qi, ip, ix, cl = (i32(np.arange(B + 1) * n), i32(batch.block_indptr), i32(batch.block_ids),
+                          i32(batch.ctx_lens))
+
+        def launch():
+            pool.extend_attention(0, q, qi, ip, ix, cl, n, max(ctx), out=out, stream=stream)
+
+        for _ in range(args.warmup):
+            launch()
+        torch.cuda.synchronize()
+        pool.check()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(args.steps)]
+        t0 = time.perf_counter()
+        for a_, b_ in evs:
+            a_.record(stream)
+            launch()
+            b_.record(stream)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        pool.check()
+    launch_s = float(np.mean([a_.elapsed_time(b_) for a_, b_ in evs])) / 1e3
+    keys = B * sum(prefix + i + 1 for i in range(n))
+    flops = 4.0 * D * Hq * keys
+    tf = flops / launch_s / 1e12
+    kv_bytes = B * (prefix + n) * 2 * Hkv * D * 2
+    print(json.dumps({
+        "metric": "chunked-prefill (extend) attention achieved TFLOP/s",
+        "value": round(tf, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(elapsed / args.steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: N(0,1) K/V and Q from a seed; block tables from a seeded permutation",
+        "config": {"workload": f"{args.config}-shaped extend attention, one layer", "sequences": B,
+                   "chunk_tokens": n, "prefix_tokens": prefix, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D},
+        "tokens_per_s": round(B * n / launch_s, 1),
+        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None, "kernel": "mkv_extend_attention",
+                     "flops_per_launch": flops, "kv_bytes_once": kv_bytes,
+                     "avg_launch_us": round(launch_s * 1e6, 2)},
+        "cpu_baseline": None,
+    }), flush=True)
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -441,6 +523,9 @@ def main():
         return
     if args.op in ("gather", "copy"):
         bench_move(args)
+        return
+    if args.op == "extend":
+        bench_extend(args)
         return
     import torch
 
