@@ -415,6 +415,28 @@ def bench_move(args):
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
         pool.check()
+        # CPU baseline: the oracle's gather (one sequence) or copy_blocks
+        # (64 pairs) on this host, one thread.
+        from oracle import oracle as orc
+
+        host = pool.read()
+        od = orc.desc(L, Hkv, D, batch.num_blocks, desc.elem_bytes)
+        c0 = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - c0 < 2.0 or reps == 0:
+            if args.op == "gather":  # 8 sequences: more than the host's caches hold
+                ns = min(8, batch.num_seqs)
+                hi = batch.block_indptr[ns]
+                orc.gather(od, host, 0, batch.block_indptr[:ns + 1], batch.block_ids[:hi], batch.ctx_lens[:ns])
+                cpu_bytes = 4 * int(batch.ctx_lens[:ns].sum()) * row
+                sample = f"oracle gather of {ns} sequences ({int(batch.ctx_lens[:ns].sum())} tokens)"
+            else:
+                ps = min(64, npairs)
+                orc.copy_blocks(od, host, perm[:ps], perm[npairs:npairs + ps])
+                cpu_bytes = 2 * ps * L * 2 * desc.block_bytes
+                sample = f"oracle copy_blocks of {ps} pairs, all layers"
+            reps += 1
+        cpu_s = (time.perf_counter() - c0) / reps
     launch_s = float(np.mean([a.elapsed_time(b) for a, b in evs])) / 1e3
     gbs = launch_bytes / launch_s / 1e9
     print(json.dumps({
@@ -427,7 +449,8 @@ def bench_move(args):
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "kernel": kernel,
                      "bytes_per_launch": launch_bytes, "avg_launch_us": round(launch_s * 1e6, 2)},
-        "cpu_baseline": None,
+        "cpu_baseline": {"value": round(cpu_bytes / cpu_s / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                         "sample": f"{sample}, {reps} repetitions"},
     }), flush=True)
 
 
@@ -484,9 +507,25 @@ def bench_extend(args):
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
         pool.check()
+        # CPU baseline: the oracle's extend attention (f32, one thread) on the
+        # last 32 tokens of the first sequence's chunk, timed on this host.
+        from oracle import oracle as orc
+
+        host = pool.read()
+        od = orc.desc(1, Hkv, D, batch.num_blocks, 2)
+        ns = min(n, 32)
+        qs = orc.bf16_to_f32(q[n - ns:n].cpu().view(torch.int16).numpy().view(np.uint16))
+        ind = batch.block_ids[batch.block_indptr[0]:batch.block_indptr[1]]
+        c0 = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - c0 < 2.0 or reps == 0:
+            orc.extend_attention(od, host, 0, qs, [0, ns], [0, ind.size], ind, [ctx[0]])
+            reps += 1
+        cpu_s = (time.perf_counter() - c0) / reps
     launch_s = float(np.mean([a_.elapsed_time(b_) for a_, b_ in evs])) / 1e3
     keys = B * sum(prefix + i + 1 for i in range(n))
     flops = 4.0 * D * Hq * keys
+    cpu_flops = 4.0 * D * Hq * sum(ctx[0] - ns + i + 1 for i in range(ns))
     tf = flops / launch_s / 1e12
     kv_bytes = B * (prefix + n) * 2 * Hkv * D * 2
     print(json.dumps({
@@ -502,7 +541,9 @@ def bench_extend(args):
                      "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None, "kernel": "mkv_extend_attention",
                      "flops_per_launch": flops, "kv_bytes_once": kv_bytes,
                      "avg_launch_us": round(launch_s * 1e6, 2)},
-        "cpu_baseline": None,
+        "cpu_baseline": {"value": round(cpu_flops / cpu_s / 1e12, 5), "unit": "TFLOP/s", "cores": 1,
+                         "kind": "port", "sample": f"oracle extend attention (f32) of the last {ns} tokens of "
+                                                   f"one {n}-token chunk after {prefix}, {reps} repetitions"},
     }), flush=True)
 
 
