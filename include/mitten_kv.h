@@ -227,13 +227,15 @@ MKV_API int mkv_decode_step(mkv_pool *pool, const mkv_decode_plan *plan, int32_t
  * sequence b has n_b = d_q_indptr[b+1] - d_q_indptr[b] query tokens at
  * positions [ctx_b - n_b, ctx_b) (ctx_b = d_ctx_lens[b], the chunk's K/V
  * already appended with mkv_append); the query at position p attends keys
- * 0..p. d_q, d_o: [d_q_indptr[num_seqs]][num_q_heads][head_dim], bf16.
+ * 0..p. d_q, d_o: [d_q_indptr[num_seqs]][num_q_heads][head_dim].
  * max_q_len / max_ctx_len bound n_b / ctx_b (a larger ctx_b is skipped and
- * reported, MKV_DEVERR_CTX). Needs a bf16 pool, head_dim 64/128/256 and at
- * most 16 query heads per KV head. Flags: MKV_ATTN_ZERO_SINK.
+ * reported, MKV_DEVERR_CTX). Any pool: bf16 pools with head_dim 64/128/256
+ * and at most 16 query heads per KV head run MFMA query tiles; other pools
+ * (f32, head_dim 32, larger groups) run one decode segment per query token.
+ * Flags: MKV_ATTN_ZERO_SINK.
  * Replaces the seq_q > 1 path of inference-model-qwen/src/model.rs:410-416
  * with its causal mask (model.rs:542-555), for the chunks scheduled by
- * inference-engine/src/prefill.rs:99-114. */
+ * inference-engine/src/prefill.rs:99-114. d_q / d_o are in the pool dtype. */
 MKV_API int mkv_extend_attention(mkv_pool *pool, int32_t layer, const void *d_q, void *d_o,
                                  const int32_t *d_q_indptr, const int32_t *d_block_indptr,
                                  const int32_t *d_block_ids, const int32_t *d_ctx_lens, int32_t num_seqs,

@@ -613,6 +613,59 @@ __global__ void __launch_bounds__(256) attn_split_kernel(KArgs a, SplitArgs sp) 
   run_segment<D, BF16, MFMA>(a, sg, lane, nsp == 1, ((int64_t)sg.b * a.Hq) * sp.S + split, sp.S);
 }
 
+// Extend attention on the decode kernels' per-sequence segments, for pools
+// the MFMA extend kernel does not take (f32, head_dim 32, more than 16
+// query heads per KV head): query token t of sequence b, at position p,
+// is decode attention over keys 0..p through b's block table, with q and o
+// rows addressed by t (a virtual sequence per token). One unit per
+// (token, KV head, query-head chunk), whole context, final stores.
+struct ExtSplitArgs {
+  const int32_t *q_indptr;  // [B+1]
+  const int32_t *ctx;       // [B] tokens in the cache, the chunk included
+  int64_t total_units;      // tokens (upper bound) * Hkv * nqc
+  int32_t B, max_ctx;
+};
+
+template <int D, bool BF16, bool MFMA>
+__global__ void __launch_bounds__(256) attn_ext_split_kernel(KArgs a, ExtSplitArgs x) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int64_t id = (int64_t)blockIdx.x * 4 + wave;
+  if (id >= x.total_units) return;
+  Seg sg;
+  sg.qc = (int)(id % a.nqc);
+  id /= a.nqc;
+  sg.h = (int)(id % a.Hkv);
+  const int t = (int)(id / a.Hkv);
+  if (t >= x.q_indptr[x.B]) return;
+  int lo = 0, hi = x.B - 1;  // the sequence holding token t: last b with q_indptr[b] <= t
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (x.q_indptr[mid] <= t) lo = mid;
+    else hi = mid - 1;
+  }
+  const int b = lo;
+  const int q0 = x.q_indptr[b], nq = x.q_indptr[b + 1] - q0, ctx = x.ctx[b];
+  const bool first = t == q0 && sg.h == 0 && sg.qc == 0 && lane == 0;
+  if (t < q0 || nq < 1 || nq > ctx || ctx > x.max_ctx) {
+    if (first || (t < q0 && sg.h == 0 && sg.qc == 0 && lane == 0)) record_error(a.d_err, MKV_DEVERR_CTX);
+    return;
+  }
+  const int nb = (ctx + kPageSize - 1) / kPageSize;
+  const int tab0 = a.indptr[b];
+  if (tab0 < 0 || a.indptr[b + 1] - tab0 < nb) {
+    if (first) record_error(a.d_err, MKV_DEVERR_TABLE);
+    return;
+  }
+  sg.b = t;
+  sg.ctx = ctx - nq + (t - q0) + 1;  // keys 0..p
+  sg.table = a.ids + tab0;
+  sg.j0 = 0;
+  sg.j1 = (sg.ctx + kPageSize - 1) / kPageSize;
+  sg.nk = sg.nv = nullptr;
+  run_segment<D, BF16, MFMA>(a, sg, lane, true, 0, 1);
+}
+
 template <int D, bool BF16>
 __global__ void __launch_bounds__(256) merge_split_kernel(KArgs a, SplitArgs sp) {
   const int lane = threadIdx.x & 63;
@@ -1938,9 +1991,6 @@ extern "C" int mkv_extend_attention(mkv_pool *pool, int32_t layer, const void *d
   bool use_mfma = false;
   int rc = check_common(p, layer, flags, scale, use_mfma);
   if (rc) return rc;
-  if (!use_mfma)
-    return set_error(MKV_ERR_INVALID_ARGUMENT,
-                     "extend attention needs a bf16 pool with head_dim 64/128/256");
   if (!d_q || !d_o || !d_q_indptr || !d_block_indptr || !d_block_ids || !d_ctx_lens)
     return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL device pointer");
   if (num_seqs < 0 || max_q_len < 0 || max_ctx_len < 0)
@@ -1949,8 +1999,24 @@ extern "C" int mkv_extend_attention(mkv_pool *pool, int32_t layer, const void *d
   if (max_q_len > max_ctx_len)
     return set_error(MKV_ERR_INVALID_ARGUMENT, "max_q_len %d > max_ctx_len %d", max_q_len, max_ctx_len);
   const int G = g.Hq / g.Hkv;
-  if (G > 16) return set_error(MKV_ERR_INVALID_ARGUMENT, "extend attention supports <= 16 query heads per KV head");
   if (!aligned16(d_q) || !aligned16(d_o)) return set_error(MKV_ERR_INVALID_ARGUMENT, "q and o must be 16-byte aligned");
+  if (!use_mfma || G > 16) {  // per-token segments on the decode kernels (see attn_ext_split_kernel)
+    const int64_t tokens = (int64_t)num_seqs * max_q_len;  // upper bound; the kernel reads q_indptr[B]
+    DeviceGuard guard(p->device);
+    hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+    KArgs a = make_kargs(p, layer, d_q, d_o, d_block_indptr, d_block_ids, scale, flags, use_mfma);
+    ExtSplitArgs x;
+    x.q_indptr = d_q_indptr;
+    x.ctx = d_ctx_lens;
+    x.B = num_seqs;
+    x.max_ctx = max_ctx_len;
+    x.total_units = tokens * g.Hkv * a.nqc;
+    const int64_t wgs = (x.total_units + 3) / 4;
+    if (wgs > INT32_MAX) return set_error(MKV_ERR_INVALID_ARGUMENT, "launch too large");
+    MKV_DISPATCH(attn_ext_split_kernel, dim3((unsigned)wgs), dim3(256), hs, a, x);
+    MKV_CHECK_LAUNCH("attn_ext_split_kernel");
+    return MKV_OK;
+  }
   const int64_t tiles = ((int64_t)max_q_len + 15) / 16;
   if (tiles * g.Hkv * num_seqs + 8 > INT32_MAX) return set_error(MKV_ERR_INVALID_ARGUMENT, "grid too large");
   DeviceGuard guard(p->device);

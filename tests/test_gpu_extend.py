@@ -1,8 +1,10 @@
 """GPU parity of extend (chunked prefill) attention through the C ABI:
 each sequence's newest tokens attend causally over the whole cache,
-against the oracle (bf16 row-relative 2e-2), plus the identities the
-oracle tests pin (the chunk's last query equals decode attention) and the
-error paths."""
+against the oracle (bf16 row-relative 2e-2, f32 max-abs 1e-5), plus the
+identities the oracle tests pin (the chunk's last query equals decode
+attention) and the error paths. Both paths: MFMA query tiles (bf16,
+head_dim 64/128/256, up to 16 query heads per KV head) and per-token
+decode segments (everything else)."""
 from __future__ import annotations
 
 import numpy as np
@@ -25,6 +27,15 @@ SHAPES = {
     "g16": (64, 4, 128),
     "mha": (4, 4, 64),
 }
+# Shapes the MFMA tile kernel does not take (per-token segments instead).
+SEGMENT_SHAPES = {
+    # name: (Hq, Hkv, D, dtype)
+    "qwen0.5b-f32": (14, 2, 64, "f32"),   # the reference's CPU-runnable configuration
+    "d32-f32": (8, 4, 32, "f32"),
+    "d128-f32": (28, 4, 128, "f32"),
+    "g32-bf16": (64, 2, 128, "bf16"),     # 32 query heads per KV head
+    "d32-bf16": (8, 2, 32, "bf16"),
+}
 
 
 def _i32(a):
@@ -33,14 +44,15 @@ def _i32(a):
     return torch.from_numpy(np.ascontiguousarray(a, np.int32)).cuda()
 
 
-def _case(shape, ctx, nq, seed, zero_sink=False, layer=1):
-    Hq, Hkv, D = SHAPES[shape]
+def _case(shape, ctx, nq, seed, zero_sink=False, layer=1, dtype="bf16"):
+    """shape: a SHAPES name or an (Hq, Hkv, D) tuple."""
+    Hq, Hkv, D = SHAPES[shape] if isinstance(shape, str) else shape
     rng = wl.SplitMix64(seed)
     batch = wl.decode_batch_from_contexts([c - 1 for c in ctx], rng, extra_blocks=2)
-    desc = PoolDesc(2, Hkv, Hq, D, batch.num_blocks, "bf16")
-    host = normal(seed + 1, desc.shape, "bf16")
+    desc = PoolDesc(2, Hkv, Hq, D, batch.num_blocks, dtype)
+    host = normal(seed + 1, desc.shape, dtype)
     q_indptr = np.concatenate([[0], np.cumsum(nq)]).astype(np.int32)
-    q = normal(seed + 2, (int(q_indptr[-1]), Hq, D), "bf16")
+    q = normal(seed + 2, (int(q_indptr[-1]), Hq, D), dtype)
     with DeviceKvPool(desc) as pool:
         pool.write(host)
         o = pool.extend_attention(layer, to_device(q), _i32(q_indptr), _i32(batch.block_indptr),
@@ -110,6 +122,19 @@ def test_extend_errors_are_reported():
     with DeviceKvPool(f32) as pool:
         import torch
 
-        q = torch.zeros((2, 14, 64), dtype=torch.float32, device="cuda")
-        with pytest.raises(BackendError):  # needs a bf16 pool
+        q = torch.zeros((2, 14, 64), dtype=torch.bfloat16, device="cuda")
+        with pytest.raises(BackendError):  # q must be in the pool dtype
             pool.extend_attention(0, q, _i32([0, 2]), _i32([0, 1]), _i32([0]), _i32([2]), 2, 2)
+
+
+@pytest.mark.parametrize("name", list(SEGMENT_SHAPES))
+def test_extend_segment_path_matches_oracle(name):
+    """f32 pools, head_dim 32 and groups above 16 run one decode segment per
+    query token: f32 within max-abs 1e-5, bf16 within row-relative 2e-2."""
+    Hq, Hkv, D, dt = SEGMENT_SHAPES[name]
+    ctx, nq = [1, 17, 40, 300, 97], [1, 17, 25, 64, 1]
+    got, ref, dec, q_indptr = _case((Hq, Hkv, D), ctx, nq, 95, dtype=dt)
+    assert_attention_close(got, ref, dt)
+    assert_attention_close(dec, ref[q_indptr[1:] - 1], dt)
+    got, ref, _, _ = _case((Hq, Hkv, D), [50, 33], [20, 33], 96, zero_sink=True, dtype=dt)
+    assert_attention_close(got, ref, dt)

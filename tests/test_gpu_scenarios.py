@@ -55,7 +55,7 @@ def _sub_batch(indptr, ids, ctx, rows):
 
 # --------------------------------------------------------------------- C1 ----
 
-def test_c1_prompt_append_then_decode_gather_attention():
+def test_c1_prompt_append_prefill_then_decode_gather_attention():
     c = wl.CONFIGS["qwen2.5-0.5b"]
     L, Hq, Hkv, D = c["num_layers"], c["num_q_heads"], c["num_kv_heads"], c["head_dim"]
     rng = wl.SplitMix64(wl.BASE_SEED + c["index"])
@@ -83,6 +83,17 @@ def test_c1_prompt_append_then_decode_gather_attention():
             assert orc.append(od, want, layer, k[layer], v[layer], slots) == -1
         pool.check()
         assert np.array_equal(bits(pool.read()), bits(want))
+        # Prefill attention of the prompts (causal, whole prompt as the chunk),
+        # first and last layer.
+        indptr, ids, ctx = bm.batch(list(range(B)))
+        q_indptr = np.concatenate([[0], np.cumsum(prompts)]).astype(np.int32)
+        for layer in (0, L - 1):
+            qp = normal(4000 + layer, (int(q_indptr[-1]), Hq, D), "f32")
+            o = pool.extend_attention(layer, to_device(qp), _i32(q_indptr), _i32(indptr), _i32(ids), _i32(ctx),
+                                      max(prompts), int(ctx.max()))
+            pool.check()
+            ref = orc.extend_attention(od, want, layer, qp, q_indptr, indptr, ids, ctx)
+            assert_attention_close(to_host(o), ref, "f32")
         for step in range(steps):
             new = np.concatenate([bm.append(s, 1)[0] for s in range(B)]).astype(np.int32)
             indptr, ids, ctx = bm.batch(list(range(B)))
