@@ -143,6 +143,21 @@ def cpu_baseline(cfg, batch, step_bytes, layers):
     orc.set_num_threads(threads)
     tn = orc.ref_faithful_batch(ctx, cfg["num_kv_heads"], cfg["num_q_heads"], cfg["head_dim"], seed=100)
     step_1t, step_nt = t1 / layers * cfg["num_layers"], tn * cfg["num_layers"]
+    # Second line: the efficient paged oracle (f32 accumulation over a bf16 /
+    # f32 pool, threaded over sequences and heads) on one layer of the same
+    # batch, K/V from a seeded host pool of the same blocks; scaled to a step.
+    es = 2 if cfg["dtype"] == "bf16" else 4
+    od = orc.desc(1, cfg["num_kv_heads"], cfg["head_dim"], batch.num_blocks, es)
+    raw = np.random.default_rng(7).standard_normal(orc.pool_bytes(od) // es, dtype=np.float32)
+    host = orc.f32_to_bf16(raw) if es == 2 else raw
+    del raw
+    q = np.random.default_rng(8).standard_normal((batch.num_seqs, cfg["num_q_heads"], cfg["head_dim"]),
+                                                 dtype=np.float32)
+    c0 = time.perf_counter()
+    orc.decode_attention(od, host, 0, q, batch.block_indptr, batch.block_ids, ctx)
+    tp = time.perf_counter() - c0
+    del host
+    step_p = tp * cfg["num_layers"]
     return {
         "value": round(step_bytes / step_1t / 1e9, 3),
         "unit": "GB/s",
@@ -155,6 +170,10 @@ def cpu_baseline(cfg, batch, step_bytes, layers):
         "threaded": {"value": round(step_bytes / step_nt / 1e9, 3), "unit": "GB/s", "cores": threads,
                      "tokens_per_s": round(batch.num_seqs / step_nt, 2),
                      "sample": f"1 layer of the sample, {threads} threads over sequences, {tn:.1f} s"},
+        "paged_oracle": {"value": round(step_bytes / step_p / 1e9, 3), "unit": "GB/s", "cores": threads,
+                         "tokens_per_s": round(batch.num_seqs / step_p, 2),
+                         "sample": f"oracle paged decode attention, 1 layer of all {batch.num_seqs} sequences, "
+                                   f"{threads} threads, {tp:.2f} s; scaled to a full step"},
         "cpu_model": cpu_info(),
         "host_cpus": os.cpu_count(),
     }
