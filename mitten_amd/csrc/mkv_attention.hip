@@ -1751,6 +1751,47 @@ extern "C" int mkv_decode_plan_destroy(mkv_decode_plan *plan) {
   return MKV_OK;
 }
 
+// Workgroups of the cooperative decode kernel the device holds at once
+// (CUs x resident workgroups per CU for the instantiation the pool's
+// geometry selects), or 0 when that kernel does not apply. Pieces beyond it
+// run in a second round; fewer leave CUs idle. Queried once per pool.
+static int64_t coop_resident(Pool *p) {
+  if (p->coop_slots >= 0) return p->coop_slots;
+  const Geom &g = p->g;
+  p->coop_slots = 0;
+  const int G = g.Hq / g.Hkv;
+  if (!mfma_applies(g) || G > kQChunkMfma || !(g.Hkv == 1 || g.Hkv == 2 || g.Hkv == 4)) return 0;
+  const int ql = (g.Hq * g.D / 8 + 64 * g.Hkv - 1) / (64 * g.Hkv);
+  if (ql > 4) return 0;
+  const void *fn = nullptr;
+#define MKV_COOP_FN(DD, WW)                                                                        \
+  fn = ql == 1   ? reinterpret_cast<const void *>(&attn_coop_kernel<DD, WW, 1, kCoopRing>)        \
+       : ql == 2 ? reinterpret_cast<const void *>(&attn_coop_kernel<DD, WW, 2, kCoopRing>)        \
+                 : reinterpret_cast<const void *>(&attn_coop_kernel<DD, WW, 4, kCoopRing - 1>)
+#define MKV_COOP_FN_W(DD)              \
+  do {                                 \
+    if (g.Hkv == 1) MKV_COOP_FN(DD, 1); \
+    else if (g.Hkv == 2) MKV_COOP_FN(DD, 2); \
+    else MKV_COOP_FN(DD, 4);            \
+  } while (0)
+  switch (g.D) {
+    case 64: MKV_COOP_FN_W(64); break;
+    case 128: MKV_COOP_FN_W(128); break;
+    default: MKV_COOP_FN_W(256); break;
+  }
+#undef MKV_COOP_FN_W
+#undef MKV_COOP_FN
+  DeviceGuard guard(p->device);
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 64 * g.Hkv, 0) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, p->device) != hipSuccess) {
+    (void)hipGetLastError();  // leave no sticky error: fall back to the fixed rule
+    return 0;
+  }
+  p->coop_slots = per_cu > 0 && cus > 0 ? (int64_t)per_cu * cus : 0;
+  return p->coop_slots;
+}
+
 extern "C" int mkv_decode_plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens,
                                      int32_t num_seqs, int32_t pieces, void *stream) {
   if (!plan) return set_error(MKV_ERR_INVALID_ARGUMENT, "plan is NULL");
@@ -1764,11 +1805,13 @@ extern "C" int mkv_decode_plan_build(mkv_decode_plan *plan, const int32_t *h_ctx
     total += (h_ctx_lens[b] + kPageSize - 1) / kPageSize;
   }
   if (total > INT32_MAX / 2) return set_error(MKV_ERR_INVALID_ARGUMENT, "batch too large");
-  // Workgroup slots: ~8 waves per CU on 256 CUs, one wave per (KV head,
-  // query chunk); a piece is one workgroup row of the grid.
+  // Pieces: as many as the cooperative kernel's resident workgroups (one
+  // round), else ~8 waves per CU on 256 CUs, one wave per (KV head, query
+  // chunk); a piece is one workgroup of the grid.
   const int G = g.Hq / g.Hkv;
   const int nqc = (G + kQChunkMfma - 1) / kQChunkMfma;
-  int64_t P = pieces ? pieces : std::max<int64_t>(1, 2048 / std::max(1, g.Hkv * nqc));
+  const int64_t resident = pieces ? 0 : coop_resident(pl->pool);
+  int64_t P = pieces ? pieces : resident ? resident : std::max<int64_t>(1, 2048 / std::max(1, g.Hkv * nqc));
   P = std::max<int64_t>(P, (total + 63) / 64);  // a piece is at most 64 blocks (one per lane)
   P = std::min<int64_t>(P, total);
   std::vector<int32_t> blk0v(num_seqs + 1);

@@ -34,6 +34,7 @@ struct Pool {
   uint32_t *d_err = nullptr; // device error word
   void *ws = nullptr;        // pool-owned attention workspace
   uint64_t ws_bytes = 0;
+  int64_t coop_slots = -1;   // resident workgroups of the decode kernel (-1: not yet queried)
 };
 
 // Thread-local last-error message and status helpers.
