@@ -1243,7 +1243,7 @@ __device__ __forceinline__ bool ext_tile(const ExtArgs &e, int Hkv, int &t, int 
   return true;
 }
 
-template <int D, int W, int KB, int R>
+template <int D, int W, int KB, int R, int TP>
 __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e) {
   constexpr int NR = D / 32, NT = D / 16;
   constexpr int RB = D * 2;                           // LDS tile row: one head's K or V row
@@ -1253,6 +1253,8 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
   constexpr int NCH = KB * BCH;                       // chunks of one step (KB blocks)
   constexpr int LPL = (NCH + 64 * W - 1) / (64 * W);  // loads per lane per step
   static_assert(R % 2 == 0, "even ring: stage s of an unrolled round uses LDS buffer s & 1");
+  constexpr int WG = W / TP;                          // waves per 16-position sub-tile
+  static_assert(W % TP == 0, "whole sub-tiles per workgroup");
   __shared__ __attribute__((aligned(16))) uint8_t tiles[2][KB][2][TILE];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1260,7 +1262,7 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
   int t, h, b;
   if (!ext_tile(e, a.Hkv, t, h, b)) return;
   const int q0 = e.q_indptr[b], nq = e.q_indptr[b + 1] - q0;
-  if (nq <= 0 || 16 * t >= nq) return;
+  if (nq <= 0 || 16 * TP * t >= nq) return;
   const int ctx = e.ctx[b];
   if (nq > ctx || ctx > e.max_ctx) {
     if (threadIdx.x == 0 && t == 0) record_error(a.d_err, MKV_DEVERR_CTX);
@@ -1276,19 +1278,23 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
   // id needs vmcnt(0) before its readfirstlane).
   typedef const __attribute__((address_space(4))) int32_t const_i32;
   const const_i32 *table = (const const_i32 *)(a.ids + tab0);
-  const int qlo = ctx - nq + 16 * t;          // first query position of the tile
-  const int qhi = min(qlo + 15, ctx - 1);     // last valid one
-  const int n = qhi / kPageSize + 1;          // blocks holding keys 0..qhi
-  const int nsteps = (n + KB - 1) / KB;       // steps of KB blocks
-  const bool computes = wave < a.G;
-  const int hq = h * a.G + min(wave, a.G - 1);
+  // The workgroup holds TP sub-tiles of 16 positions; wave = (sub-tile, head slot).
+  const int sub = wave / WG, hw = wave % WG;
+  const int row0 = 16 * (TP * t + sub);                  // first chunk row of this wave's sub-tile
+  const int qlo = ctx - nq + row0;                       // its first query position
+  const int qhi_wg = min(ctx - nq + 16 * TP * (t + 1) - 1, ctx - 1);
+  const int n = qhi_wg / kPageSize + 1;                  // blocks the workgroup streams: keys 0..qhi_wg
+  const int nw = min(n, (qlo + 15) / kPageSize + 1);     // blocks this wave's sub-tile sees
+  const int nsteps = (n + KB - 1) / KB;                  // steps of KB blocks
+  const bool computes = hw < a.G;
+  const int hq = h * a.G + min(hw, a.G - 1);
   const int qp = qlo + m16;                   // this lane's query position (rows past nq: unused)
   const int64_t spare = dummy_offset(a);
 
   // Q^T operand: lane holds Q[row 16t + lane%16][32r + 8*(lane/16) .. +8].
   bf16x8 qop[NR];
   {
-    const int row = min(16 * t + m16, nq - 1);
+    const int row = min(row0 + m16, nq - 1);
     const uint8_t *qp8 = static_cast<const uint8_t *>(a.q) + ((int64_t)(q0 + row) * a.Hq + hq) * D * 2;
 #pragma unroll
     for (int r = 0; r < NR; r++)
@@ -1374,7 +1380,7 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
 #pragma unroll
     for (int kb = 0; kb < KB; kb++) {
       const int k = step * KB + kb;
-      if (KB > 1 && k >= n) {  // uniform: blocks past n exist only in the last step
+      if (k >= nw) {  // uniform: past this sub-tile's last position (or past n in the last step)
 #pragma unroll
         for (int i = 0; i < 4; i++) sr[kb][i] = -INFINITY;
         masked = true;
@@ -1422,7 +1428,7 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
 #pragma unroll
     for (int kb = 0; kb < KB; kb++) {
       const int k = step * KB + kb;
-      if (k >= n) continue;  // uniform
+      if (k >= nw) continue;  // uniform
       float pr[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) pr[i] = fast_exp2(fmaf(sr[kb][i], a.sl2, -st.m));
@@ -1460,7 +1466,7 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
   if (!computes) return;
   st.l += __shfl_xor(st.l, 16);
   st.l += __shfl_xor(st.l, 32);
-  const int row = 16 * t + m16;
+  const int row = row0 + m16;
   if (row >= nq) return;
   const float f = final_scale(st.m, st.l, a.zero_sink);
   uint16_t *op = reinterpret_cast<uint16_t *>(a.o) + ((int64_t)(q0 + row) * a.Hq + hq) * D + 4 * g4;
@@ -2101,8 +2107,8 @@ extern "C" int mkv_extend_attention(mkv_pool *pool, int32_t layer, const void *d
     MKV_CHECK_LAUNCH("attn_ext_split_kernel");
     return MKV_OK;
   }
-  const int64_t tiles = ((int64_t)max_q_len + 15) / 16;
-  if (tiles * g.Hkv * num_seqs + 8 > INT32_MAX) return set_error(MKV_ERR_INVALID_ARGUMENT, "grid too large");
+  if (((int64_t)max_q_len + 15) / 16 * g.Hkv * num_seqs + 8 > INT32_MAX)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "grid too large");
   DeviceGuard guard(p->device);
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
   KArgs a = make_kargs(p, layer, d_q, d_o, d_block_indptr, d_block_ids, scale, flags, true);
@@ -2111,26 +2117,34 @@ extern "C" int mkv_extend_attention(mkv_pool *pool, int32_t layer, const void *d
   e.ctx = d_ctx_lens;
   e.B = num_seqs;
   e.max_ctx = max_ctx_len;
-  // Linear workgroup index -> (tile, KV head, sequence), grouped by XCD.
-  const int64_t total = tiles * g.Hkv * num_seqs;
+  // Waves per 16-position sub-tile: the next power of two >= G. Two
+  // sub-tiles per workgroup share each K/V tile (K/V streamed once per 32
+  // positions) where that stays within 16 waves and their register budget
+  // (head_dim <= 128) and chunks are longer than one sub-tile. Measured at
+  // Qwen-7B heads: 8 x 512 after 4k 526 -> 480 us, 8 x 2,048 prompts 560 ->
+  // 534 us; 16-token chunks would leave half the waves idle (168 -> 220 us).
+  const int WG = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : G <= 8 ? 8 : 16;
+  const int TP = (WG <= 8 && g.D <= 128 && max_q_len > 16) ? 2 : 1;
+  const int W = WG * TP;
+  const int64_t tiles = ((int64_t)max_q_len + 16 * TP - 1) / (16 * TP);
+  const int64_t total = tiles * g.Hkv * num_seqs;  // linear index -> (tile, KV head, sequence), grouped by XCD
   e.tiles = (int32_t)tiles;
   e.per_xcd = (int32_t)((total + 7) / 8);
-  const int W = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : G <= 8 ? 8 : 16;
   const dim3 grid((unsigned)(8 * (int64_t)e.per_xcd)), block(64 * W);
-#define MKV_EXT(DD)                                                                       \
-  do {                                                                                    \
-    switch (W) {                                                                          \
-      case 1: hipLaunchKernelGGL((attn_extend_kernel<DD, 1, kExtKB, kExtR>), grid, block, 0, hs, a, e); break;  \
-      case 2: hipLaunchKernelGGL((attn_extend_kernel<DD, 2, kExtKB, kExtR>), grid, block, 0, hs, a, e); break;  \
-      case 4: hipLaunchKernelGGL((attn_extend_kernel<DD, 4, kExtKB, kExtR>), grid, block, 0, hs, a, e); break;  \
-      case 8: hipLaunchKernelGGL((attn_extend_kernel<DD, 8, kExtKB, kExtR>), grid, block, 0, hs, a, e); break;  \
-      default: hipLaunchKernelGGL((attn_extend_kernel<DD, 16, kExtKB, kExtR>), grid, block, 0, hs, a, e); break; \
-    }                                                                                     \
+#define MKV_EXT(DD, TT)                                                                                 \
+  do {                                                                                                  \
+    switch (W / TT) {                                                                                   \
+      case 1: hipLaunchKernelGGL((attn_extend_kernel<DD, 1 * TT, kExtKB, kExtR, TT>), grid, block, 0, hs, a, e); break; \
+      case 2: hipLaunchKernelGGL((attn_extend_kernel<DD, 2 * TT, kExtKB, kExtR, TT>), grid, block, 0, hs, a, e); break; \
+      case 4: hipLaunchKernelGGL((attn_extend_kernel<DD, 4 * TT, kExtKB, kExtR, TT>), grid, block, 0, hs, a, e); break; \
+      case 8: hipLaunchKernelGGL((attn_extend_kernel<DD, 8 * TT, kExtKB, kExtR, TT>), grid, block, 0, hs, a, e); break; \
+      default: hipLaunchKernelGGL((attn_extend_kernel<DD, 16, kExtKB, kExtR, 1>), grid, block, 0, hs, a, e); break;   \
+    }                                                                                                   \
   } while (0)
   switch (g.D) {
-    case 64: MKV_EXT(64); break;
-    case 128: MKV_EXT(128); break;
-    default: MKV_EXT(256); break;
+    case 64: if (TP == 2) MKV_EXT(64, 2); else MKV_EXT(64, 1); break;
+    case 128: if (TP == 2) MKV_EXT(128, 2); else MKV_EXT(128, 1); break;
+    default: MKV_EXT(256, 1); break;
   }
 #undef MKV_EXT
   MKV_CHECK_LAUNCH("attn_extend_kernel");

@@ -87,6 +87,15 @@ def test_extend_attention_zero_sink():
     assert_attention_close(got, ref, "bf16")
 
 
+@pytest.mark.parametrize("shape", ["qwen7b", "qwen0.5b", "mha"])
+def test_extend_short_chunks(shape):
+    """Chunks of at most 16 tokens (one query sub-tile per workgroup) after
+    prefixes of assorted lengths."""
+    got, ref, dec, q_indptr = _case(shape, [16, 300, 1000, 47, 8], [16, 1, 9, 16, 3], 97)
+    assert_attention_close(got, ref, "bf16")
+    assert_attention_close(dec, ref[q_indptr[1:] - 1], "bf16")
+
+
 def test_extend_long_context_chunk():
     """A 512-token chunk at the end of an 8k context (the pool-pressure
     configuration's chunked prefill)."""
