@@ -220,6 +220,171 @@ __global__ void __launch_bounds__(256) qk_norm_rope_append_kernel(PrepArgs a) {
   }
 }
 
+
+// Sum over the LPR lanes of each row group (LPR = 4, 8, ..., 64 consecutive
+// lanes); every lane of the group gets the same bits (each step adds two
+// values that are equal up to the order of a commutative addition).
+template <int LPR>
+__device__ __forceinline__ float row_sum(float v) {
+  v += dpp_f<0xb1>(v);                             // quad_perm [1,0,3,2]: lane ^ 1
+  if constexpr (LPR >= 4) v += dpp_f<0x4e>(v);     // quad_perm [2,3,0,1]: lane ^ 2
+  if constexpr (LPR >= 8) v += dpp_f<0x141>(v);    // row_half_mirror: the other quad
+  if constexpr (LPR >= 16) v += dpp_f<0x140>(v);   // row_mirror: the other half-row
+  if constexpr (LPR >= 32) v += __shfl_xor(v, 16);
+  if constexpr (LPR >= 64) v += __shfl_xor(v, 32);
+  return v;
+}
+
+// Vector form, one wave per token: lane holds VEC = 16 / ES contiguous
+// elements of a head row (one 16-byte load), a row spans LPR = D / VEC lanes
+// and one load instruction covers RPI = 64 / LPR rows. Used when
+// rotary_dim / 2 is a multiple of VEC, so that a lane's elements all rotate
+// or all pass through and their partners (d +- rotary_dim/2) sit at the same
+// element index of lane +- rotary_dim / (2 VEC). Per wave: position and slot
+// by scalar loads, then weights, frequencies, the token's first v chunk and
+// kPrepLoads row loads, all issued before any is used; the token's cos/sin
+// table goes to the wave's own LDS slice (no workgroup barrier: waves of a
+// workgroup are independent tokens).
+constexpr int kPrepTokens = 4;  // waves (tokens) per workgroup
+constexpr int kPrepLoads = 8;   // row loads in flight per lane
+
+template <int D, bool BF16>
+__global__ void __launch_bounds__(256) prep_wave_kernel(PrepArgs a) {
+#pragma clang fp contract(off)
+  constexpr int ES = BF16 ? 2 : 4;
+  constexpr int VEC = 16 / ES;
+  constexpr int LPR = D / VEC;
+  constexpr int RPI = 64 / LPR;
+  __shared__ float cs[kPrepTokens][2][D / 2];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int t = blockIdx.x * kPrepTokens + wave;
+  if (t >= a.n) return;  // wave-uniform
+  typedef const __attribute__((address_space(4))) int32_t const_i32;
+  const int pos = *(const const_i32 *)(a.pos + t);
+  const int64_t slot = *(const const_i32 *)(a.slots + t);
+  const bool slot_ok = slot >= 0 && slot < a.nslots;
+  const int sub = lane % LPR, rin = lane / LPR;
+  const int d0 = sub * VEC;
+  const int heads = a.Hq + a.Hkv;
+  const int half = a.rd >> 1;
+
+  float wq[VEC], wk[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; e += 4) {
+    const float4 q4 = *reinterpret_cast<const float4 *>(a.wq + d0 + e);
+    const float4 k4 = *reinterpret_cast<const float4 *>(a.wk + d0 + e);
+    wq[e] = q4.x, wq[e + 1] = q4.y, wq[e + 2] = q4.z, wq[e + 3] = q4.w;
+    wk[e] = k4.x, wk[e + 1] = k4.y, wk[e + 2] = k4.z, wk[e + 3] = k4.w;
+  }
+  constexpr int NF = (D / 2 + 63) / 64;  // angles per lane
+  float fr[NF];
+#pragma unroll
+  for (int j = 0; j < NF; j++) fr[j] = a.inv_freq[min(lane + 64 * j, max(half - 1, 0))];
+  const int vchunks = (int)(a.row_bytes >> 4);
+  const uint4 *vsrc = reinterpret_cast<const uint4 *>(a.v + (int64_t)t * a.row_bytes);
+  const uint4 v0 = vsrc[min(lane, vchunks - 1)];
+  uint4 xr[kPrepLoads];
+  auto load_rows = [&](int r0) {
+#pragma unroll
+    for (int u = 0; u < kPrepLoads; u++) {
+      const int r = min(r0 + u * RPI + rin, heads - 1);
+      const uint8_t *src = r < a.Hq ? a.q + ((int64_t)t * a.Hq + r) * a.q_head_stride * ES
+                                    : a.k + ((int64_t)t * a.Hkv + (r - a.Hq)) * D * ES;
+      xr[u] = *reinterpret_cast<const uint4 *>(src + (int64_t)d0 * ES);
+    }
+  };
+  load_rows(0);
+
+  float *cw = cs[wave][0], *sw = cs[wave][1];
+#pragma unroll
+  for (int j = 0; j < NF; j++) {  // angle = pos * inv_freq[i], in f32 as the reference forms it
+    const int i = lane + 64 * j;
+    if (i < half) {
+      float sn, c;
+      sincosf((float)pos * fr[j], &sn, &c);
+      cw[i] = c;
+      sw[i] = sn;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < VEC; e++) {  // RMSNorm weight is applied as (1 + w)
+    wq[e] = a.norm ? wq[e] + 1.0f : 1.0f;
+    wk[e] = a.norm ? wk[e] + 1.0f : 1.0f;
+  }
+  if (slot_ok) {  // v rows are appended as is
+    uint4 *vdst = reinterpret_cast<uint4 *>(a.v_plane + slot * a.row_bytes);  // slot s = block s/16, row s%16
+    if (lane < vchunks) vdst[lane] = v0;
+    for (int i = lane + 64; i < vchunks; i += 64) vdst[i] = vsrc[i];
+  } else if (lane == 0) {
+    record_error(a.d_err, MKV_DEVERR_SLOT);
+  }
+  // The table written by other lanes of this wave, read below.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const bool rot = d0 < a.rd;
+  const int i0 = !rot ? 0 : d0 < half ? d0 : d0 - half;
+  const int hl = half / VEC;  // partner distance in lanes
+  const int partner = !rot ? lane : sub < hl ? lane + hl : lane - hl;
+  float c[VEC], sg[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; e++) {
+    c[e] = rot ? cw[i0 + e] : 1.0f;
+    // first half x1*c - x2*s, second half x2*c + x1*s (a - b*s == a + b*(-s) exactly)
+    sg[e] = rot ? (d0 < half ? -sw[i0 + e] : sw[i0 + e]) : 0.0f;
+  }
+
+  for (int r0 = 0; r0 < heads; r0 += kPrepLoads * RPI) {
+    if (r0) load_rows(r0);  // more than kPrepLoads * RPI heads
+#pragma unroll
+    for (int u = 0; u < kPrepLoads; u++) {
+      const int r = r0 + u * RPI + rin;
+      const bool is_q = r < a.Hq;
+      float x[VEC];
+      if constexpr (BF16) {
+        const uint32_t w32[4] = {xr[u].x, xr[u].y, xr[u].z, xr[u].w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          x[2 * j] = __uint_as_float(w32[j] << 16);
+          x[2 * j + 1] = __uint_as_float(w32[j] & 0xffff0000u);
+        }
+      } else {
+        x[0] = __uint_as_float(xr[u].x), x[1] = __uint_as_float(xr[u].y);
+        x[2] = __uint_as_float(xr[u].z), x[3] = __uint_as_float(xr[u].w);
+      }
+      if (a.norm) {  // x * (mean(x^2) + eps)^-1/2, then * (1 + w)
+        float ss = x[0] * x[0];
+#pragma unroll
+        for (int e = 1; e < VEC; e++) ss += x[e] * x[e];
+        const float inv = 1.0f / sqrtf(row_sum<LPR>(ss) / (float)D + a.eps);
+#pragma unroll
+        for (int e = 0; e < VEC; e++) x[e] = (x[e] * inv) * (is_q ? wq[e] : wk[e]);
+      }
+      if (a.rd) {
+#pragma unroll
+        for (int e = 0; e < VEC; e++) {
+          const float other = __shfl(x[e], partner);
+          x[e] = rot ? x[e] * c[e] + other * sg[e] : x[e];
+        }
+      }
+      uint4 o;
+      if constexpr (BF16) {
+        o.x = pack_bf16x2(x[0], x[1]), o.y = pack_bf16x2(x[2], x[3]);
+        o.z = pack_bf16x2(x[4], x[5]), o.w = pack_bf16x2(x[6], x[7]);
+      } else {
+        o.x = __float_as_uint(x[0]), o.y = __float_as_uint(x[1]);
+        o.z = __float_as_uint(x[2]), o.w = __float_as_uint(x[3]);
+      }
+      if (is_q) {
+        *reinterpret_cast<uint4 *>(a.q_out + (((int64_t)t * a.Hq + r) * D + d0) * ES) = o;
+      } else if (r < heads && slot_ok) {
+        *reinterpret_cast<uint4 *>(a.k_plane + slot * a.row_bytes + ((int64_t)(r - a.Hq) * D + d0) * ES) = o;
+      }
+    }
+  }
+}
+
 }  // namespace mkv
 
 using namespace mkv;
@@ -281,11 +446,19 @@ extern "C" int mkv_qk_norm_rope_append(mkv_pool *pool, int32_t layer, const void
   DeviceGuard guard(p->device);
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
   const bool bf = g.dtype == MKV_DTYPE_BF16;
-  const dim3 grid((unsigned)num_tokens), block(256);
-#define MKV_PREP(DD)                                                                         \
-  do {                                                                                       \
-    if (bf) hipLaunchKernelGGL((qk_norm_rope_append_kernel<DD, true>), grid, block, 0, hs, a); \
-    else hipLaunchKernelGGL((qk_norm_rope_append_kernel<DD, false>), grid, block, 0, hs, a);   \
+  // The wave-per-token kernel needs rotary_dim / 2 to be a multiple of its
+  // 16-byte vector (8 bf16 or 4 f32 elements) and reads the weights as
+  // 16-byte vectors; other rotary widths, or unaligned weights, take the
+  // workgroup-per-token kernel (1 to 4 elements per lane).
+  const bool wave_form = rotary_dim % (2 * (bf ? 8 : 4)) == 0 && aligned16(a.wq) && aligned16(a.wk);
+  const dim3 block(256);
+  const dim3 grid(wave_form ? (unsigned)((num_tokens + kPrepTokens - 1) / kPrepTokens) : (unsigned)num_tokens);
+#define MKV_PREP(DD)                                                                              \
+  do {                                                                                            \
+    if (wave_form && bf) hipLaunchKernelGGL((prep_wave_kernel<DD, true>), grid, block, 0, hs, a);  \
+    else if (wave_form) hipLaunchKernelGGL((prep_wave_kernel<DD, false>), grid, block, 0, hs, a);  \
+    else if (bf) hipLaunchKernelGGL((qk_norm_rope_append_kernel<DD, true>), grid, block, 0, hs, a); \
+    else hipLaunchKernelGGL((qk_norm_rope_append_kernel<DD, false>), grid, block, 0, hs, a);        \
   } while (0)
   switch (g.D) {
     case 32: MKV_PREP(32); break;

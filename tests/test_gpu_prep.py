@@ -33,6 +33,12 @@ CASES = {
     "f32-d128": (8, 2, 128, 64, 1e6, "f32", True, True),
     "f32-d256-no-rope": (8, 1, 256, 0, 1e6, "f32", True, True),
     "f32-d32": (4, 2, 32, 16, 1e4, "f32", False, False),
+    # rotary halves that are not a multiple of the 16-byte vector take the
+    # workgroup-per-token kernel; a partner distance of 6 lanes (not a power of 2)
+    "d128-rd8-narrow": (28, 4, 128, 8, 1e6, "bf16", True, True),
+    "f32-d64-rd4-narrow": (14, 2, 64, 4, 1e4, "f32", False, True),
+    "d128-rd96": (28, 4, 128, 96, 1e6, "bf16", True, True),
+    "d256-f32-full": (8, 1, 256, 256, 1e4, "f32", False, True),
 }
 
 
@@ -148,6 +154,39 @@ def test_prep_position_zero_is_norm_only():
         p = pool.read()
     assert np.array_equal(a, b)
     assert np.array_equal(p[0, 0, 0, :5], p[0, 0, 0, 5:10])
+
+
+def test_prep_unaligned_weights():
+    """Norm weights at a 4-byte offset (not 16-byte aligned) take the
+    workgroup-per-token kernel; both launches agree with the oracle."""
+    import torch
+
+    Hq, Hkv, D, n = 28, 4, 128, 9
+    desc = PoolDesc(1, Hkv, Hq, D, 4, "bf16")
+    rng = np.random.default_rng(9)
+    q = orc.f32_to_bf16(rng.standard_normal((n, Hq, 2, D)).astype(np.float32))
+    k = orc.f32_to_bf16(rng.standard_normal((n, Hkv, D)).astype(np.float32))
+    v = orc.f32_to_bf16(rng.standard_normal((n, Hkv, D)).astype(np.float32))
+    w = rng.uniform(-0.5, 0.5, D).astype(np.float32)
+    f = rope_inv_freq(D, 1e6)
+    pos, slots = rng.integers(0, 9000, n).astype(np.int32), np.arange(n, dtype=np.int32)
+    buf = torch.zeros(D + 1, dtype=torch.float32, device="cuda")
+    buf[1:] = torch.from_numpy(w).cuda()
+    outs = []
+    for wt in (_f32(w), buf[1:]):
+        with DeviceKvPool(desc) as pool:
+            pool.write(np.zeros(desc.shape, np.uint16))
+            qo = pool.qk_norm_rope_append(0, to_device(q), to_device(k), to_device(v), _i32(pos), _i32(slots),
+                                          wt, wt, _f32(f))
+            pool.check()
+            outs.append((to_host(qo), pool.read()))
+    ref_pool = np.zeros(desc.shape, np.uint16)
+    ref_q = orc.qk_norm_rope_append(odesc(desc), ref_pool, 0, widen(q), widen(k), widen(v), w, w, f, 1e-6,
+                                    pos, slots)
+    for got_q, got_pool in outs:
+        _close(got_q, ref_q, "bf16", "q")
+        _close(got_pool[0, 0], ref_pool[0, 0], "bf16", "k plane")
+        assert np.array_equal(got_pool[0, 1], ref_pool[0, 1])
 
 
 def test_prep_bad_slot_is_reported_and_skipped():
