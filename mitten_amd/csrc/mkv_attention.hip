@@ -1022,12 +1022,30 @@ __device__ __forceinline__ void mfma_store_t(const KArgs &a, int b, int h, int l
 // nothing waits for them at a sequence boundary.
 //
 // LDS layout: tile rows of RB = W*D*2 bytes with 16-byte chunk c of row r
-// stored at chunk c ^ swz(r) (swz permutes the row's low four chunk bits), so
-// the K reads (16 rows, one chunk each) and V reads (4 rows x 4 chunks) of a
-// 16-lane group hit distinct banks. Q rows (D*2 bytes, [Hq][D] order) use
-// chunk c ^ (row mod chunks-per-row).
+// stored at chunk c ^ swz(r), swz(r) = 2 * (r / rows-per-512-bytes) (2r for
+// rows of 512 bytes or more). Measured with the LDS bank-conflict counter on
+// gfx950, for the K reads (ds_read_b128: rows m16, chunks g4 + 4r) and the
+// transposed V reads (ds_read_b64_tr_b16: 4 rows x 4 half-chunks per 16
+// lanes) of 512- and 1024-byte rows: no conflicts (the previous swizzle, row
+// bits 0-1 and 2-3 swapped: both reads 2-way). Q rows (D*2 bytes, [Hq][D]
+// order) use chunk c ^ (row mod chunks-per-row).
 __device__ __forceinline__ int tile_swz(int row, int cpr) {
-  return (((row & 3) << 2) | ((row >> 2) & 3)) & (cpr - 1);
+  const int rpw = cpr >= 32 ? 1 : 32 / cpr;  // rows per 512 bytes
+  return (2 * (row / rpw)) & (cpr - 1);
+}
+
+// The extend kernel's one-head tiles (rows of 2 * head_dim bytes) take a
+// swizzle per tile, each measured free of bank conflicts at head_dim 64, 128
+// and 256 (no single row swizzle is, for both reads, at all three):
+//   K tile: chunk c of row r at c ^ r          (ds_read_b128 reads)
+//   V tile: chunk c of row r at c ^ v_swz(r)   (ds_read_b64_tr_b16 reads),
+// v_swz linear over GF(2) in the row's four bits, which flip chunk bits by
+// 2, 4, 11 and 1. With the decode swizzle above both reads were 2-way
+// conflicted at head_dim 128 (47% of the kernel's LDS cycles stalled).
+__device__ __forceinline__ int ext_k_swz(int row, int cpr) { return row & (cpr - 1); }
+__device__ __forceinline__ int ext_v_swz(int row, int cpr) {
+  const int s = ((row & 1) << 1) ^ ((row & 2) << 1) ^ (((row >> 2) & 1) * 11) ^ ((row >> 3) & 1);
+  return s & (cpr - 1);
 }
 
 template <int D, int W, int QL, int R>
@@ -1345,10 +1363,10 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
   int k_rd[NR], v_rd[NT];
   const int vrow = 4 * g4 + a4;
 #pragma unroll
-  for (int r = 0; r < NR; r++) k_rd[r] = m16 * RB + (((g4 + 4 * r) ^ tile_swz(m16, CPR)) << 4);
+  for (int r = 0; r < NR; r++) k_rd[r] = m16 * RB + (((g4 + 4 * r) ^ ext_k_swz(m16, CPR)) << 4);
 #pragma unroll
   for (int nn = 0; nn < NT; nn++)
-    v_rd[nn] = vrow * RB + (((2 * nn + (rq >> 1)) ^ tile_swz(vrow, CPR)) << 4) + 8 * (rq & 1);
+    v_rd[nn] = vrow * RB + (((2 * nn + (rq >> 1)) ^ ext_v_swz(vrow, CPR)) << 4) + 8 * (rq & 1);
 
   auto stage = [&](int s, int step) {
     issue(ring[(s + R - 1) % R], badr[(s + R - 1) % R], step + R - 1);
@@ -1365,7 +1383,7 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
         // would poison O); K rows there are masked in the scores instead.
         u32x4 val = ring[s][i];
         if (kv && (((badr[s] >> kb) & 1) || kPageSize * (step * KB + kb) + row >= ctx)) val = u32x4{0u, 0u, 0u, 0u};
-        *reinterpret_cast<u32x4 *>(tiles[s & 1][kb][kv] + row * RB + ((cc ^ tile_swz(row, CPR)) << 4)) = val;
+        *reinterpret_cast<u32x4 *>(tiles[s & 1][kb][kv] + row * RB + ((cc ^ (kv ? ext_v_swz(row, CPR) : ext_k_swz(row, CPR))) << 4)) = val;
       }
     }
     __syncthreads();
