@@ -232,6 +232,12 @@ MKV_API int mkv_decode_step(mkv_pool *pool, const mkv_decode_plan *plan, int32_t
  * reported, MKV_DEVERR_CTX). Any pool: bf16 pools with head_dim 64/128/256
  * and at most 16 query heads per KV head run MFMA query tiles; other pools
  * (f32, head_dim 32, larger groups) run one decode segment per query token.
+ * When the MFMA tiles would leave the device's resident workgroup slots
+ * empty (few short chunks over long contexts), each key range is split in up
+ * to 4 and the f32 partials are merged by a second launch; they use the
+ * pool-owned workspace shared with mkv_decode_attention (grown on demand:
+ * that call synchronises the stream once, and such calls on one pool must
+ * not run concurrently on different streams).
  * Flags: MKV_ATTN_ZERO_SINK.
  * Replaces the seq_q > 1 path of inference-model-qwen/src/model.rs:410-416
  * with its causal mask (model.rs:542-555), for the chunks scheduled by

@@ -1243,6 +1243,8 @@ struct ExtArgs {
   const int32_t *ctx;       // [B] tokens in the cache, the chunk included
   int32_t B, max_ctx;
   int32_t tiles, per_xcd;   // query tiles per sequence; logical workgroups per XCD
+  int32_t splits;           // key-range splits per (tile, KV head, sequence); > 1: f32 partials + merge
+  int32_t max_q;            // max_q_len: with splits, partial rows exist for B * max_q tokens
 };
 
 // Workgroups are dealt to the 8 XCDs round-robin by linear index. The
@@ -1250,14 +1252,18 @@ struct ExtArgs {
 // (L % 8) * per_xcd + L / 8, so each XCD receives a contiguous run of
 // logical indices: the query tiles of one (sequence, KV head) share that
 // XCD's L2 while they stream the same K/V. Logical index = tile + tiles *
-// (head + Hkv * sequence); false for the padding past the last one.
-__device__ __forceinline__ bool ext_tile(const ExtArgs &e, int Hkv, int &t, int &h, int &b) {
+// (head + Hkv * (sequence + B * split)); false for the padding past the last
+// one.
+__device__ __forceinline__ bool ext_tile(const ExtArgs &e, int Hkv, int &t, int &h, int &b, int &sp) {
   const int L = blockIdx.x;
   const int logical = (L & 7) * e.per_xcd + (L >> 3);
-  if (logical >= e.tiles * Hkv * e.B) return false;
-  t = logical % e.tiles;
-  h = (logical / e.tiles) % Hkv;
-  b = logical / (e.tiles * Hkv);
+  const int per_split = e.tiles * Hkv * e.B;
+  if (logical >= per_split * e.splits) return false;
+  const int r = logical % per_split;
+  sp = logical / per_split;
+  t = r % e.tiles;
+  h = (r / e.tiles) % Hkv;
+  b = r / (e.tiles * Hkv);
   return true;
 }
 
@@ -1277,12 +1283,15 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int m16 = lane & 15, g4 = lane >> 4, a4 = m16 >> 2, rq = m16 & 3;
-  int t, h, b;
-  if (!ext_tile(e, a.Hkv, t, h, b)) return;
+  int t, h, b, sp;
+  if (!ext_tile(e, a.Hkv, t, h, b, sp)) return;
   const int q0 = e.q_indptr[b], nq = e.q_indptr[b + 1] - q0;
   if (nq <= 0 || 16 * TP * t >= nq) return;
   const int ctx = e.ctx[b];
-  if (nq > ctx || ctx > e.max_ctx) {
+  // (With splits, a chunk longer than max_q_len or a q_indptr past
+  // num_seqs * max_q_len tokens would address partial rows past the workspace.)
+  if (nq > ctx || ctx > e.max_ctx ||
+      (e.splits > 1 && (nq > e.max_q || q0 < 0 || (int64_t)q0 + nq > (int64_t)e.B * e.max_q))) {
     if (threadIdx.x == 0 && t == 0) record_error(a.d_err, MKV_DEVERR_CTX);
     return;
   }
@@ -1303,7 +1312,11 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
   const int qhi_wg = min(ctx - nq + 16 * TP * (t + 1) - 1, ctx - 1);
   const int n = qhi_wg / kPageSize + 1;                  // blocks the workgroup streams: keys 0..qhi_wg
   const int nw = min(n, (qlo + 15) / kPageSize + 1);     // blocks this wave's sub-tile sees
-  const int nsteps = (n + KB - 1) / KB;                  // steps of KB blocks
+  // Steps of KB blocks; with splits, this workgroup takes its share of them
+  // (a short context can leave a split none: it stores an empty partial).
+  const int nsteps_all = (n + KB - 1) / KB;
+  const int sps = (nsteps_all + e.splits - 1) / e.splits;
+  const int st0 = min(sp * sps, nsteps_all), st1 = min(st0 + sps, nsteps_all);
   const bool computes = hw < a.G;
   const int hq = h * a.G + min(hw, a.G - 1);
   const int qp = qlo + m16;                   // this lane's query position (rows past nq: unused)
@@ -1436,7 +1449,9 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
       const float ms = mloc * a.sl2;
       const bool need = ms > st.m + kRescaleSlack;
       const float mn = need ? ms : st.m;
-      const float al = fast_exp2(st.m - mn);
+      // A column with nothing visible yet (possible in a later key range)
+      // keeps m = -inf, l = 0, O = 0: scale 0, not exp2(-inf - -inf) = NaN.
+      const float al = st.m == -INFINITY ? 0.0f : fast_exp2(st.m - mn);
       st.l *= al;
 #pragma unroll
       for (int nn = 0; nn < NT; nn++) st.O[nn] *= al;
@@ -1470,28 +1485,48 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
   };
 
 #pragma unroll
-  for (int s = 0; s < R - 1; s++) issue(ring[s], badr[s], s);
-  const int nfull = nsteps / R;
-  int k0 = 0;
+  for (int s = 0; s < R - 1; s++) issue(ring[s], badr[s], st0 + s);
+  const int nfull = (st1 - st0) / R;
+  int k0 = st0;
   for (int it = 0; it < nfull; it++, k0 += R) {
 #pragma unroll
     for (int s = 0; s < R; s++) stage(s, k0 + s);
   }
 #pragma unroll
   for (int s = 0; s < R - 1; s++)
-    if (k0 + s < nsteps) stage(s, k0 + s);
+    if (k0 + s < st1) stage(s, k0 + s);
 
   if (!computes) return;
   st.l += __shfl_xor(st.l, 16);
   st.l += __shfl_xor(st.l, 32);
   const int row = row0 + m16;
   if (row >= nq) return;
+  if (e.splits > 1) {  // f32 partial (m, l, O) of this key range, merged by merge_ext_kernel
+    const int64_t prow = ((int64_t)(q0 + row) * a.Hq + hq) * e.splits + sp;
+    float *wo = a.ws_o + prow * D + 4 * g4;
+#pragma unroll
+    for (int nn = 0; nn < NT; nn++) *reinterpret_cast<f32x4 *>(wo + 16 * nn) = st.O[nn];
+    if (g4 == 0) *reinterpret_cast<float2 *>(a.ws_ml + 2 * prow) = make_float2(st.m, st.l);
+    return;
+  }
   const float f = final_scale(st.m, st.l, a.zero_sink);
   uint16_t *op = reinterpret_cast<uint16_t *>(a.o) + ((int64_t)(q0 + row) * a.Hq + hq) * D + 4 * g4;
 #pragma unroll
   for (int nn = 0; nn < NT; nn++)
     *reinterpret_cast<uint2 *>(op + 16 * nn) = make_uint2(pack_bf16x2(st.O[nn][0] * f, st.O[nn][1] * f),
                                                           pack_bf16x2(st.O[nn][2] * f, st.O[nn][3] * f));
+}
+
+// Log-sum-exp merge of the extend kernel's key-range partials: one wave per
+// (query token, query head) row, partials row * splits + s.
+template <int D, bool BF16>
+__global__ void __launch_bounds__(256) merge_ext_kernel(KArgs a, ExtArgs e) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  const int64_t tokens = min((int64_t)e.q_indptr[e.B], (int64_t)e.B * e.max_q);
+  if (row >= tokens * a.Hq) return;
+  merge_rows<D, BF16>(a, lane, row * e.splits, 1, e.splits, row);
 }
 
 template <int D, bool BF16>
@@ -1779,6 +1814,19 @@ extern "C" int mkv_decode_plan_destroy(mkv_decode_plan *plan) {
 // (CUs x resident workgroups per CU for the instantiation the pool's
 // geometry selects), or 0 when that kernel does not apply. Pieces beyond it
 // run in a second round; fewer leave CUs idle. Queried once per pool.
+// Compute units of the pool's device, queried once (-1 when unknown).
+static int device_cus(Pool *p) {
+  if (p->cus == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, p->device) != hipSuccess) {
+      (void)hipGetLastError();
+      cus = 0;
+    }
+    p->cus = cus > 0 ? cus : -1;
+  }
+  return p->cus;
+}
+
 static int64_t coop_resident(Pool *p) {
   if (p->coop_slots >= 0) return p->coop_slots;
   const Geom &g = p->g;
@@ -2125,7 +2173,7 @@ extern "C" int mkv_extend_attention(mkv_pool *pool, int32_t layer, const void *d
     MKV_CHECK_LAUNCH("attn_ext_split_kernel");
     return MKV_OK;
   }
-  if (((int64_t)max_q_len + 15) / 16 * g.Hkv * num_seqs + 8 > INT32_MAX)
+  if (4 * (((int64_t)max_q_len + 15) / 16 * g.Hkv * num_seqs) + 8 > INT32_MAX)
     return set_error(MKV_ERR_INVALID_ARGUMENT, "grid too large");
   DeviceGuard guard(p->device);
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
@@ -2135,6 +2183,8 @@ extern "C" int mkv_extend_attention(mkv_pool *pool, int32_t layer, const void *d
   e.ctx = d_ctx_lens;
   e.B = num_seqs;
   e.max_ctx = max_ctx_len;
+  e.splits = 1;
+  e.max_q = max_q_len;
   // Waves per 16-position sub-tile: the next power of two >= G. Two
   // sub-tiles per workgroup share each K/V tile (K/V streamed once per 32
   // positions) where that stays within 16 waves and their register budget
@@ -2145,26 +2195,74 @@ extern "C" int mkv_extend_attention(mkv_pool *pool, int32_t layer, const void *d
   const int TP = (WG <= 8 && g.D <= 128 && max_q_len > 16) ? 2 : 1;
   const int W = WG * TP;
   const int64_t tiles = ((int64_t)max_q_len + 16 * TP - 1) / (16 * TP);
-  const int64_t total = tiles * g.Hkv * num_seqs;  // linear index -> (tile, KV head, sequence), grouped by XCD
+  const int64_t per_split = tiles * g.Hkv * num_seqs;  // (tile, KV head, sequence) workgroups
+  const void *fn = nullptr;
+#define MKV_EXT_FN(DD, TT)                                                                                  \
+  do {                                                                                                      \
+    switch (W / TT) {                                                                                       \
+      case 1: fn = reinterpret_cast<const void *>(&attn_extend_kernel<DD, 1 * TT, kExtKB, kExtR, TT>); break; \
+      case 2: fn = reinterpret_cast<const void *>(&attn_extend_kernel<DD, 2 * TT, kExtKB, kExtR, TT>); break; \
+      case 4: fn = reinterpret_cast<const void *>(&attn_extend_kernel<DD, 4 * TT, kExtKB, kExtR, TT>); break; \
+      case 8: fn = reinterpret_cast<const void *>(&attn_extend_kernel<DD, 8 * TT, kExtKB, kExtR, TT>); break; \
+      default: fn = reinterpret_cast<const void *>(&attn_extend_kernel<DD, 16, kExtKB, kExtR, 1>); break;     \
+    }                                                                                                       \
+  } while (0)
+  switch (g.D) {
+    case 64: if (TP == 2) MKV_EXT_FN(64, 2); else MKV_EXT_FN(64, 1); break;
+    case 128: if (TP == 2) MKV_EXT_FN(128, 2); else MKV_EXT_FN(128, 1); break;
+    default: MKV_EXT_FN(256, 1); break;
+  }
+#undef MKV_EXT_FN
+  // When the launch leaves resident workgroup slots empty (short chunks over
+  // long contexts: one workgroup per (sequence, KV head) streams a whole
+  // context), each key range splits in up to 4, at least 8 steps apiece;
+  // the f32 partials go to the pool-owned workspace and a second launch
+  // merges them. Slots = resident workgroups per CU of this instantiation
+  // (occupancy query, once per pool) x CUs.
+  int &per_cu = p->ext_per_cu[g.D == 64 ? 0 : g.D == 128 ? 1 : 2][W == 1 ? 0 : W == 2 ? 1 : W == 4 ? 2 : W == 8 ? 3 : 4][TP - 1];
+  if (per_cu == 0) {
+    int n_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n_cu, fn, 64 * W, 0) != hipSuccess) {
+      (void)hipGetLastError();  // leave no sticky error: no splitting
+      n_cu = 0;
+    }
+    per_cu = n_cu > 0 ? n_cu : -1;
+  }
+  const int cus = device_cus(p);
+  const int64_t slots = per_cu > 0 && cus > 0 ? (int64_t)per_cu * cus : 0;
+  const int64_t steps_max = ((int64_t)(max_ctx_len + kPageSize - 1) / kPageSize + kExtKB - 1) / kExtKB;
+  if (per_split < slots)
+    e.splits = (int32_t)std::min<int64_t>({4, (slots + per_split - 1) / per_split, std::max<int64_t>(1, steps_max / 8)});
+  const int64_t rows = (int64_t)num_seqs * max_q_len * g.Hq;  // bounds the (token, query head) rows
+  if (e.splits > 1) {
+    const uint64_t ml_bytes = ((uint64_t)rows * e.splits * 8 + 255) / 256 * 256;
+    const uint64_t need = ml_bytes + (uint64_t)rows * e.splits * g.D * 4;
+    if (p->ws_bytes < need) {
+      MKV_CHECK_HIP(hipStreamSynchronize(hs));  // earlier launches may read the old buffer
+      if (p->ws) MKV_CHECK_HIP(hipFree(p->ws));
+      p->ws = nullptr;
+      p->ws_bytes = 0;
+      MKV_CHECK_HIP(hipMalloc(&p->ws, need));
+      p->ws_bytes = need;
+    }
+    a.ws_ml = reinterpret_cast<float *>(p->ws);
+    a.ws_o = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(p->ws) + ml_bytes);
+  }
+  const int64_t total = per_split * e.splits;  // linear index -> (tile, KV head, sequence, split), grouped by XCD
   e.tiles = (int32_t)tiles;
   e.per_xcd = (int32_t)((total + 7) / 8);
   const dim3 grid((unsigned)(8 * (int64_t)e.per_xcd)), block(64 * W);
-#define MKV_EXT(DD, TT)                                                                                 \
-  do {                                                                                                  \
-    switch (W / TT) {                                                                                   \
-      case 1: hipLaunchKernelGGL((attn_extend_kernel<DD, 1 * TT, kExtKB, kExtR, TT>), grid, block, 0, hs, a, e); break; \
-      case 2: hipLaunchKernelGGL((attn_extend_kernel<DD, 2 * TT, kExtKB, kExtR, TT>), grid, block, 0, hs, a, e); break; \
-      case 4: hipLaunchKernelGGL((attn_extend_kernel<DD, 4 * TT, kExtKB, kExtR, TT>), grid, block, 0, hs, a, e); break; \
-      case 8: hipLaunchKernelGGL((attn_extend_kernel<DD, 8 * TT, kExtKB, kExtR, TT>), grid, block, 0, hs, a, e); break; \
-      default: hipLaunchKernelGGL((attn_extend_kernel<DD, 16, kExtKB, kExtR, 1>), grid, block, 0, hs, a, e); break;   \
-    }                                                                                                   \
-  } while (0)
-  switch (g.D) {
-    case 64: if (TP == 2) MKV_EXT(64, 2); else MKV_EXT(64, 1); break;
-    case 128: if (TP == 2) MKV_EXT(128, 2); else MKV_EXT(128, 1); break;
-    default: MKV_EXT(256, 1); break;
-  }
-#undef MKV_EXT
+  void *args[] = {&a, &e};
+  MKV_CHECK_HIP(hipLaunchKernel(fn, grid, block, args, 0, hs));
   MKV_CHECK_LAUNCH("attn_extend_kernel");
+  if (e.splits > 1) {
+    const dim3 mgrid((unsigned)((rows + 3) / 4));
+    switch (g.D) {
+      case 64: hipLaunchKernelGGL((merge_ext_kernel<64, true>), mgrid, dim3(256), 0, hs, a, e); break;
+      case 128: hipLaunchKernelGGL((merge_ext_kernel<128, true>), mgrid, dim3(256), 0, hs, a, e); break;
+      default: hipLaunchKernelGGL((merge_ext_kernel<256, true>), mgrid, dim3(256), 0, hs, a, e); break;
+    }
+    MKV_CHECK_LAUNCH("merge_ext_kernel");
+  }
   return MKV_OK;
 }

@@ -35,6 +35,8 @@ struct Pool {
   void *ws = nullptr;        // pool-owned attention workspace
   uint64_t ws_bytes = 0;
   int64_t coop_slots = -1;   // resident workgroups of the decode kernel (-1: not yet queried)
+  int cus = 0;               // compute units of the device (0: not yet queried)
+  int ext_per_cu[3][5][2] = {};  // resident extend workgroups per CU by (head_dim, waves, sub-tiles); 0: not yet queried
 };
 
 // Thread-local last-error message and status helpers.

@@ -136,6 +136,32 @@ def test_extend_errors_are_reported():
             pool.extend_attention(0, q, _i32([0, 2]), _i32([0, 1]), _i32([0]), _i32([2]), 2, 2)
 
 
+def test_extend_split_key_ranges_with_empty_splits():
+    """Few sequences over long contexts split each key range (f32 partials,
+    then a merge); short contexts in the same launch leave some splits with
+    no blocks, which must merge as empty partials."""
+    got, ref, dec, q_indptr = _case("qwen7b", [3000, 1, 17, 6000, 40], [16, 1, 3, 12, 40], 98)
+    assert_attention_close(got, ref, "bf16")
+    assert_attention_close(dec, ref[q_indptr[1:] - 1], "bf16")
+
+
+def test_extend_split_rejects_chunk_past_max_q_len():
+    """With split key ranges a chunk longer than max_q_len is reported
+    (its partial rows would lie past the workspace), not written."""
+    Hq, Hkv, D = SHAPES["qwen7b"]
+    rng = wl.SplitMix64(99)
+    batch = wl.decode_batch_from_contexts([2000 - 1], rng, extra_blocks=2)
+    desc = PoolDesc(1, Hkv, Hq, D, batch.num_blocks, "bf16")
+    with DeviceKvPool(desc) as pool:
+        pool.write(normal(99, desc.shape, "bf16"))
+        q = to_device(normal(100, (20, Hq, D), "bf16"))
+        pool.extend_attention(0, q, _i32([0, 20]), _i32(batch.block_indptr), _i32(batch.block_ids),
+                              _i32(batch.ctx_lens), 16, 2000)
+        with pytest.raises(DeviceIndexError) as ei:
+            pool.check()
+        assert ei.value.bits & dp.DEVERR_CTX
+
+
 @pytest.mark.parametrize("name", list(SEGMENT_SHAPES))
 def test_extend_segment_path_matches_oracle(name):
     """f32 pools, head_dim 32 and groups above 16 run one decode segment per
