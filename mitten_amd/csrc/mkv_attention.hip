@@ -1251,9 +1251,11 @@ struct ExtArgs {
 // launch has 8 * per_xcd workgroups; workgroup L becomes logical index
 // (L % 8) * per_xcd + L / 8, so each XCD receives a contiguous run of
 // logical indices: the query tiles of one (sequence, KV head) share that
-// XCD's L2 while they stream the same K/V. Logical index = tile + tiles *
-// (head + Hkv * (sequence + B * split)); false for the padding past the last
-// one.
+// XCD's L2 while they stream the same K/V. Logical index = (tiles - 1 -
+// tile) + tiles * (head + Hkv * (sequence + B * split)); false for the
+// padding past the last one. The last tile of a chunk attends the most keys,
+// so a sequence's tiles start longest first (causal 2k-token prompts: 518 ->
+// 487 us), leaving the short ones for the tail.
 __device__ __forceinline__ bool ext_tile(const ExtArgs &e, int Hkv, int &t, int &h, int &b, int &sp) {
   const int L = blockIdx.x;
   const int logical = (L & 7) * e.per_xcd + (L >> 3);
@@ -1261,7 +1263,7 @@ __device__ __forceinline__ bool ext_tile(const ExtArgs &e, int Hkv, int &t, int 
   if (logical >= per_split * e.splits) return false;
   const int r = logical % per_split;
   sp = logical / per_split;
-  t = r % e.tiles;
+  t = e.tiles - 1 - r % e.tiles;
   h = (r / e.tiles) % Hkv;
   b = r / (e.tiles * Hkv);
   return true;
