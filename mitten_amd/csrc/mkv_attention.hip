@@ -391,45 +391,78 @@ __device__ __forceinline__ void valu_segment(const KArgs &a, const Seg &sg, int 
   }
   const int64_t head_off = (int64_t)sg.h * D * ES + ld * 16;
   const int t_begin = sg.j0 * kPageSize, t_end = min(sg.ctx, sg.j1 * kPageSize);
-  const int n_iter = (t_end - t_begin + TPI - 1) / TPI;
-  for (int it = 0; it < n_iter; it++) {
-    const int t = t_begin + it * TPI + lt;
-    bool valid = t < t_end;
-    float kf[VEC], vf[VEC];
+  // Tokens go in batches of BT = TPI * U (U loads of K and of V per lane),
+  // a batch inside one block: its block id is wave-uniform and comes by a
+  // scalar load. The next batch's loads are issued before this batch is
+  // used, so a block costs about one memory round trip instead of a block-id
+  // load and a K/V load per TPI tokens.
+  constexpr int U = (kPageSize / TPI) < 1 ? 1 : (kPageSize / TPI) > 4 ? 4 : kPageSize / TPI;
+  constexpr int BT = TPI * U;
+  static_assert(kPageSize % BT == 0, "a batch lies inside one block");
+  typedef const __attribute__((address_space(4))) int32_t const_i32;
+  const const_i32 *tab = (const const_i32 *)sg.table;
+  const int nbat = t_end > t_begin ? (t_end - t_begin + BT - 1) / BT : 0;
+  u32x4 kr[2][U], vr[2][U];
+  bool okr[2];
+  auto fetch = [&](u32x4 (&kd)[U], u32x4 (&vd)[U], bool &okb, int bi) {
+    const int tb = t_begin + min(bi, nbat - 1) * BT;  // batches past the end re-read the last one
+    const int32_t blk = tab[tb / kPageSize];           // uniform: a scalar load
+    okb = blk >= 0 && blk < a.nblocks;
+    const int64_t boff = (int64_t)(okb ? blk : 0) * a.block_bytes + head_off;
 #pragma unroll
-    for (int e = 0; e < VEC; e++) kf[e] = vf[e] = 0.0f;
-    if (valid) {
-      if (sg.nk && t == sg.ctx - 1) {
-        load_chunk<BF16, VEC>(sg.nk + ld * 16, kf);
-        load_chunk<BF16, VEC>(sg.nv + ld * 16, vf);
+    for (int u = 0; u < U; u++) {
+      const int t = tb + u * TPI + lt;
+      const bool fresh = sg.nk && t == sg.ctx - 1;  // the step's new row, read from its input
+      const int64_t off = boff + (int64_t)(t % kPageSize) * a.row_bytes;
+      kd[u] = *reinterpret_cast<const u32x4 *>(fresh ? sg.nk + ld * 16 : a.k_plane + off);
+      vd[u] = *reinterpret_cast<const u32x4 *>(fresh ? sg.nv + ld * 16 : a.v_plane + off);
+    }
+  };
+  auto consume = [&](const u32x4 (&kd)[U], const u32x4 (&vd)[U], bool okb, int bi) {
+    if (!okb && lane == 0) record_error(a.d_err, MKV_DEVERR_BLOCK);
+    const int tb = t_begin + bi * BT;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int t = tb + u * TPI + lt;
+      const bool valid = okb && t < t_end;
+      float kf[VEC], vf[VEC];
+      if constexpr (BF16) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          kf[2 * e] = bf16_lo(kd[u][e]), kf[2 * e + 1] = bf16_hi(kd[u][e]);
+          vf[2 * e] = bf16_lo(vd[u][e]), vf[2 * e + 1] = bf16_hi(vd[u][e]);
+        }
       } else {
-        const int32_t blk = sg.table[t / kPageSize];
-        if (blk < 0 || blk >= a.nblocks) {
-          record_error(a.d_err, MKV_DEVERR_BLOCK);
-          valid = false;
-        } else {
-          const int64_t off = (int64_t)blk * a.block_bytes + (t % kPageSize) * a.row_bytes + head_off;
-          load_chunk<BF16, VEC>(a.k_plane + off, kf);
-          load_chunk<BF16, VEC>(a.v_plane + off, vf);
+#pragma unroll
+        for (int e = 0; e < 4; e++) kf[e] = __uint_as_float(kd[u][e]), vf[e] = __uint_as_float(vd[u][e]);
+      }
+#pragma unroll
+      for (int g = 0; g < QC; g++) {
+        if (g >= nq) break;
+        float s = 0.0f;
+#pragma unroll
+        for (int e = 0; e < VEC; e++) s = fmaf(qv[g][e], kf[e], s);
+        s = row_sum<LPT>(s);  // DPP steps within the token's lanes (no LDS round trips)
+        if (valid) {
+          const float mn = fmaxf(st.m[g], s);
+          const float al = fast_exp2(st.m[g] - mn);
+          const float p = fast_exp2(s - mn);
+          st.l[g] = st.l[g] * al + p;
+#pragma unroll
+          for (int e = 0; e < VEC; e++) st.acc[g][e] = fmaf(p, vf[e], st.acc[g][e] * al);
+          st.m[g] = mn;
         }
       }
     }
-#pragma unroll
-    for (int g = 0; g < QC; g++) {
-      if (g >= nq) break;
-      float s = 0.0f;
-#pragma unroll
-      for (int e = 0; e < VEC; e++) s = fmaf(qv[g][e], kf[e], s);
-#pragma unroll
-      for (int o = LPT / 2; o >= 1; o >>= 1) s += __shfl_xor(s, o);
-      if (valid) {
-        const float mn = fmaxf(st.m[g], s);
-        const float al = fast_exp2(st.m[g] - mn);
-        const float p = fast_exp2(s - mn);
-        st.l[g] = st.l[g] * al + p;
-#pragma unroll
-        for (int e = 0; e < VEC; e++) st.acc[g][e] = fmaf(p, vf[e], st.acc[g][e] * al);
-        st.m[g] = mn;
+  };
+  if (nbat > 0) {
+    fetch(kr[0], vr[0], okr[0], 0);
+    for (int bi = 0; bi < nbat; bi += 2) {
+      fetch(kr[1], vr[1], okr[1], bi + 1);
+      consume(kr[0], vr[0], okr[0], bi);
+      if (bi + 1 < nbat) {
+        fetch(kr[0], vr[0], okr[0], bi + 2);
+        consume(kr[1], vr[1], okr[1], bi + 1);
       }
     }
   }

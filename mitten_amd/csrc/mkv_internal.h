@@ -81,6 +81,26 @@ __device__ __forceinline__ void record_error(uint32_t *d_err, uint32_t bit) {
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+// DPP lane move within 16-lane rows (CTRL a dpp_ctrl code; all lanes active).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the LPR lanes of each row group (LPR = 4, 8, ..., 64 consecutive
+// lanes); every lane of the group gets the same bits (each step adds two
+// values that are equal up to the order of a commutative addition).
+template <int LPR>
+__device__ __forceinline__ float row_sum(float v) {
+  v += dpp_f<0xb1>(v);                             // quad_perm [1,0,3,2]: lane ^ 1
+  if constexpr (LPR >= 4) v += dpp_f<0x4e>(v);     // quad_perm [2,3,0,1]: lane ^ 2
+  if constexpr (LPR >= 8) v += dpp_f<0x141>(v);    // row_half_mirror: the other quad
+  if constexpr (LPR >= 16) v += dpp_f<0x140>(v);   // row_mirror: the other half-row
+  if constexpr (LPR >= 32) v += __shfl_xor(v, 16);
+  if constexpr (LPR >= 64) v += __shfl_xor(v, 32);
+  return v;
+}
+
 // f32 -> bf16 bits, round to nearest even (NaN kept NaN).
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   uint32_t u = __float_as_uint(f);

@@ -76,11 +76,6 @@ __device__ __forceinline__ void store_row_part(uint8_t *p, int i0, const float (
 // Sum over the 64 lanes of a wave, the same value in every lane: DPP steps
 // inside each 16-lane row (pairs, quads, half-rows, rows), then the four row
 // sums read out and added as ((r0 + r1) + (r2 + r3)).
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
-}
-
 __device__ __forceinline__ float wave_sum(float v) {
   v += dpp_f<0xb1>(v);   // quad_perm [1,0,3,2]
   v += dpp_f<0x4e>(v);   // quad_perm [2,3,0,1]
@@ -220,20 +215,6 @@ __global__ void __launch_bounds__(256) qk_norm_rope_append_kernel(PrepArgs a) {
   }
 }
 
-
-// Sum over the LPR lanes of each row group (LPR = 4, 8, ..., 64 consecutive
-// lanes); every lane of the group gets the same bits (each step adds two
-// values that are equal up to the order of a commutative addition).
-template <int LPR>
-__device__ __forceinline__ float row_sum(float v) {
-  v += dpp_f<0xb1>(v);                             // quad_perm [1,0,3,2]: lane ^ 1
-  if constexpr (LPR >= 4) v += dpp_f<0x4e>(v);     // quad_perm [2,3,0,1]: lane ^ 2
-  if constexpr (LPR >= 8) v += dpp_f<0x141>(v);    // row_half_mirror: the other quad
-  if constexpr (LPR >= 16) v += dpp_f<0x140>(v);   // row_mirror: the other half-row
-  if constexpr (LPR >= 32) v += __shfl_xor(v, 16);
-  if constexpr (LPR >= 64) v += __shfl_xor(v, 32);
-  return v;
-}
 
 // Vector form, one wave per token: lane holds VEC = 16 / ES contiguous
 // elements of a head row (one 16-byte load), a row spans LPR = D / VEC lanes
