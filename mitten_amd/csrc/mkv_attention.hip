@@ -564,16 +564,14 @@ __device__ __forceinline__ void merge_rows(const KArgs &a, int lane, int64_t bas
       if (i < cnt && has)
         ov[i] = *reinterpret_cast<const fvec *>(a.ws_o + (base + (int64_t)(s0 + i) * stride) * D + d0);
     }
-    float mb = ml.x;
-#pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) mb = fmaxf(mb, __shfl_xor(mb, o));
+    // Max and weighted sum over lanes 0..15 (the partials) by DPP row steps,
+    // read from lane 0 (no LDS round trips).
+    float mb = row16_max(ml.x);
     mb = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, mb)));
     const float Mn = fmaxf(M, mb);
     const float carry = M == -INFINITY ? 0.0f : fast_exp2(M - Mn);
     const float w = (lane < cnt && ml.x != -INFINITY) ? fast_exp2(ml.x - Mn) : 0.0f;
-    float lw = ml.y * w;
-#pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) lw += __shfl_xor(lw, o);
+    const float lw = row_sum<16>(ml.y * w);
     L = L * carry + __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, lw)));
     acc *= carry;
 #pragma unroll

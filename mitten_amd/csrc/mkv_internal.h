@@ -101,6 +101,15 @@ __device__ __forceinline__ float row_sum(float v) {
   return v;
 }
 
+// Maximum over the 16 lanes of each DPP row, in every lane of the row.
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f<0xb1>(v));   // lane ^ 1
+  v = fmaxf(v, dpp_f<0x4e>(v));   // lane ^ 2
+  v = fmaxf(v, dpp_f<0x141>(v));  // the other quad of the half-row
+  v = fmaxf(v, dpp_f<0x140>(v));  // the other half-row
+  return v;
+}
+
 // f32 -> bf16 bits, round to nearest even (NaN kept NaN).
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   uint32_t u = __float_as_uint(f);
