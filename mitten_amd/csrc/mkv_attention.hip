@@ -19,7 +19,8 @@
 //   flight while one is computed; the running max moves only when it grows
 //   by more than 2^8, so O is rarely rescaled.
 // Other dtypes/shapes use a VALU loop: lanes split a token row into 16-byte
-// chunks and reduce scores across the row's lanes with shuffles.
+// chunks and reduce scores across the row's lanes with DPP steps; a batch of
+// tokens inside one block is loaded while the previous batch is used.
 //
 // Two work decompositions:
 //   split grid (mkv_decode_attention): units (sequence, split, KV head, query
@@ -1252,14 +1253,16 @@ attn_coop_kernel(KArgs a, PlanDev pd) {
 // with the causal mask of model.rs:542-555 (a key at position j is visible to
 // the query at position p iff j <= p).
 //
-// One workgroup per (16-token query tile, KV head, sequence); W >= G waves,
-// wave g computing query head h*G + g for the tile's 16 positions (the MFMA
-// column dimension). The workgroup streams the head's K/V blocks 0..(last
-// tile position)/16 through the same double-buffered, swizzled LDS tile as
-// the decode kernel (rows of one head: D*2 bytes), loaded cooperatively
-// three blocks deep; scores, online softmax and the V^T transpose reads are
-// those of the decode kernel, with the causal mask applied on blocks that
-// reach past the tile's first position.
+// One workgroup per (query tile of 16 or 32 positions, KV head, sequence,
+// key-range split); per 16-position sub-tile, W/TP >= G waves, wave g
+// computing query head h*G + g for the sub-tile's positions (the MFMA column
+// dimension). The workgroup streams the head's K/V blocks 0..(last tile
+// position)/16 (its split's share of them) through a double-buffered LDS
+// tile (rows of one head: D*2 bytes; K and V tiles each with their own
+// bank-conflict-free swizzle), loaded cooperatively one step of two blocks
+// ahead; scores, online softmax and the V^T transpose reads follow the
+// decode kernel, with the causal mask applied on blocks that reach past a
+// sub-tile's first position.
 // ===========================================================================
 
 // Extend kernel: two blocks (32 keys) per softmax step, steps loaded one
