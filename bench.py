@@ -24,7 +24,10 @@ blocks (all layers) to a payload and its import into other blocks.
 (one layer per launch); `--op copy` measures copy_blocks (COW copies and
 compaction moves) of `--copy-pairs` block pairs over all layers; `--op
 extend` measures chunked-prefill attention (TFLOP/s against the bf16 MFMA
-peak).
+peak). `--op shared` measures the decode step of 256 sequences over one
+radix-shared 4,100-token prefix (GB/s on unique and on logical bytes) and
+its copy-on-write copies and compaction moves; `--op pressure` measures a
+step of 8 chunk appends and 504 decodes over a 217,982-block (200 GB) pool.
 """
 from __future__ import annotations
 
@@ -62,13 +65,16 @@ def parse():
                     help="time the steps without per-launch HIP events (roofline fields null)")
     ap.add_argument("--cpu-layers", type=int, default=5,
                     help="layers of the batch in the CPU baseline sample")
-    ap.add_argument("--op", choices=["decode", "prep", "wire", "gather", "copy", "extend"], default="decode",
+    ap.add_argument("--op", choices=["decode", "prep", "wire", "gather", "copy", "extend", "shared", "pressure"],
+                    default="decode",
                     help="decode: the decode step (headline); prep: the fused q/k-norm + RoPE + "
                          "append kernel on a prefill chunk; wire: KV block export + import of a "
                          "handoff; gather: block-table gather of the decode batch, one layer; "
                          "copy: copy_blocks of --copy-pairs block pairs, all layers; extend: chunked-"
                          "prefill attention of --extend-seqs chunks of --tokens-per-chunk after "
-                         "--prefix tokens")
+                         "--prefix tokens; shared: decode step of 256 sequences over a radix-shared "
+                         "prefix, with its copy-on-write copies and compaction moves; pressure: "
+                         "chunk appends + decode step over a 200 GB pool")
     ap.add_argument("--extend-seqs", type=int, default=8, help="--op extend: sequences")
     ap.add_argument("--tokens-per-chunk", type=int, default=512, help="--op extend: chunk length")
     ap.add_argument("--prefix", type=int, default=4096, help="--op extend: cached tokens before the chunk")
@@ -125,7 +131,7 @@ def cpu_info():
     return model
 
 
-def cpu_baseline(cfg, batch, step_bytes, layers):
+def cpu_baseline(cfg, batch, step_bytes, layers, paged=True):
     """Reference-faithful CPU decode (contiguous f32 cache grown by a copy per
     token, repeat_kv materialised, mask, softmax, matmuls) for `layers` layers
     of every sequence of the batch, scaled to a full step. The primary figure
@@ -143,6 +149,23 @@ def cpu_baseline(cfg, batch, step_bytes, layers):
     orc.set_num_threads(threads)
     tn = orc.ref_faithful_batch(ctx, cfg["num_kv_heads"], cfg["num_q_heads"], cfg["head_dim"], seed=100)
     step_1t, step_nt = t1 / layers * cfg["num_layers"], tn * cfg["num_layers"]
+    out = {
+        "value": round(step_bytes / step_1t / 1e9, 3),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"{layers} of {cfg['num_layers']} layers x all {batch.num_seqs} sequences, 1 thread, "
+                   f"{t1:.1f} s; scaled to a full step"),
+        "tokens_per_s": round(batch.num_seqs / step_1t, 2),
+        "ms_per_step": round(step_1t * 1e3, 1),
+        "threaded": {"value": round(step_bytes / step_nt / 1e9, 3), "unit": "GB/s", "cores": threads,
+                     "tokens_per_s": round(batch.num_seqs / step_nt, 2),
+                     "sample": f"1 layer of the sample, {threads} threads over sequences, {tn:.1f} s"},
+        "cpu_model": cpu_info(),
+        "host_cpus": os.cpu_count(),
+    }
+    if not paged:
+        return out
     # Second line: the efficient paged oracle (f32 accumulation over a bf16 /
     # f32 pool, threaded over sequences and heads) on one layer of the same
     # batch, K/V from a seeded host pool of the same blocks; scaled to a step.
@@ -158,25 +181,11 @@ def cpu_baseline(cfg, batch, step_bytes, layers):
     tp = time.perf_counter() - c0
     del host
     step_p = tp * cfg["num_layers"]
-    return {
-        "value": round(step_bytes / step_1t / 1e9, 3),
-        "unit": "GB/s",
-        "cores": 1,
-        "kind": "port",
-        "sample": (f"{layers} of {cfg['num_layers']} layers x all {batch.num_seqs} sequences, 1 thread, "
-                   f"{t1:.1f} s; scaled to a full step"),
-        "tokens_per_s": round(batch.num_seqs / step_1t, 2),
-        "ms_per_step": round(step_1t * 1e3, 1),
-        "threaded": {"value": round(step_bytes / step_nt / 1e9, 3), "unit": "GB/s", "cores": threads,
-                     "tokens_per_s": round(batch.num_seqs / step_nt, 2),
-                     "sample": f"1 layer of the sample, {threads} threads over sequences, {tn:.1f} s"},
-        "paged_oracle": {"value": round(step_bytes / step_p / 1e9, 3), "unit": "GB/s", "cores": threads,
-                         "tokens_per_s": round(batch.num_seqs / step_p, 2),
-                         "sample": f"oracle paged decode attention, 1 layer of all {batch.num_seqs} sequences, "
-                                   f"{threads} threads, {tp:.2f} s; scaled to a full step"},
-        "cpu_model": cpu_info(),
-        "host_cpus": os.cpu_count(),
-    }
+    out["paged_oracle"] = {"value": round(step_bytes / step_p / 1e9, 3), "unit": "GB/s", "cores": threads,
+                           "tokens_per_s": round(batch.num_seqs / step_p, 2),
+                           "sample": f"oracle paged decode attention, 1 layer of all {batch.num_seqs} sequences, "
+                                     f"{threads} threads, {tp:.2f} s; scaled to a full step"}
+    return out
 
 
 def bench_prep(args):
@@ -566,6 +575,237 @@ def bench_extend(args):
     }), flush=True)
 
 
+def _decode_step_run(pool, plan, batch, L, Hq, Hkv, D, seed, dev, stream, pre_layer=None, cached_loads=False):
+    """Q and new K/V rows of every layer, and a step function: the host plan
+    of the step, then per layer `pre_layer(layer)` (if given) and the fused
+    append + attention."""
+    import torch
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    B = batch.num_seqs
+    q = torch.randn((L, B, Hq, D), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    kn = torch.randn((L, B, Hkv, D), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    vn = torch.randn((L, B, Hkv, D), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(dev)
+    indptr, ids = i32(batch.block_indptr), i32(batch.block_ids)
+    run_layer = pool.bind_decode_step(plan, kn, vn, q, indptr, ids, out, stream=stream, cached_loads=cached_loads)
+    ctx_host = batch.ctx_lens.copy()
+
+    def step():
+        plan.build(ctx_host, 0, stream=stream)
+        for layer in range(L):
+            if pre_layer is not None:
+                pre_layer(layer)
+            run_layer(layer)
+
+    return step
+
+
+def _time_steps(step, steps, warmup, stream):
+    """Wall-clock seconds per step over `steps` steps after `warmup`, and the
+    HIP-event average of one step on `stream`."""
+    import torch
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for a_, b_ in evs:
+        a_.record(stream)
+        step()
+        b_.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    ev = float(np.mean([a_.elapsed_time(b_) for a_, b_ in evs])) / 1e3
+    return wall, ev
+
+
+def _time_copies(pool, src, dst, reps, stream):
+    """HIP-event average seconds of one copy_blocks launch of the pairs."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    s_, d_ = (torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(dev) for a in (src, dst))
+    pool.copy_blocks(s_, d_, stream=stream)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for a_, b_ in evs:
+        a_.record(stream)
+        pool.copy_blocks(s_, d_, stream=stream)
+        b_.record(stream)
+    torch.cuda.synchronize()
+    pool.check()
+    return float(np.mean([a_.elapsed_time(b_) for a_, b_ in evs])) / 1e3
+
+
+def bench_shared(args):
+    """Decode step over a radix-shared prefix (the prefix-sharing
+    configuration): 256 sequences share a 4,100-token prefix after
+    copy-on-write, so the prefix's 256 full blocks are the same ids in every
+    table and each sequence owns its copy of the partial block and a suffix
+    of ~U{64..1024} tokens. One step = the host plan, then fused append +
+    attention for all 28 layers, as in the headline. GB/s is reported on
+    unique bytes (every shared block counted once: the HBM figure) and on
+    logical bytes (each sequence's whole context, what per-sequence caches
+    would read). The copy-on-write copies (255 partial blocks) and a
+    compaction's batched moves (a fifth of the blocks) are timed as
+    copy_blocks launches over all layers, in GB/s of the moved bytes."""
+    import torch
+
+    from mitten_amd import DeviceKvPool, PoolDesc
+    from mitten_amd import workloads as wl
+
+    cfg = wl.CONFIGS["qwen2.5-7b"]
+    L, Hq, Hkv, D = cfg["num_layers"], cfg["num_q_heads"], cfg["num_kv_heads"], cfg["head_dim"]
+    seqs, prefix = 256, 4100
+    batch = wl.shared_prefix_batch(seqs, prefix, 64, 1024, wl.SplitMix64(wl.BASE_SEED + 3))
+    desc = PoolDesc(L, Hkv, Hq, D, batch.num_blocks, "bf16")
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    row = 2 * Hkv * D * 2  # K and V bytes of one token in one layer
+    qo_meta = wl.algorithmic_bytes_attention(batch, Hq, Hkv, D, 2) - batch.total_tokens * row
+    app = wl.algorithmic_bytes_append(seqs, Hkv, D, 2)
+    logical = L * (batch.total_tokens * row + qo_meta + app)
+    unique = L * (batch.meta["unique_tokens"] * row + qo_meta + app)
+    with DeviceKvPool(desc) as pool:
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(wl.BASE_SEED + 3)
+        view = pool.tensor()
+        for layer in range(L):
+            view[layer].normal_(generator=gen)
+        del view
+        plan = pool.plan(batch.ctx_lens, stream=stream)
+        # The tables share the prefix's blocks, so the loads go through the
+        # caches (MKV_ATTN_CACHED_LOADS), as an engine would ask when its
+        # radix cache hands out shared blocks; the non-temporal default is
+        # timed beside it.
+        step = _decode_step_run(pool, plan, batch, L, Hq, Hkv, D, wl.BASE_SEED + 33, dev, stream,
+                                cached_loads=True)
+        wall, ev = _time_steps(step, args.steps, args.warmup, stream)
+        step_nt = _decode_step_run(pool, plan, batch, L, Hq, Hkv, D, wl.BASE_SEED + 33, dev, stream)
+        wall_nt, _ = _time_steps(step_nt, args.steps, args.warmup, stream)
+        pool.check()
+        info = plan.info()
+        plan.close()
+        # Copy-on-write: the last holder keeps the prefix's partial block, the
+        # other 255 sequences get copies. Compaction: a fifth of the blocks
+        # move from the top of the id space into holes below it.
+        own = batch.meta["own_first"]
+        cow_src, cow_dst = np.full(seqs - 1, own[0], np.int32), own[1:].astype(np.int32)
+        n_mv = batch.num_blocks // 5
+        mv_src = np.arange(batch.num_blocks - n_mv, batch.num_blocks, dtype=np.int32)
+        mv_dst = wl.permutation(batch.num_blocks - n_mv, wl.SplitMix64(wl.BASE_SEED + 35))[:n_mv].astype(np.int32)
+        per_pair = L * 2 * 16 * Hkv * D * 2 * 2 + 8
+        cow_s = _time_copies(pool, cow_src, cow_dst, args.steps, stream)
+        mv_s = _time_copies(pool, mv_src, mv_dst, args.steps, stream)
+    result = {
+        "metric": "shared-prefix decode step: HBM GB/s on unique bytes (% peak); effective GB/s on logical bytes",
+        "value": round(unique / wall / 1e9, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(wall * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: N(0,1) K/V/Q from a seed; shared prefix ids and own blocks from a seeded permutation",
+        "config": {"workload": f"radix-shared decode step: {seqs} sequences over one {prefix}-token prefix "
+                               f"(suffixes U[64, 1024]), Qwen2.5-7B heads, {L} layers",
+                   "layers": L, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "block_size": 16,
+                   "sequences": seqs, "prefix_tokens": prefix, "shared_blocks": int(batch.meta["shared_blocks"].size),
+                   "tokens_attended": batch.total_tokens, "unique_tokens": batch.meta["unique_tokens"],
+                   "pool_blocks": batch.num_blocks, "plan": info},
+        "pct_peak": round(100.0 * unique / wall / 1e9 / PEAK_HBM_GBS, 2),
+        "effective_gbs_logical": round(logical / wall / 1e9, 2),
+        "logical_bytes_per_step": logical, "unique_bytes_per_step": unique,
+        "tokens_per_s": round(seqs / wall, 1),
+        "step_us_hip_events": round(ev * 1e6, 1),
+        "loads": "cached (MKV_ATTN_CACHED_LOADS)",
+        "nontemporal_loads": {"ms_per_step": round(wall_nt * 1e3, 4),
+                              "effective_gbs_logical": round(logical / wall_nt / 1e9, 2),
+                              "unique_gbs": round(unique / wall_nt / 1e9, 2)},
+        "cow_copies": {"pairs": int(cow_src.size), "bytes": int(cow_src.size) * per_pair,
+                       "avg_launch_us": round(cow_s * 1e6, 2),
+                       "gbs": round(cow_src.size * per_pair / cow_s / 1e9, 2)},
+        "compaction_moves": {"pairs": int(n_mv), "bytes": int(n_mv) * per_pair,
+                             "avg_launch_us": round(mv_s * 1e6, 2),
+                             "gbs": round(n_mv * per_pair / mv_s / 1e9, 2)},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(cfg, batch, logical, 1)
+        result["cpu_baseline"]["bytes"] = "logical (each sequence's whole context)"
+    print(json.dumps(result), flush=True)
+
+
+def bench_pressure(args):
+    """One step of a pool under pressure (the pool-pressure configuration):
+    the 217,982-block pool of a 200 GB budget (all 28 layers, Qwen2.5-7B
+    heads), 512 sequences with log-normal lengths (median 2,048, sigma 1,
+    capped at 32,768) in blocks from a seeded permutation of the pool. Per
+    step and layer, 8 sequences append a 512-token chunk (mkv_append) and
+    the other 504 run the fused append + decode attention; the chunks'
+    prefill attention is left out, as the configuration states."""
+    import torch
+
+    from mitten_amd import DeviceKvPool, PoolDesc
+    from mitten_amd import workloads as wl
+
+    cfg = wl.CONFIGS["qwen2.5-7b"]
+    L, Hq, Hkv, D = cfg["num_layers"], cfg["num_q_heads"], cfg["num_kv_heads"], cfg["head_dim"]
+    nblocks, seqs, chunk, chunk_seqs = 217_982, 512, 512, 8
+    batch, chunk_slots, lengths = wl.pool_pressure_step(nblocks, seqs, chunk, chunk_seqs,
+                                                        wl.SplitMix64(wl.BASE_SEED + 4))
+    desc = PoolDesc(L, Hkv, Hq, D, nblocks, "bf16")
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    n_chunk = int(chunk_slots.size)
+    step_bytes = L * (wl.algorithmic_bytes_attention(batch, Hq, Hkv, D, 2)
+                      + wl.algorithmic_bytes_append(batch.num_seqs, Hkv, D, 2)
+                      + wl.algorithmic_bytes_append(n_chunk, Hkv, D, 2))
+    with DeviceKvPool(desc) as pool:
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(wl.BASE_SEED + 4)
+        view = pool.tensor()
+        for layer in range(L):
+            view[layer].normal_(generator=gen)
+        del view
+        kc = torch.randn((L, n_chunk, Hkv, D), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
+        vc = torch.randn((L, n_chunk, Hkv, D), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
+        cs = torch.from_numpy(chunk_slots).to(dev)
+
+        def chunk_append(layer):
+            pool.append(layer, kc[layer], vc[layer], cs, stream=stream)
+
+        plan = pool.plan(batch.ctx_lens, stream=stream)
+        step = _decode_step_run(pool, plan, batch, L, Hq, Hkv, D, wl.BASE_SEED + 44, dev, stream,
+                                pre_layer=chunk_append)
+        wall, ev = _time_steps(step, args.steps, args.warmup, stream)
+        pool.check()
+        info = plan.info()
+        plan.close()
+        pool_bytes = pool.nbytes
+    result = {
+        "metric": "pool-pressure step (chunk appends + fused decode step): achieved HBM GB/s (% peak)",
+        "value": round(step_bytes / wall / 1e9, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(wall * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: N(0,1) K/V/Q from a seed; log-normal lengths and block ids from a seeded permutation",
+        "config": {"workload": f"pool-pressure step: {nblocks}-block pool ({pool_bytes / 1e9:.1f} GB), {seqs} "
+                               f"log-normal sequences, {chunk_seqs} x {chunk}-token chunk appends + "
+                               f"{batch.num_seqs} decodes, Qwen2.5-7B heads, {L} layers",
+                   "layers": L, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "block_size": 16,
+                   "pool_blocks": nblocks, "pool_bytes": pool_bytes, "sequences": seqs,
+                   "tokens_held": int(lengths.sum()), "decode_sequences": batch.num_seqs,
+                   "tokens_attended": batch.total_tokens, "chunk_tokens": n_chunk, "plan": info},
+        "pct_peak": round(100.0 * step_bytes / wall / 1e9 / PEAK_HBM_GBS, 2),
+        "step_bytes": step_bytes, "tokens_per_s": round((batch.num_seqs + n_chunk) / wall, 1),
+        "step_us_hip_events": round(ev * 1e6, 1),
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(cfg, batch, step_bytes, 1, paged=False)
+    print(json.dumps(result), flush=True)
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -586,6 +826,12 @@ def main():
         return
     if args.op == "extend":
         bench_extend(args)
+        return
+    if args.op == "shared":
+        bench_shared(args)
+        return
+    if args.op == "pressure":
+        bench_pressure(args)
         return
     import torch
 

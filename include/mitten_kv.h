@@ -78,9 +78,14 @@ enum {
                                     inference-model-qwen/src/model.rs:210-213 */
   MKV_ATTN_FORCE_VALU = 1u << 1, /* use the VALU kernel even where MFMA applies */
   MKV_ATTN_FORCE_MFMA = 1u << 2, /* fail unless the MFMA kernel applies */
-  MKV_ATTN_PER_HEAD_LOADS = 1u << 3 /* planned MFMA path: one wave per KV head loads its
-                                       own rows, instead of the workgroup loading whole
-                                       token rows of every head (same results) */
+  MKV_ATTN_PER_HEAD_LOADS = 1u << 3, /* planned MFMA path: one wave per KV head loads its
+                                        own rows, instead of the workgroup loading whole
+                                        token rows of every head (same results) */
+  MKV_ATTN_CACHED_LOADS = 1u << 4     /* planned MFMA path: K/V loads through the caches
+                                        instead of non-temporal. For batches whose tables
+                                        share blocks (a radix-shared prefix: its blocks are
+                                        re-read from the cache); slower for distinct blocks.
+                                        Same results. */
 };
 
 /* qk_norm_rope_append flags. */

@@ -35,7 +35,7 @@ MKV_ERR_NO_DEVICE = 5
 
 DEVERR_SLOT, DEVERR_BLOCK, DEVERR_TABLE, DEVERR_COPY, DEVERR_CTX, DEVERR_CHECKSUM = 1, 2, 4, 8, 16, 32
 
-ATTN_ZERO_SINK, ATTN_FORCE_VALU, ATTN_FORCE_MFMA, ATTN_PER_HEAD_LOADS = 1, 2, 4, 8
+ATTN_ZERO_SINK, ATTN_FORCE_VALU, ATTN_FORCE_MFMA, ATTN_PER_HEAD_LOADS, ATTN_CACHED_LOADS = 1, 2, 4, 8, 16
 PREP_PLAIN_Q, PREP_NO_NORM = 1, 2
 
 DTYPES = {"f32": 0, "bf16": 1}
@@ -441,7 +441,7 @@ class DeviceKvPool:
         p.build(ctx_lens, pieces, stream)
         return p
 
-    def _planned_args(self, plan, q, block_indptr, block_ids, out, scale, zero_sink, kernel):
+    def _planned_args(self, plan, q, block_indptr, block_ids, out, scale, zero_sink, kernel, cached_loads=False):
         d = self.desc
         if plan.pool is not self:
             raise BackendError(MKV_ERR_INVALID_ARGUMENT, "plan belongs to another pool")
@@ -464,12 +464,17 @@ class DeviceKvPool:
             flags |= ATTN_FORCE_MFMA | ATTN_PER_HEAD_LOADS
         elif kernel is not None:
             raise ValueError(f"unknown kernel {kernel!r}")
+        if cached_loads:
+            flags |= ATTN_CACHED_LOADS
         return out, scale, flags
 
     def decode_attention_planned(self, layer: int, plan, q, block_indptr, block_ids, out=None,
                                  scale: float | None = None, zero_sink: bool = False,
-                                 kernel: str | None = None, stream=None):
-        out, scale, flags = self._planned_args(plan, q, block_indptr, block_ids, out, scale, zero_sink, kernel)
+                                 kernel: str | None = None, stream=None, cached_loads: bool = False):
+        """cached_loads: K/V loads through the caches (MKV_ATTN_CACHED_LOADS),
+        for batches whose tables share blocks."""
+        out, scale, flags = self._planned_args(plan, q, block_indptr, block_ids, out, scale, zero_sink, kernel,
+                                               cached_loads)
         _raise(self._lib.mkv_decode_attention_planned(
             self._h, plan._h, layer, _dptr(q), _dptr(out), _dptr(block_indptr), _dptr(block_ids),
             scale, flags, _stream_handle(stream)))
@@ -477,11 +482,12 @@ class DeviceKvPool:
 
     def decode_step(self, layer: int, plan, k_new, v_new, q, block_indptr, block_ids, out=None,
                     scale: float | None = None, zero_sink: bool = False, kernel: str | None = None,
-                    stream=None):
+                    stream=None, cached_loads: bool = False):
         """Append k_new/v_new ([B, Hkv, D]) at position ctx-1 of every sequence,
         then attend over ctx tokens, in one launch (plus the split-K merge)."""
         d = self.desc
-        out, scale, flags = self._planned_args(plan, q, block_indptr, block_ids, out, scale, zero_sink, kernel)
+        out, scale, flags = self._planned_args(plan, q, block_indptr, block_ids, out, scale, zero_sink, kernel,
+                                               cached_loads)
         B = plan.num_seqs
         self._check_tensor(k_new, (B, d.num_kv_heads, d.head_dim), "k_new")
         self._check_tensor(v_new, (B, d.num_kv_heads, d.head_dim), "v_new")
@@ -492,7 +498,7 @@ class DeviceKvPool:
 
     def bind_decode_step(self, plan, k_new, v_new, q, block_indptr, block_ids, out,
                          scale: float | None = None, zero_sink: bool = False,
-                         kernel: str | None = None, stream=None):
+                         kernel: str | None = None, stream=None, cached_loads: bool = False):
         """Validates, once, the buffers of every layer of one decode step
         (k_new, v_new: [L, B, Hkv, D]; q, out: [L, B, Hq, D]) and returns
         `run(layer)`, which enqueues mkv_decode_step for that layer with no
@@ -504,7 +510,7 @@ class DeviceKvPool:
         self._check_tensor(q, (L, B, d.num_q_heads, d.head_dim), "q")
         self._check_tensor(out, (L, B, d.num_q_heads, d.head_dim), "out")
         _, scale, flags = self._planned_args(plan, q[0], block_indptr, block_ids, out[0], scale, zero_sink,
-                                             kernel)
+                                             kernel, cached_loads)
         fn = self._lib.mkv_decode_step
         h, ph = self._h, plan._h
         sh = _stream_handle(stream)

@@ -9,6 +9,7 @@ slot of the appended token, slot = table[pos // 16] * 16 + pos % 16
 """
 from __future__ import annotations
 
+import math
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -108,6 +109,84 @@ def decode_batch_from_contexts(contexts, rng: SplitMix64, extra_blocks: int = 0,
 
 def uniform_contexts(B: int, lo: int, hi: int, rng: SplitMix64):
     return [rng.uniform_int(lo, hi) for _ in range(B)]
+
+
+def lognormal_lengths(rng: SplitMix64, n: int, median: int, sigma: float, cap: int) -> list[int]:
+    """n lengths median * exp(sigma * z), z ~ N(0,1) by Box-Muller, rounded
+    and clamped to [1, cap]."""
+    out = []
+    for _ in range(n):
+        u1, u2 = rng.uniform01(), rng.uniform01()
+        z = math.sqrt(-2.0 * math.log(u1)) * math.cos(2.0 * math.pi * u2)
+        out.append(int(min(cap, max(1, round(median * math.exp(sigma * z))))))
+    return out
+
+
+def shared_prefix_batch(num_seqs: int, prefix: int, suffix_lo: int, suffix_hi: int,
+                        rng: SplitMix64) -> DecodeBatch:
+    """A decode step after radix sharing and copy-on-write: every sequence
+    holds `prefix` shared tokens plus a suffix ~U{suffix_lo..suffix_hi} and
+    appends one token. Its table starts with the prefix's full blocks, the
+    same ids in every table (refcounted, read by every sequence), followed by
+    its own blocks: its copy of the prefix's partial block and its suffix.
+    Ids come from a seeded permutation of the pool. meta["shared_blocks"]
+    holds the shared ids, meta["own_first"] each sequence's first own block
+    (its copy of the partial block) and meta["unique_tokens"] the tokens
+    attended once each: the shared blocks' tokens once plus every
+    sequence's own tokens."""
+    full = prefix // PAGE
+    ctx = np.asarray([prefix + rng.uniform_int(suffix_lo, suffix_hi) for _ in range(num_seqs)], np.int64)
+    attend = ctx + 1
+    own = (attend + PAGE - 1) // PAGE - full
+    num_blocks = full + int(own.sum())
+    perm = permutation(num_blocks, rng)
+    shared = perm[:full]
+    indptr = np.zeros(num_seqs + 1, np.int32)
+    np.cumsum(own + full, out=indptr[1:])
+    ids = np.empty(int(indptr[-1]), np.int32)
+    nxt = full
+    own_first = np.empty(num_seqs, np.int32)
+    for b in range(num_seqs):
+        o = int(own[b])
+        ids[indptr[b]:indptr[b] + full] = shared
+        ids[indptr[b] + full:indptr[b + 1]] = perm[nxt:nxt + o]
+        own_first[b] = perm[nxt]
+        nxt += o
+    slots = ids[indptr[:-1] + ctx // PAGE].astype(np.int64) * PAGE + ctx % PAGE
+    unique = full * PAGE + int((attend - full * PAGE).sum())
+    return DecodeBatch(attend.astype(np.int32), indptr, ids, slots.astype(np.int32), num_blocks,
+                       meta={"shared_blocks": shared.astype(np.int32), "own_first": own_first,
+                             "unique_tokens": unique, "prefix": prefix})
+
+
+def pool_pressure_step(num_blocks: int, num_seqs: int, chunk: int, chunk_seqs: int,
+                       rng: SplitMix64) -> tuple[DecodeBatch, np.ndarray, np.ndarray]:
+    """One step of a pool under pressure: `num_seqs` sequences with lengths
+    ~LogNormal(ln 2048, 1) capped at 32,768 hold blocks drawn from a seeded
+    permutation of a `num_blocks` pool; the first `chunk_seqs` append a
+    `chunk`-token chunk, the others decode one token. Returns the decode
+    batch of the decoding sequences, the chunk tokens' slots and all
+    sequences' lengths before the step."""
+    lengths = np.asarray(lognormal_lengths(rng, num_seqs, 2048, 1.0, 32768), np.int64)
+    grow = np.where(np.arange(num_seqs) < chunk_seqs, chunk, 1)
+    nblk = (lengths + grow + PAGE - 1) // PAGE
+    if int(nblk.sum()) > num_blocks:
+        raise ValueError("the sequences need more blocks than the pool holds")
+    perm = permutation(num_blocks, rng)
+    starts = np.concatenate([[0], np.cumsum(nblk)])
+    tables = [perm[starts[b]:starts[b + 1]] for b in range(num_seqs)]
+    chunk_slots = []
+    for b in range(chunk_seqs):
+        pos = lengths[b] + np.arange(chunk)
+        chunk_slots.append(tables[b][pos // PAGE].astype(np.int64) * PAGE + pos % PAGE)
+    dec = range(chunk_seqs, num_seqs)
+    ctx = lengths[chunk_seqs:]
+    indptr = np.zeros(len(dec) + 1, np.int32)
+    np.cumsum(nblk[chunk_seqs:], out=indptr[1:])
+    ids = np.concatenate([tables[b] for b in dec]).astype(np.int32)
+    slots = ids[indptr[:-1] + ctx // PAGE].astype(np.int64) * PAGE + ctx % PAGE
+    batch = DecodeBatch((ctx + 1).astype(np.int32), indptr, ids, slots.astype(np.int32), num_blocks)
+    return batch, np.concatenate(chunk_slots).astype(np.int32), lengths.astype(np.int32)
 
 
 # Benchmark configurations (shapes of the BASELINE configurations).

@@ -346,6 +346,38 @@ def test_planned_zero_sink(shape):
     assert_attention_close(got, ref, dt)
 
 
+@pytest.mark.parametrize("shape", ["qwen7b-bf16", "gemma2b-bf16"])
+def test_cached_loads_on_shared_prefix_tables(shape):
+    """Tables that share a prefix's blocks (as after radix sharing), decoded
+    with the cache-resident loads (MKV_ATTN_CACHED_LOADS): the fused step
+    appends bit-exactly, the outputs are bit-identical to the non-temporal
+    default and match the oracle."""
+    L, Hq, Hkv, D, dt = SHAPES[shape]
+    batch = wl.shared_prefix_batch(24, 300, 5, 90, wl.SplitMix64(66))
+    desc = PoolDesc(L, Hkv, Hq, D, batch.num_blocks, dt)
+    host = normal(67, desc.shape, dt)
+    B = batch.num_seqs
+    q = normal(68, (B, Hq, D), dt)
+    kn, vn = normal(69, (B, Hkv, D), dt), normal(70, (B, Hkv, D), dt)
+    outs = []
+    for cached in (False, True):
+        with DeviceKvPool(desc) as pool:
+            pool.write(host)
+            plan = pool.plan(batch.ctx_lens, pieces=11)
+            o = pool.decode_step(L - 1, plan, to_device(kn), to_device(vn), to_device(q), _i32(batch.block_indptr),
+                                 _i32(batch.block_ids), kernel="mfma", cached_loads=cached)
+            pool.check()
+            outs.append((to_host(o), pool.read()))
+            plan.close()
+    want = host.copy()
+    assert orc.append(odesc(desc), want, L - 1, kn, vn, batch.slot_mapping) == -1
+    assert np.array_equal(bits(outs[1][1]), bits(want))
+    assert np.array_equal(bits(outs[0][0]), bits(outs[1][0]))
+    ref = orc.decode_attention(odesc(desc), want, L - 1, widen(q), batch.block_indptr, batch.block_ids,
+                               batch.ctx_lens)
+    assert_attention_close(outs[1][0], ref, dt)
+
+
 @pytest.mark.parametrize("name", ["qwen2.5-7b", "gemma-2b-mqa"])
 def test_decode_step_full_config_one_layer(name):
     """Fused append + planned attention at the configuration's full size."""

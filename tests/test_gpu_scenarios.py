@@ -18,8 +18,6 @@ gathers; within the attention tolerances for decode attention).
 """
 from __future__ import annotations
 
-import math
-
 import numpy as np
 import pytest
 
@@ -235,21 +233,12 @@ def test_c4_radix_sharing_cow_decode_and_compaction():
 C5_BLOCKS, C5_SEQS, C5_CHUNK, C5_CHUNK_SEQS = 217_982, 512, 512, 8
 
 
-def _lognormal_lengths(rng: wl.SplitMix64, n: int, median: int, sigma: float, cap: int):
-    out = []
-    for _ in range(n):
-        u1, u2 = rng.uniform01(), rng.uniform01()
-        z = math.sqrt(-2.0 * math.log(u1)) * math.cos(2.0 * math.pi * u2)  # Box-Muller
-        out.append(int(min(cap, max(1, round(median * math.exp(sigma * z))))))
-    return out
-
-
 def test_c5_pool_pressure_chunked_append_and_decode():
     import torch
 
     L, Hq, Hkv, D = 1, 28, 4, 128  # Qwen-7B heads, 1 of 28 layers
     rng = wl.SplitMix64(wl.BASE_SEED + 4)
-    lengths = _lognormal_lengths(rng, C5_SEQS, 2048, 1.0, 32768)
+    lengths = wl.lognormal_lengths(rng, C5_SEQS, 2048, 1.0, 32768)
     desc = PoolDesc(L, Hkv, Hq, D, C5_BLOCKS, "bf16")
     bm = BlockManager(C5_BLOCKS)
     seqs = list(range(C5_SEQS))
