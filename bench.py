@@ -690,6 +690,32 @@ def bench_shared(args):
         pool.check()
         info = plan.info()
         plan.close()
+        # The shared-prefix step (mkv_decode_step_shared_prefix): the prefix
+        # read once for all 256 sequences on MFMA tiles, the suffixes through
+        # a suffix plan, both merged.
+        full = prefix // 16
+        ip = batch.block_indptr
+        sptr = (ip - full * np.arange(seqs + 1)).astype(np.int32)
+        sids = np.concatenate([batch.block_ids[ip[b] + full:ip[b + 1]] for b in range(seqs)]).astype(np.int32)
+        slen = (batch.ctx_lens - 16 * full).astype(np.int32)
+        i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(dev)
+        splan = pool.plan_suffixes(slen, stream=stream)
+        gen2 = torch.Generator(device=dev)
+        gen2.manual_seed(wl.BASE_SEED + 33)
+        bf = lambda *shape: torch.randn(shape, generator=gen2, device=dev, dtype=torch.float32).to(torch.bfloat16)
+        q, kn, vn = bf(L, seqs, Hq, D), bf(L, seqs, Hkv, D), bf(L, seqs, Hkv, D)
+        out = torch.empty_like(q)
+        run_sp = pool.bind_decode_step_shared_prefix(splan, kn, vn, q, i32(batch.meta["shared_blocks"]), i32(sptr),
+                                                     i32(sids), out, stream=stream)
+
+        def step_sp():
+            splan.build(slen, 0, stream=stream)
+            for layer in range(L):
+                run_sp(layer)
+
+        wall_sp, ev_sp = _time_steps(step_sp, args.steps, args.warmup, stream)
+        pool.check()
+        splan.close()
         # Copy-on-write: the last holder keeps the prefix's partial block, the
         # other 255 sequences get copies. Compaction: a fifth of the blocks
         # move from the top of the id space into holes below it.
@@ -722,6 +748,12 @@ def bench_shared(args):
         "nontemporal_loads": {"ms_per_step": round(wall_nt * 1e3, 4),
                               "effective_gbs_logical": round(logical / wall_nt / 1e9, 2),
                               "unique_gbs": round(unique / wall_nt / 1e9, 2)},
+        "shared_prefix_step": {"entry": "mkv_decode_step_shared_prefix", "ms_per_step": round(wall_sp * 1e3, 4),
+                               "step_us_hip_events": round(ev_sp * 1e6, 1),
+                               "effective_gbs_logical": round(logical / wall_sp / 1e9, 2),
+                               "unique_gbs": round(unique / wall_sp / 1e9, 2),
+                               "pct_peak_unique": round(100.0 * unique / wall_sp / 1e9 / PEAK_HBM_GBS, 2),
+                               "tokens_per_s": round(seqs / wall_sp, 1)},
         "cow_copies": {"pairs": int(cow_src.size), "bytes": int(cow_src.size) * per_pair,
                        "avg_launch_us": round(cow_s * 1e6, 2),
                        "gbs": round(cow_src.size * per_pair / cow_s / 1e9, 2)},

@@ -226,6 +226,40 @@ MKV_API int mkv_decode_step(mkv_pool *pool, const mkv_decode_plan *plan, int32_t
                             const int32_t *d_block_indptr, const int32_t *d_block_ids,
                             float scale, uint32_t flags, void *stream);
 
+/* ---- decode over a shared prefix ------------------------------------------ */
+
+/* A step whose sequences all share one prefix of full blocks, as radix
+ * sharing hands them out (inference-engine/src/radix_cache.rs:64-117 returns
+ * the same pages to every request that matched the prefix). There is no
+ * counterpart in the reference: it keeps one contiguous cache per request
+ * and attends over the prefix again for each (model.rs:390-416). Here the
+ * prefix's K/V are read once for all sequences and its attention runs on
+ * MFMA tiles. Sequence b attends the prefix's 16 * prefix_blocks tokens
+ * followed by its suffix of suffix_len_b tokens.
+ *
+ * mkv_decode_plan_build_suffixes: as mkv_decode_plan_build, over the suffix
+ * lengths (>= 1: the appended token is in the suffix). A plan built this way
+ * stores every sequence's result as partials for the step below.
+ *
+ * mkv_decode_step_shared_prefix: mkv_decode_step over prefix + suffix.
+ * d_prefix_ids: the prefix's prefix_blocks block ids (device). The tables
+ * d_block_indptr / d_block_ids hold each sequence's suffix blocks only;
+ * d_k_new / d_v_new (both or neither) go at suffix position suffix_len_b - 1.
+ * Three launches: the prefix over all queries (f32 partials per key range in
+ * the pool-owned workspace, grown on demand as for mkv_extend_attention),
+ * the suffixes through the plan, and their merge. bf16 pools, head_dim
+ * 64/128/256, at most 16 query heads per KV head. Same result as
+ * mkv_decode_step over tables prefix + suffix, within the attention
+ * tolerance (the partials merge in another order). Flags: MKV_ATTN_ZERO_SINK. */
+MKV_API int mkv_decode_plan_build_suffixes(mkv_decode_plan *plan, const int32_t *h_suffix_lens,
+                                           int32_t num_seqs, int32_t pieces, void *stream);
+MKV_API int mkv_decode_step_shared_prefix(mkv_pool *pool, const mkv_decode_plan *plan,
+                                          int32_t layer, const void *d_k_new, const void *d_v_new,
+                                          const void *d_q, void *d_o, const int32_t *d_prefix_ids,
+                                          int32_t prefix_blocks, const int32_t *d_block_indptr,
+                                          const int32_t *d_block_ids, float scale, uint32_t flags,
+                                          void *stream);
+
 /* ---- extend (chunked prefill) attention ----------------------------------- */
 
 /* Causal attention of each sequence's newest tokens over its whole cache:

@@ -537,14 +537,15 @@ __device__ __forceinline__ void run_segment(const KArgs &a, const Seg &sg, int l
   }
 }
 
-// Log-sum-exp merge of n partial rows ws[base + s*stride], s < n, into o.
-// Lane s holds partial s's (m, l); lane d holds dims d + 64k of every
-// partial. Up to 16 partials merge in one memory round trip: all their loads
-// are issued before the first use; weights exp2(m_s - M) are broadcast with
-// readlane. More partials take further rounds of 16.
-template <int D, bool BF16>
-__device__ __forceinline__ void merge_rows(const KArgs &a, int lane, int64_t base, int64_t stride, int n,
-                                           int64_t out_row) {
+// Log-sum-exp merge of n partial rows into row out_row of o: partial s has
+// (m, l) at ml_at(s) and its D floats at o_at(s). Lane s holds partial s's
+// (m, l); lane d holds dims d + 64k of every partial. Up to 16 partials
+// merge in one memory round trip: all their loads are issued before the
+// first use; weights exp2(m_s - M) are broadcast with readlane. More
+// partials take further rounds of 16.
+template <int D, bool BF16, class MlAt, class OAt>
+__device__ __forceinline__ void merge_partials(const KArgs &a, int lane, int n, MlAt ml_at, OAt o_at,
+                                               int64_t out_row) {
   // Lane owns DPL contiguous dims (one vector load per partial row); all
   // loads of up to SB partials are issued before their first use.
   constexpr int DPL = (D + 63) / 64;
@@ -557,13 +558,12 @@ __device__ __forceinline__ void merge_rows(const KArgs &a, int lane, int64_t bas
   for (int s0 = 0; s0 < n; s0 += SB) {
     const int cnt = min(SB, n - s0);
     float2 ml = make_float2(-INFINITY, 0.0f);
-    if (lane < cnt) ml = *reinterpret_cast<const float2 *>(a.ws_ml + 2 * (base + (int64_t)(s0 + lane) * stride));
+    if (lane < cnt) ml = *reinterpret_cast<const float2 *>(ml_at(s0 + lane));
     fvec ov[SB];
 #pragma unroll
     for (int i = 0; i < SB; i++) {
       ov[i] = fvec{};
-      if (i < cnt && has)
-        ov[i] = *reinterpret_cast<const fvec *>(a.ws_o + (base + (int64_t)(s0 + i) * stride) * D + d0);
+      if (i < cnt && has) ov[i] = *reinterpret_cast<const fvec *>(o_at(s0 + i) + d0);
     }
     // Max and weighted sum over lanes 0..15 (the partials) by DPP row steps,
     // read from lane 0 (no LDS round trips).
@@ -598,6 +598,15 @@ __device__ __forceinline__ void merge_rows(const KArgs &a, int lane, int64_t bas
   } else {
     *reinterpret_cast<fvec *>(reinterpret_cast<float *>(a.o) + out_row * D + d0) = acc * f;
   }
+}
+
+// Partials ws[base + s*stride], s < n, of the kernel's workspace.
+template <int D, bool BF16>
+__device__ __forceinline__ void merge_rows(const KArgs &a, int lane, int64_t base, int64_t stride, int n,
+                                           int64_t out_row) {
+  merge_partials<D, BF16>(
+      a, lane, n, [&](int s) { return a.ws_ml + 2 * (base + (int64_t)s * stride); },
+      [&](int s) { return a.ws_o + (base + (int64_t)s * stride) * D; }, out_row);
 }
 
 // ===========================================================================
@@ -1282,12 +1291,16 @@ constexpr int kExtKB = 2;  // blocks per softmax step of the extend kernel
 constexpr int kExtR = 2;   // ring depth (steps) of the extend kernel
 
 struct ExtArgs {
-  const int32_t *q_indptr;  // [B+1] query tokens of each sequence in q / o
+  const int32_t *q_indptr;  // [B+1] query tokens of each sequence in q / o; null: one sequence of
+                            // v_nq queries over v_ctx tokens of the table a.ids (no indptr, no ctx)
   const int32_t *ctx;       // [B] tokens in the cache, the chunk included
   int32_t B, max_ctx;
   int32_t tiles, per_xcd;   // query tiles per sequence; logical workgroups per XCD
   int32_t splits;           // key-range splits per (tile, KV head, sequence); > 1: f32 partials + merge
   int32_t max_q;            // max_q_len: with splits, partial rows exist for B * max_q tokens
+  int32_t causal;           // 0: every query sees all ctx keys (a shared prefix's decode queries)
+  int32_t partial;          // 1: f32 partials whatever the split count, merged by the caller
+  int32_t v_nq, v_ctx;      // the one sequence when q_indptr is null
 };
 
 // Workgroups are dealt to the 8 XCDs round-robin by linear index. The
@@ -1330,18 +1343,19 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
   const int m16 = lane & 15, g4 = lane >> 4, a4 = m16 >> 2, rq = m16 & 3;
   int t, h, b, sp;
   if (!ext_tile(e, a.Hkv, t, h, b, sp)) return;
-  const int q0 = e.q_indptr[b], nq = e.q_indptr[b + 1] - q0;
+  const bool virt = e.q_indptr == nullptr;  // one sequence; the host checked its table length
+  const int q0 = virt ? 0 : e.q_indptr[b], nq = virt ? e.v_nq : e.q_indptr[b + 1] - q0;
   if (nq <= 0 || 16 * TP * t >= nq) return;
-  const int ctx = e.ctx[b];
-  // (With splits, a chunk longer than max_q_len or a q_indptr past
+  const int ctx = virt ? e.v_ctx : e.ctx[b];
+  // (With partials, a chunk longer than max_q_len or a q_indptr past
   // num_seqs * max_q_len tokens would address partial rows past the workspace.)
-  if (nq > ctx || ctx > e.max_ctx ||
-      (e.splits > 1 && (nq > e.max_q || q0 < 0 || (int64_t)q0 + nq > (int64_t)e.B * e.max_q))) {
+  if ((e.causal && nq > ctx) || ctx < 1 || ctx > e.max_ctx ||
+      ((e.splits > 1 || e.partial) && (nq > e.max_q || q0 < 0 || (int64_t)q0 + nq > (int64_t)e.B * e.max_q))) {
     if (threadIdx.x == 0 && t == 0) record_error(a.d_err, MKV_DEVERR_CTX);
     return;
   }
-  const int tab0 = a.indptr[b], nbt = (ctx + kPageSize - 1) / kPageSize;
-  if (tab0 < 0 || a.indptr[b + 1] - tab0 < nbt) {
+  const int tab0 = virt ? 0 : a.indptr[b], nbt = (ctx + kPageSize - 1) / kPageSize;
+  if (!virt && (tab0 < 0 || a.indptr[b + 1] - tab0 < nbt)) {
     if (threadIdx.x == 0 && t == 0) record_error(a.d_err, MKV_DEVERR_TABLE);
     return;
   }
@@ -1353,8 +1367,10 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
   // The workgroup holds TP sub-tiles of 16 positions; wave = (sub-tile, head slot).
   const int sub = wave / WG, hw = wave % WG;
   const int row0 = 16 * (TP * t + sub);                  // first chunk row of this wave's sub-tile
-  const int qlo = ctx - nq + row0;                       // its first query position
-  const int qhi_wg = min(ctx - nq + 16 * TP * (t + 1) - 1, ctx - 1);
+  // Its first query position; without the causal mask every query stands at
+  // the last position and sees all ctx keys.
+  const int qlo = e.causal ? ctx - nq + row0 : ctx - 1;
+  const int qhi_wg = e.causal ? min(ctx - nq + 16 * TP * (t + 1) - 1, ctx - 1) : ctx - 1;
   const int n = qhi_wg / kPageSize + 1;                  // blocks the workgroup streams: keys 0..qhi_wg
   const int nw = min(n, (qlo + 15) / kPageSize + 1);     // blocks this wave's sub-tile sees
   // Steps of KB blocks; with splits, this workgroup takes its share of them
@@ -1364,7 +1380,7 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
   const int st0 = min(sp * sps, nsteps_all), st1 = min(st0 + sps, nsteps_all);
   const bool computes = hw < a.G;
   const int hq = h * a.G + min(hw, a.G - 1);
-  const int qp = qlo + m16;                   // this lane's query position (rows past nq: unused)
+  const int qp = e.causal ? qlo + m16 : ctx - 1;  // this lane's query position (rows past nq: unused)
   const int64_t spare = dummy_offset(a);
 
   // Q^T operand: lane holds Q[row 16t + lane%16][32r + 8*(lane/16) .. +8].
@@ -1546,7 +1562,7 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
   st.l += __shfl_xor(st.l, 32);
   const int row = row0 + m16;
   if (row >= nq) return;
-  if (e.splits > 1) {  // f32 partial (m, l, O) of this key range, merged by merge_ext_kernel
+  if (e.splits > 1 || e.partial) {  // f32 partial (m, l, O) of this key range, merged later
     const int64_t prow = ((int64_t)(q0 + row) * a.Hq + hq) * e.splits + sp;
     float *wo = a.ws_o + prow * D + 4 * g4;
 #pragma unroll
@@ -1585,6 +1601,32 @@ __global__ void __launch_bounds__(256) merge_planned_kernel(KArgs a, PlanDev pd)
   const int first = pd.seq_piece0[b];
   merge_rows<D, BF16>(a, lane, (int64_t)(first + b) * a.Hq + hq, a.Hq, pd.seq_npiece[b],
                       (int64_t)b * a.Hq + hq);
+}
+
+// Decode over a shared prefix: row (sequence b, query head hq) merges b's
+// suffix partials (one per piece, in the plan's workspace, as
+// merge_planned_kernel reads them) with the prefix's S key-range partials
+// (extend workspace rows (b * Hq + hq) * S + s); one wave per row, every
+// sequence of the plan.
+struct PrefixParts {
+  const float *ml;  // (m, l) pairs of the prefix partials
+  const float *o;   // their f32 rows
+  int32_t S;        // key-range partials per (sequence, query head)
+};
+
+template <int D, bool BF16>
+__global__ void __launch_bounds__(256) merge_prefix_kernel(KArgs a, PlanDev pd, PrefixParts pp) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  if (row >= (int64_t)pd.B * a.Hq) return;
+  const int b = (int)(row / a.Hq), hq = (int)(row % a.Hq);
+  const int n1 = pd.seq_npiece[b];
+  const int64_t base1 = (int64_t)(pd.seq_piece0[b] + b) * a.Hq + hq, base2 = row * pp.S;
+  merge_partials<D, BF16>(
+      a, lane, n1 + pp.S,
+      [&](int s) { return s < n1 ? a.ws_ml + 2 * (base1 + (int64_t)s * a.Hq) : pp.ml + 2 * (base2 + s - n1); },
+      [&](int s) { return s < n1 ? a.ws_o + (base1 + (int64_t)s * a.Hq) * D : pp.o + (base2 + s - n1) * D; }, row);
 }
 
 // ===========================================================================
@@ -1714,6 +1756,7 @@ struct Plan {
   size_t flat_cap = 0;
   const int32_t *bound_indptr = nullptr;  // tables flat_id was built from
   const int32_t *bound_ids = nullptr;
+  bool all_partial = false;  // every sequence stores partials (built for a shared prefix's suffixes)
 };
 
 static PlanDev plan_dev(const Plan *pl) {
@@ -1909,8 +1952,8 @@ static int64_t coop_resident(Pool *p) {
   return p->coop_slots;
 }
 
-extern "C" int mkv_decode_plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens,
-                                     int32_t num_seqs, int32_t pieces, void *stream) {
+static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t num_seqs, int32_t pieces,
+                      bool all_partial, void *stream) {
   if (!plan) return set_error(MKV_ERR_INVALID_ARGUMENT, "plan is NULL");
   Plan *pl = reinterpret_cast<Plan *>(plan);
   const Geom &g = pl->pool->g;
@@ -2014,11 +2057,11 @@ extern "C" int mkv_decode_plan_build(mkv_decode_plan *plan, const int32_t *h_ctx
   }
   int n_merge = 0;
   for (int32_t b = 0; b < num_seqs; b++)
-    if (snpiece[b] > 1) mseq[n_merge++] = b;
+    if (snpiece[b] > 1 || all_partial) mseq[n_merge++] = b;
   int32_t *fseq = mseq + n_merge, *fmeta = fseq + total;
   for (int32_t b = 0; b < num_seqs; b++) {
     const int nb = blk0[b + 1] - blk0[b];
-    const int single = snpiece[b] == 1 ? kMetaSingle : 0;
+    const int single = snpiece[b] == 1 && !all_partial ? kMetaSingle : 0;
     for (int j = 0; j < nb; j++) {
       const int last = j == nb - 1;
       fseq[blk0[b] + j] = b;
@@ -2065,7 +2108,18 @@ extern "C" int mkv_decode_plan_build(mkv_decode_plan *plan, const int32_t *h_ctx
   pl->BP = (int32_t)BP;
   pl->total = (int32_t)total;
   pl->n_merge = n_merge;
+  pl->all_partial = all_partial;
   return MKV_OK;
+}
+
+extern "C" int mkv_decode_plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t num_seqs,
+                                     int32_t pieces, void *stream) {
+  return plan_build(plan, h_ctx_lens, num_seqs, pieces, false, stream);
+}
+
+extern "C" int mkv_decode_plan_build_suffixes(mkv_decode_plan *plan, const int32_t *h_suffix_lens,
+                                              int32_t num_seqs, int32_t pieces, void *stream) {
+  return plan_build(plan, h_suffix_lens, num_seqs, pieces, true, stream);
 }
 
 extern "C" int mkv_decode_plan_info(const mkv_decode_plan *plan, int32_t *out_pieces,
@@ -2080,7 +2134,8 @@ extern "C" int mkv_decode_plan_info(const mkv_decode_plan *plan, int32_t *out_pi
 
 static int launch_planned(Pool *p, const Plan *pl, int32_t layer, const void *d_k_new, const void *d_v_new,
                           const void *d_q, void *d_o, const int32_t *d_block_indptr,
-                          const int32_t *d_block_ids, float scale, uint32_t flags, void *stream) {
+                          const int32_t *d_block_ids, float scale, uint32_t flags, void *stream,
+                          bool merge = true) {
   const Geom &g = p->g;
   if (pl->pool != p) return set_error(MKV_ERR_INVALID_ARGUMENT, "plan belongs to another pool");
   if (pl->B < 1) return set_error(MKV_ERR_INVALID_ARGUMENT, "plan was never built");
@@ -2163,7 +2218,7 @@ static int launch_planned(Pool *p, const Plan *pl, int32_t layer, const void *d_
     MKV_DISPATCH(attn_planned_kernel, grid, block, hs, a, pd);
     MKV_CHECK_LAUNCH("attn_planned_kernel");
   }
-  if (pl->n_merge) {
+  if (pl->n_merge && merge) {
     const int64_t mwgs = ((int64_t)pl->n_merge * g.Hq + 3) / 4;
     MKV_DISPATCH_MERGE(merge_planned_kernel, dim3((unsigned)mwgs), dim3(256), hs, a, pd);
     MKV_CHECK_LAUNCH("merge_planned_kernel");
@@ -2188,6 +2243,68 @@ extern "C" int mkv_decode_step(mkv_pool *pool, const mkv_decode_plan *plan, int3
   if (!d_k_new || !d_v_new) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL new K/V rows");
   return launch_planned(reinterpret_cast<Pool *>(pool), reinterpret_cast<const Plan *>(plan), layer,
                         d_k_new, d_v_new, d_q, d_o, d_block_indptr, d_block_ids, scale, flags, stream);
+}
+
+static int launch_ext_tiles(Pool *p, KArgs &a, ExtArgs &e, int split_cap, hipStream_t hs);
+
+extern "C" int mkv_decode_step_shared_prefix(mkv_pool *pool, const mkv_decode_plan *plan, int32_t layer,
+                                             const void *d_k_new, const void *d_v_new, const void *d_q,
+                                             void *d_o, const int32_t *d_prefix_ids, int32_t prefix_blocks,
+                                             const int32_t *d_block_indptr, const int32_t *d_block_ids,
+                                             float scale, uint32_t flags, void *stream) {
+  if (!pool || !plan) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL pool or plan");
+  Pool *p = reinterpret_cast<Pool *>(pool);
+  const Plan *pl = reinterpret_cast<const Plan *>(plan);
+  const Geom &g = p->g;
+  if (pl->pool != p) return set_error(MKV_ERR_INVALID_ARGUMENT, "plan belongs to another pool");
+  if (pl->B < 1) return set_error(MKV_ERR_INVALID_ARGUMENT, "plan was never built");
+  if (!pl->all_partial)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "the plan must be built with mkv_decode_plan_build_suffixes");
+  if (!d_prefix_ids || prefix_blocks < 1 || prefix_blocks > INT32_MAX / (2 * kPageSize))
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "need a prefix of >= 1 block ids");
+  if ((d_k_new == nullptr) != (d_v_new == nullptr))
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "give both new K and V rows, or neither");
+  bool use_mfma = false;
+  int rc = check_common(p, layer, flags, scale, use_mfma);
+  if (rc) return rc;
+  if (!use_mfma || g.Hq / g.Hkv > kQChunkMfma)
+    return set_error(MKV_ERR_INVALID_ARGUMENT,
+                     "shared-prefix decode needs bf16 KV, head_dim 64/128/256 and at most 16 query heads per KV head");
+  if (!d_q || !d_o || !d_block_indptr || !d_block_ids)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL device pointer");
+  if (!aligned16(d_q) || !aligned16(d_o)) return set_error(MKV_ERR_INVALID_ARGUMENT, "q and o must be 16-byte aligned");
+  DeviceGuard guard(p->device);
+  hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  // 1. The prefix: the B decode queries as one chunk over the prefix's keys,
+  //    no causal mask, f32 partials per key range (pool workspace).
+  KArgs ap = make_kargs(p, layer, d_q, d_o, nullptr, d_prefix_ids, scale, flags, true);
+  ExtArgs e{};
+  e.B = 1;
+  e.max_ctx = e.v_ctx = prefix_blocks * kPageSize;
+  e.max_q = e.v_nq = pl->B;
+  e.causal = 0;
+  e.partial = 1;
+  rc = launch_ext_tiles(p, ap, e, 16, hs);
+  if (rc) return rc;
+  // 2. The suffixes (and the fused append): every sequence's partials, one
+  //    per piece, in the plan's workspace.
+  rc = launch_planned(p, pl, layer, d_k_new, d_v_new, d_q, d_o, d_block_indptr, d_block_ids, scale, flags, stream,
+                      false);
+  if (rc) return rc;
+  // 3. Both runs of partials merged into o.
+  KArgs am = make_kargs(p, layer, d_q, d_o, d_block_indptr, d_block_ids, scale, flags, true);
+  am.ws_ml = reinterpret_cast<float *>(pl->d_ws);
+  am.ws_o = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(pl->d_ws) + pl->ws_ml_bytes);
+  const PlanDev pd = plan_dev(pl);
+  const PrefixParts pp{ap.ws_ml, ap.ws_o, e.splits};
+  const dim3 mgrid((unsigned)(((int64_t)pl->B * g.Hq + 3) / 4));
+  switch (g.D) {
+    case 64: hipLaunchKernelGGL((merge_prefix_kernel<64, true>), mgrid, dim3(256), 0, hs, am, pd, pp); break;
+    case 128: hipLaunchKernelGGL((merge_prefix_kernel<128, true>), mgrid, dim3(256), 0, hs, am, pd, pp); break;
+    default: hipLaunchKernelGGL((merge_prefix_kernel<256, true>), mgrid, dim3(256), 0, hs, am, pd, pp); break;
+  }
+  MKV_CHECK_LAUNCH("merge_prefix_kernel");
+  return MKV_OK;
 }
 
 extern "C" int mkv_extend_attention(mkv_pool *pool, int32_t layer, const void *d_q, void *d_o,
@@ -2227,18 +2344,31 @@ extern "C" int mkv_extend_attention(mkv_pool *pool, int32_t layer, const void *d
     MKV_CHECK_LAUNCH("attn_ext_split_kernel");
     return MKV_OK;
   }
-  if (4 * (((int64_t)max_q_len + 15) / 16 * g.Hkv * num_seqs) + 8 > INT32_MAX)
-    return set_error(MKV_ERR_INVALID_ARGUMENT, "grid too large");
   DeviceGuard guard(p->device);
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
   KArgs a = make_kargs(p, layer, d_q, d_o, d_block_indptr, d_block_ids, scale, flags, true);
-  ExtArgs e;
+  ExtArgs e{};
   e.q_indptr = d_q_indptr;
   e.ctx = d_ctx_lens;
   e.B = num_seqs;
   e.max_ctx = max_ctx_len;
-  e.splits = 1;
   e.max_q = max_q_len;
+  e.causal = 1;
+  return launch_ext_tiles(p, a, e, 4, hs);
+}
+
+// MFMA query tiles of the extend kernel for e (B, max_q, max_ctx, causal,
+// partial and the sequence arguments set): picks the instantiation and the
+// key-range split (at most split_cap), grows the pool workspace when
+// partials are stored, launches, and merges the splits unless e.partial
+// (then a.ws_ml / a.ws_o and e.splits describe the partials left).
+static int launch_ext_tiles(Pool *p, KArgs &a, ExtArgs &e, int split_cap, hipStream_t hs) {
+  const Geom &g = p->g;
+  const int G = g.Hq / g.Hkv;
+  const int64_t num_seqs = e.B, max_q_len = e.max_q, max_ctx_len = e.max_ctx;
+  if (((max_q_len + 15) / 16 * g.Hkv * num_seqs) * split_cap + 8 > INT32_MAX)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "grid too large");
+  e.splits = 1;
   // Waves per 16-position sub-tile: the next power of two >= G. Two
   // sub-tiles per workgroup share each K/V tile (K/V streamed once per 32
   // positions) where that stays within 16 waves and their register budget
@@ -2286,9 +2416,10 @@ extern "C" int mkv_extend_attention(mkv_pool *pool, int32_t layer, const void *d
   const int64_t slots = per_cu > 0 && cus > 0 ? (int64_t)per_cu * cus : 0;
   const int64_t steps_max = ((int64_t)(max_ctx_len + kPageSize - 1) / kPageSize + kExtKB - 1) / kExtKB;
   if (per_split < slots)
-    e.splits = (int32_t)std::min<int64_t>({4, (slots + per_split - 1) / per_split, std::max<int64_t>(1, steps_max / 8)});
+    e.splits = (int32_t)std::min<int64_t>({(int64_t)split_cap, (slots + per_split - 1) / per_split,
+                                           std::max<int64_t>(1, steps_max / 8)});
   const int64_t rows = (int64_t)num_seqs * max_q_len * g.Hq;  // bounds the (token, query head) rows
-  if (e.splits > 1) {
+  if (e.splits > 1 || e.partial) {
     const uint64_t ml_bytes = ((uint64_t)rows * e.splits * 8 + 255) / 256 * 256;
     const uint64_t need = ml_bytes + (uint64_t)rows * e.splits * g.D * 4;
     if (p->ws_bytes < need) {
@@ -2309,7 +2440,7 @@ extern "C" int mkv_extend_attention(mkv_pool *pool, int32_t layer, const void *d
   void *args[] = {&a, &e};
   MKV_CHECK_HIP(hipLaunchKernel(fn, grid, block, args, 0, hs));
   MKV_CHECK_LAUNCH("attn_extend_kernel");
-  if (e.splits > 1) {
+  if (e.splits > 1 && !e.partial) {
     const dim3 mgrid((unsigned)((rows + 3) / 4));
     switch (g.D) {
       case 64: hipLaunchKernelGGL((merge_ext_kernel<64, true>), mgrid, dim3(256), 0, hs, a, e); break;

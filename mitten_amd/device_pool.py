@@ -441,6 +441,38 @@ class DeviceKvPool:
         p.build(ctx_lens, pieces, stream)
         return p
 
+    def plan_suffixes(self, suffix_lens, pieces: int = 0, stream=None) -> "DecodePlan":
+        """Work plan of a step over a shared prefix, from the host suffix
+        lengths (tokens after the prefix, the appended one included); for
+        decode_step_shared_prefix."""
+        p = DecodePlan(self, suffixes=True)
+        p.build(suffix_lens, pieces, stream)
+        return p
+
+    def decode_step_shared_prefix(self, layer: int, plan, k_new, v_new, q, prefix_ids, block_indptr, block_ids,
+                                  out=None, scale: float | None = None, zero_sink: bool = False,
+                                  kernel: str | None = None, stream=None):
+        """decode_step over a prefix of whole blocks that every sequence of the
+        plan shares (prefix_ids, int32 on the device) followed by each
+        sequence's suffix table (block_indptr / block_ids). k_new / v_new:
+        [B, Hkv, D] appended at suffix position suffix_len - 1, or both None."""
+        d = self.desc
+        if not getattr(plan, "suffixes", False):
+            raise BackendError(MKV_ERR_INVALID_ARGUMENT, "the plan must come from plan_suffixes")
+        out, scale, flags = self._planned_args(plan, q, block_indptr, block_ids, out, scale, zero_sink, kernel)
+        self._i32(prefix_ids, "prefix_ids")
+        B = plan.num_seqs
+        if (k_new is None) != (v_new is None):
+            raise ValueError("give both k_new and v_new, or neither")
+        if k_new is not None:
+            self._check_tensor(k_new, (B, d.num_kv_heads, d.head_dim), "k_new")
+            self._check_tensor(v_new, (B, d.num_kv_heads, d.head_dim), "v_new")
+        _raise(self._lib.mkv_decode_step_shared_prefix(
+            self._h, plan._h, layer, _dptr(k_new) if k_new is not None else None,
+            _dptr(v_new) if v_new is not None else None, _dptr(q), _dptr(out), _dptr(prefix_ids),
+            int(prefix_ids.shape[0]), _dptr(block_indptr), _dptr(block_ids), scale, flags, _stream_handle(stream)))
+        return out
+
     def _planned_args(self, plan, q, block_indptr, block_ids, out, scale, zero_sink, kernel, cached_loads=False):
         d = self.desc
         if plan.pool is not self:
@@ -531,6 +563,39 @@ class DeviceKvPool:
         run.keep_alive = keep
         return run
 
+    def bind_decode_step_shared_prefix(self, plan, k_new, v_new, q, prefix_ids, block_indptr, block_ids, out,
+                                       scale: float | None = None, zero_sink: bool = False, stream=None):
+        """bind_decode_step for decode_step_shared_prefix: validates the
+        buffers of every layer once ([L, B, ...]) and returns `run(layer)`."""
+        d = self.desc
+        if not getattr(plan, "suffixes", False):
+            raise BackendError(MKV_ERR_INVALID_ARGUMENT, "the plan must come from plan_suffixes")
+        L, B = d.num_layers, plan.num_seqs
+        self._check_tensor(k_new, (L, B, d.num_kv_heads, d.head_dim), "k_new")
+        self._check_tensor(v_new, (L, B, d.num_kv_heads, d.head_dim), "v_new")
+        self._check_tensor(q, (L, B, d.num_q_heads, d.head_dim), "q")
+        self._check_tensor(out, (L, B, d.num_q_heads, d.head_dim), "out")
+        self._i32(prefix_ids, "prefix_ids")
+        _, scale, flags = self._planned_args(plan, q[0], block_indptr, block_ids, out[0], scale, zero_sink, None)
+        fn = self._lib.mkv_decode_step_shared_prefix
+        kv_stride = B * d.num_kv_heads * d.head_dim * d.elem_bytes
+        qo_stride = B * d.num_q_heads * d.head_dim * d.elem_bytes
+        kb, vb, qb, ob = k_new.data_ptr(), v_new.data_ptr(), q.data_ptr(), out.data_ptr()
+        pre, npre = _dptr(prefix_ids), int(prefix_ids.shape[0])
+        ip, ix, sh = _dptr(block_indptr), _dptr(block_ids), _stream_handle(stream)
+        args = [(self._h, plan._h, layer, ctypes.c_void_p(kb + layer * kv_stride),
+                 ctypes.c_void_p(vb + layer * kv_stride), ctypes.c_void_p(qb + layer * qo_stride),
+                 ctypes.c_void_p(ob + layer * qo_stride), pre, npre, ip, ix, scale, flags, sh) for layer in range(L)]
+        keep = (k_new, v_new, q, out, prefix_ids, block_indptr, block_ids)
+
+        def run(layer: int) -> None:
+            st = fn(*args[layer])
+            if st:
+                _raise(st)
+
+        run.keep_alive = keep
+        return run
+
     # -- host read-back / upload (tests) ------------------------------------------------------
     def read(self) -> np.ndarray:
         """Copy of the whole pool as numpy (uint16 bit patterns for bf16)."""
@@ -575,9 +640,10 @@ class DecodePlan:
     """Host-built work plan of one decode step (balanced pieces of the batch's
     blocks), reused by every layer of the step."""
 
-    def __init__(self, pool: DeviceKvPool):
+    def __init__(self, pool: DeviceKvPool, suffixes: bool = False):
         self.pool = pool
         self._lib = pool._lib
+        self.suffixes = suffixes  # built over the suffixes of a shared prefix
         h = ctypes.c_void_p()
         _raise(self._lib.mkv_decode_plan_create(pool._h, ctypes.byref(h)))
         self._h = h
@@ -586,7 +652,8 @@ class DecodePlan:
     def build(self, ctx_lens, pieces: int = 0, stream=None) -> None:
         c = np.ascontiguousarray(ctx_lens, np.int32)
         self._ctx = c  # the upload is asynchronous; keep the host copy alive
-        _raise(self._lib.mkv_decode_plan_build(self._h, _i32p(c), c.size, pieces, _stream_handle(stream)))
+        fn = self._lib.mkv_decode_plan_build_suffixes if self.suffixes else self._lib.mkv_decode_plan_build
+        _raise(fn(self._h, _i32p(c), c.size, pieces, _stream_handle(stream)))
         self.num_seqs = int(c.size)
 
     def info(self):
