@@ -312,6 +312,11 @@ class BlockManager(_Handle):
                                       _ptr(ctx, I32P)))
         return indptr, ids[: indptr[-1]].copy(), ctx[: s.size].copy()
 
+    def batch_shared_prefix(self, seqs):
+        """The step's tables split at the blocks every sequence shares: see
+        split_shared_prefix."""
+        return split_shared_prefix(*self.batch(seqs))
+
     def free_blocks(self) -> int:
         return _lib_h().mkvh_bm_free_blocks(self._h)
 
@@ -326,3 +331,30 @@ class BlockManager(_Handle):
 
     def check_invariants(self) -> None:
         _check(_lib_h().mkvh_bm_check_invariants(self._h))
+
+
+def split_shared_prefix(block_indptr, block_ids, ctx_lens):
+    """Splits a step's block tables at the longest run of leading block ids
+    that every table holds (radix sharing hands the same pages to each
+    request that matched a prefix, inference-engine/src/radix_cache.rs:64-117),
+    limited to pages that are full before each sequence's last token.
+    Returns (prefix_ids int32[n], suffix_indptr int32[B+1], suffix_ids int32,
+    suffix_lens int32[B]) for DeviceKvPool.plan_suffixes and
+    decode_step_shared_prefix; n = 0 when nothing is shared."""
+    ip = np.asarray(block_indptr, np.int64)
+    ids = np.asarray(block_ids, np.int32)
+    ctx = np.asarray(ctx_lens, np.int64)
+    B = ctx.size
+    lens = ip[1:] - ip[:-1]
+    limit = int(min(((ctx - 1) // 16).min(), lens.min())) if B else 0
+    n = 0
+    if limit > 0:
+        lead = ids[ip[:-1, None] + np.arange(limit)[None, :]]  # [B, limit] leading ids
+        same = (lead == lead[0]).all(axis=0)
+        n = limit if same.all() else int(np.argmin(same))
+    suffix_indptr = (ip - n * np.arange(B + 1)).astype(np.int32)
+    keep = np.ones(ids.size, bool)
+    for b in range(B):
+        keep[ip[b]:ip[b] + n] = False
+    return (ids[ip[0]:ip[0] + n].copy() if B else ids[:0].copy(), suffix_indptr, ids[keep],
+            (ctx - 16 * n).astype(np.int32))

@@ -8,8 +8,10 @@ gathers; within the attention tolerances for decode attention).
 * C4, radix sharing at Qwen-7B head shapes (2 of 28 layers): 256 sequences
   fork one 4,100-token prefix (256 full blocks + a 4-token partial block),
   copy-on-write of the shared partial block on the first append (255 copies,
-  the last holder writes in place), suffixes, decode steps, then 20% of the
-  sequences finish and the pool is compacted by batched block moves.
+  the last holder writes in place), suffixes, decode steps, the
+  shared-prefix step over the block manager's tables (equal to the plain
+  attention), then 20% of the sequences finish and the pool is compacted by
+  batched block moves.
 * C5, pool pressure at Qwen-7B head shapes (1 of 28 layers): the
   217,982-block pool of a 200 GB budget, 512 sequences with log-normal
   lengths (median 2,048, sigma 1, capped at 32,768); per step 8 sequences
@@ -198,6 +200,24 @@ def test_c4_radix_sharing_cow_decode_and_compaction():
             plan.close()
         pool.check()
         assert np.array_equal(bits(pool.read()), bits(want))
+        # The shared-prefix step over the same tables: the prefix's 256 full
+        # pages (the partial one was copied on write) read once for all 256
+        # sequences, then each suffix; equal to the plain planned attention.
+        indptr, ids, ctx = bm.batch(seqs)
+        pre, s_ptr, s_ids, s_len = bm.batch_shared_prefix(seqs)
+        assert pre.size == prefix_blocks - 1 and np.array_equal(pre, shared[:-1])
+        q = normal(550, (C4_SEQS, Hq, D), "bf16")
+        plan = pool.plan(ctx)
+        o_full = to_host(pool.decode_attention_planned(1, plan, to_device(q), _i32(indptr), _i32(ids)))
+        plan.close()
+        splan = pool.plan_suffixes(s_len)
+        o_sp = to_host(pool.decode_step_shared_prefix(1, splan, None, None, to_device(q), _i32(pre), _i32(s_ptr),
+                                                      _i32(s_ids)))
+        splan.close()
+        pool.check()
+        assert_attention_close(o_sp, widen(o_full), "bf16")
+        sp_, si_, sc_ = _sub_batch(indptr, ids, ctx, sample)
+        assert_attention_close(o_sp[sample], orc.decode_attention(od, want, 1, widen(q[sample]), sp_, si_, sc_), "bf16")
         # 20% of the sequences finish; compaction moves tail blocks into the holes.
         done = seqs[::5]
         live = [s for s in seqs if s not in done]

@@ -341,3 +341,40 @@ def test_random_lifecycle_keeps_invariants():
         bm.check_invariants()
     bm.plan_compaction()
     bm.check_invariants()
+
+
+def test_split_shared_prefix_tables():
+    from mitten_amd.host import split_shared_prefix
+
+    # three tables sharing blocks 7, 8, 9; the third diverges at its 4th block
+    ip = np.array([0, 5, 10, 14], np.int32)
+    ids = np.array([7, 8, 9, 1, 2, 7, 8, 9, 1, 3, 7, 8, 9, 4], np.int32)
+    ctx = np.array([70, 80, 60], np.int32)
+    pre, sp, si, sl = split_shared_prefix(ip, ids, ctx)
+    assert pre.tolist() == [7, 8, 9]
+    assert sp.tolist() == [0, 2, 4, 5] and si.tolist() == [1, 2, 1, 3, 4] and sl.tolist() == [22, 32, 12]
+    # a sequence whose last token sits in a shared block caps the prefix
+    pre, sp, si, sl = split_shared_prefix(ip, ids, np.array([70, 80, 48], np.int32))
+    assert pre.tolist() == [7, 8] and sl.tolist() == [38, 48, 16]
+    # nothing shared
+    pre, sp, si, sl = split_shared_prefix(np.array([0, 1, 2], np.int32), np.array([5, 6], np.int32),
+                                          np.array([3, 4], np.int32))
+    assert pre.size == 0 and si.tolist() == [5, 6] and sl.tolist() == [3, 4]
+
+
+def test_block_manager_shared_prefix_after_fork():
+    """Forked sequences share the prefix's full pages (refcounted); the
+    split puts exactly those in the prefix and every suffix starts with the
+    sequence's own pages."""
+    bm = BlockManager(64)
+    assert bm.admit(0, np.arange(100, dtype=np.uint32)) == 0
+    bm.append(0, 100)  # 6 full pages + 4 tokens
+    for s in (1, 2):
+        bm.fork(0, s)
+    for s in (0, 1, 2):
+        bm.append(s, 5 + s)  # COW of the partial page for all but its last holder
+    pre, sp, si, sl = bm.batch_shared_prefix([0, 1, 2])
+    assert pre.tolist() == list(bm.table(0)[:6]) and all(bm.refcount(int(b)) == 3 for b in pre)
+    assert sl.tolist() == [100 + 5 - 96, 100 + 6 - 96, 100 + 7 - 96]
+    own = [si[sp[b]:sp[b + 1]] for b in range(3)]
+    assert len({int(o[0]) for o in own}) == 3  # each sequence's own copy of the partial page
