@@ -1486,10 +1486,11 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
       // With two sub-tiles (one 16-wave workgroup per CU) the score MFMAs
       // issue at raised wave priority, so a wave that reaches them overtakes
       // the waves busy with exponentials and the matrix pipe stays fed
-      // (8 x 512 after 4k: 455 -> 435-445 us). The same around the PV
-      // products gained nothing, and with one sub-tile (two workgroups per
-      // CU) it cost 16-token chunks 15%.
-      if constexpr (TP == 2) __builtin_amdgcn_s_setprio(1);
+      // (8 x 512 after 4k: 455 -> 435-445 us at priority 1, about 1% more
+      // at 3). The same around the PV products or the load issue gained
+      // nothing, and with one sub-tile (two workgroups per CU) it cost
+      // 16-token chunks 15%.
+      if constexpr (TP == 2) __builtin_amdgcn_s_setprio(3);
 #pragma unroll
       for (int r = 0; r < NR; r++)
         S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kq[r]), qop[r], S, 0, 0, 0);
