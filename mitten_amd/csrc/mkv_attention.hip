@@ -1483,18 +1483,19 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
 #pragma unroll
       for (int r = 0; r < NR; r++) kq[r] = *reinterpret_cast<const u32x4 *>(tk + k_rd[r]);
       f32x4 S = {0.f, 0.f, 0.f, 0.f};
-      // With two sub-tiles (one 16-wave workgroup per CU) the score MFMAs
-      // issue at raised wave priority, so a wave that reaches them overtakes
-      // the waves busy with exponentials and the matrix pipe stays fed
-      // (8 x 512 after 4k: 455 -> 435-445 us at priority 1, about 1% more
-      // at 3). The same around the PV products or the load issue gained
-      // nothing, and with one sub-tile (two workgroups per CU) it cost
-      // 16-token chunks 15%.
-      if constexpr (TP == 2) __builtin_amdgcn_s_setprio(3);
+      // Where one workgroup fills a CU (two sub-tiles, or head_dim 256) the
+      // score MFMAs issue at raised wave priority, so a wave that reaches
+      // them overtakes the waves busy with exponentials and the matrix pipe
+      // stays fed (8 x 512 after 4k: 455 -> 435-445 us at priority 1, about
+      // 1% more at 3; head_dim 256: 259 -> 255 us). The same around the PV
+      // products or the load issue gained nothing, and with one sub-tile at
+      // head_dim <= 128 (two workgroups per CU) it cost 16-token chunks 15%.
+      constexpr bool kPrio = TP == 2 || D == 256;
+      if constexpr (kPrio) __builtin_amdgcn_s_setprio(3);
 #pragma unroll
       for (int r = 0; r < NR; r++)
         S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kq[r]), qop[r], S, 0, 0, 0);
-      if constexpr (TP == 2) __builtin_amdgcn_s_setprio(0);
+      if constexpr (kPrio) __builtin_amdgcn_s_setprio(0);
       const bool kbad = (bad >> kb) & 1;
       const bool full = !kbad && kPageSize * k + kPageSize - 1 <= qlo && kPageSize * k + kPageSize <= ctx;
 #pragma unroll
