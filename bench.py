@@ -588,13 +588,14 @@ def _decode_step_run(pool, plan, batch, L, Hq, Hkv, D, seed, dev, stream, pre_la
     kn = torch.randn((L, B, Hkv, D), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
     vn = torch.randn((L, B, Hkv, D), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
     out = torch.empty_like(q)
-    i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(dev)
-    indptr, ids = i32(batch.block_indptr), i32(batch.block_ids)
-    run_layer = pool.bind_decode_step(plan, kn, vn, q, indptr, ids, out, stream=stream, cached_loads=cached_loads)
+    ip, ix = batch.block_indptr.astype(np.uint32), batch.block_ids.astype(np.uint32)
     ctx_host = batch.ctx_lens.copy()
+    plan.build(ctx_host, 0, stream=stream, block_indptr=ip, block_ids=ix)
+    run_layer = pool.bind_decode_step(plan, kn, vn, q, None, None, out, stream=stream, cached_loads=cached_loads)
 
     def step():
-        plan.build(ctx_host, 0, stream=stream)
+        # The engine's per-step call: host page tables (u32 CSR) into the plan.
+        plan.build(ctx_host, 0, stream=stream, block_indptr=ip, block_ids=ix)
         for layer in range(L):
             if pre_layer is not None:
                 pre_layer(layer)
@@ -906,15 +907,18 @@ def main():
     launch_bytes = attn_bytes + (app_bytes if args.mode == "step" else 0)
 
     ctx_host = batch.ctx_lens.copy()
-    plan = pool.plan(ctx_host, pieces=args.pieces, stream=stream)
+    ip_h, ids_h = batch.block_indptr.astype(np.uint32), batch.block_ids.astype(np.uint32)
+    plan = pool.plan(ctx_host, pieces=args.pieces, stream=stream, block_indptr=ip_h, block_ids=ids_h)
 
-    run_layer = pool.bind_decode_step(plan, k_new, v_new, q, indptr, ids, out, kernel=kernel, stream=stream)
+    run_layer = pool.bind_decode_step(plan, k_new, v_new, q, None, None, out, kernel=kernel, stream=stream)
 
     def step(events=None):
         """events: None, or L+1 timing events recorded between launches (the
         fused step has nothing else between consecutive layers)."""
         if args.mode != "split":
-            plan.build(ctx_host, args.pieces, stream=stream)  # host plan of this step
+            # The engine's one call per step: host lengths and host page
+            # tables (u32 CSR), validated, copied and uploaded with the plan.
+            plan.build(ctx_host, args.pieces, stream=stream, block_indptr=ip_h, block_ids=ids_h)
         for layer in range(L):
             if args.mode != "step":
                 pool.append(layer, k_new[layer], v_new[layer], slots, stream=stream)
@@ -923,7 +927,7 @@ def main():
             if args.mode == "step":
                 run_layer(layer)
             elif args.mode == "planned":
-                pool.decode_attention_planned(layer, plan, q[layer], indptr, ids, out=out[layer],
+                pool.decode_attention_planned(layer, plan, q[layer], None, None, out=out[layer],
                                               kernel=kernel, stream=stream)
             else:
                 pool.decode_attention(layer, q[layer], indptr, ids, ctx, max_ctx, out=out[layer],

@@ -22,9 +22,20 @@
  *   - Every function returns an mkv_status (0 = MKV_OK). On failure a message
  *     is available from mkv_last_error() (thread-local). No C++ exception and
  *     no abort crosses this boundary.
- *   - Pointers named d_* are device pointers (HBM), 16-byte aligned. Metadata
- *     arrays (slot mappings, block tables, context lengths) are device int32.
- *     The mkv_validate_* functions check the same arrays on the host.
+ *   - Pointers named d_* are device pointers (HBM), 16-byte aligned; h_* are
+ *     host pointers. Metadata comes in two forms:
+ *       * host arrays in the engine's own form (the *_host entry points and
+ *         mkv_decode_plan_build_tables): page ids are u32 (PageIndex,
+ *         inference-engine/src/request.rs:6), a batch's page tables
+ *         (Vec<Vec<u32>>, inference-backend/src/batch.rs:24-26) are passed
+ *         as a CSR pair u32 indptr[B+1] / ids[indptr[B]]. They are validated
+ *         on the host (a bad id returns MKV_ERR_INVALID_ARGUMENT and nothing
+ *         is launched) and copied before the call returns: the caller keeps
+ *         ownership and may reuse the arrays at once. The library uploads
+ *         them on `stream` ahead of the launch;
+ *       * device int32 arrays (the other entry points), read by the kernels
+ *         when they run. The mkv_validate_* functions check such arrays on
+ *         the host.
  *   - Kernels bound-check every slot and block id they dereference against
  *     the pool; an out-of-range id is skipped (never dereferenced) and
  *     recorded in the pool's device error word, read by mkv_pool_check().
@@ -191,6 +202,49 @@ MKV_API int mkv_decode_attention_workspace_size(const mkv_pool *pool, int32_t nu
                                         int32_t max_ctx_len, int32_t split_tokens,
                                         uint64_t *out_bytes);
 
+/* ---- host metadata (the engine's u32 form) ------------------------------- */
+
+/* mkv_append with a host slot mapping (slot = page * page_size + offset, as
+ * the engine derives it from kv_pages: prefill.rs:72-81, scheduler.rs:42-57). */
+MKV_API int mkv_append_host(mkv_pool *pool, int32_t layer, const void *d_k, const void *d_v,
+                            const uint32_t *h_slot_mapping, int32_t num_tokens, void *stream);
+/* mkv_append_all_layers with a host slot mapping. */
+MKV_API int mkv_append_all_layers_host(mkv_pool *pool, const void *d_k, const void *d_v,
+                                       const uint32_t *h_slot_mapping, int32_t num_tokens, void *stream);
+/* mkv_gather with host tables: sequence b's first h_ctx_lens[b] tokens
+ * through table h_block_ids[h_block_indptr[b] ..), written at element offset
+ * (sum of the earlier h_ctx_lens) * Hkv * D of the outputs. */
+MKV_API int mkv_gather_host(mkv_pool *pool, int32_t layer, const uint32_t *h_block_indptr,
+                            const uint32_t *h_block_ids, const int32_t *h_ctx_lens, int32_t num_seqs,
+                            void *d_out_k, void *d_out_v, int64_t out_capacity_tokens, void *stream);
+/* mkv_copy_blocks with host pairs; the pairs are checked as
+ * mkv_validate_copy_pairs does (distinct destinations, no block both a
+ * source and a destination) before anything is launched. */
+MKV_API int mkv_copy_blocks_host(mkv_pool *pool, const uint32_t *h_src_blocks, const uint32_t *h_dst_blocks,
+                                 int32_t num_pairs, void *stream);
+/* mkv_extend_attention with host metadata: sequence b has h_q_lens[b] new
+ * tokens (its extend_len, request.rs:46-54; 0 <= q_len <= ctx) whose query
+ * rows follow those of sequence b-1 in d_q / d_o, and h_ctx_lens[b] tokens
+ * in its table (the chunk included). */
+MKV_API int mkv_extend_attention_host(mkv_pool *pool, int32_t layer, const void *d_q, void *d_o,
+                                      const int32_t *h_q_lens, const int32_t *h_ctx_lens,
+                                      const uint32_t *h_block_indptr, const uint32_t *h_block_ids,
+                                      int32_t num_seqs, float scale, uint32_t flags, void *stream);
+/* mkv_qk_norm_rope_append with host positions and slots. */
+MKV_API int mkv_qk_norm_rope_append_host(mkv_pool *pool, int32_t layer, const void *d_q, const void *d_k,
+                                         const void *d_v, const float *d_q_norm_w, const float *d_k_norm_w,
+                                         const float *d_inv_freq, int32_t rotary_dim, float eps,
+                                         const int32_t *h_positions, const uint32_t *h_slot_mapping,
+                                         int32_t num_tokens, void *d_q_out, uint32_t flags, void *stream);
+/* mkv_wire_export / mkv_wire_import with host block ids; the import's
+ * destinations must be distinct (checked). */
+MKV_API int mkv_wire_export_host(mkv_pool *pool, const uint32_t *h_block_ids, int32_t num_blocks,
+                                 int32_t layer_begin, int32_t num_layers, void *d_payload, uint64_t *d_checksums,
+                                 void *stream);
+MKV_API int mkv_wire_import_host(mkv_pool *pool, const uint32_t *h_block_ids, int32_t num_blocks,
+                                 int32_t layer_begin, int32_t num_layers, const void *d_payload,
+                                 const uint64_t *d_expected, uint64_t *d_checksums, void *stream);
+
 /* ---- planned decode (production path) ----------------------------------- */
 
 /* A decode plan is the work decomposition of one engine step, built on the
@@ -205,12 +259,26 @@ typedef struct mkv_decode_plan mkv_decode_plan;
 MKV_API int mkv_decode_plan_create(mkv_pool *pool, mkv_decode_plan **out_plan);
 MKV_API int mkv_decode_plan_destroy(mkv_decode_plan *plan);
 /* h_ctx_lens: host array, tokens each sequence attends (>= 1).
- * pieces: 0 = chosen by the library. Uploads asynchronously on `stream`. */
+ * pieces: 0 = chosen by the library. Uploads asynchronously on `stream`.
+ * A plan built this way has no tables: its decode calls pass device tables. */
 MKV_API int mkv_decode_plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens,
                                   int32_t num_seqs, int32_t pieces, void *stream);
+/* The engine's one call per step: mkv_decode_plan_build plus the batch's
+ * page tables as host CSR (u32 indptr[num_seqs+1], u32 ids), validated
+ * against the pool and copied into the plan (uploaded on `stream` with the
+ * plan). The step's decode calls then pass NULL tables and read the plan's.
+ * A later build replaces the tables; the calls already enqueued keep the
+ * ones they were enqueued with only if they run first on the same stream,
+ * so rebuild a plan on the stream that uses it. */
+MKV_API int mkv_decode_plan_build_tables(mkv_decode_plan *plan, const int32_t *h_ctx_lens,
+                                         const uint32_t *h_block_indptr, const uint32_t *h_block_ids,
+                                         int32_t num_seqs, int32_t pieces, void *stream);
 MKV_API int mkv_decode_plan_info(const mkv_decode_plan *plan, int32_t *out_pieces,
                                  int32_t *out_blocks_per_piece, int32_t *out_merge_seqs);
-/* mkv_decode_attention over the plan's sequences and context lengths. */
+/* mkv_decode_attention over the plan's sequences and context lengths.
+ * Tables: d_block_indptr / d_block_ids (device, read on every call, so a
+ * table rewritten in place between calls is seen by the next one), or both
+ * NULL for the tables given to mkv_decode_plan_build_tables. */
 MKV_API int mkv_decode_attention_planned(mkv_pool *pool, const mkv_decode_plan *plan,
                                          int32_t layer, const void *d_q, void *d_o,
                                          const int32_t *d_block_indptr,
@@ -220,7 +288,8 @@ MKV_API int mkv_decode_attention_planned(mkv_pool *pool, const mkv_decode_plan *
  * d_k_new[b], d_v_new[b] ([num_seqs][num_kv_heads][head_dim]) at position
  * ctx_b - 1 (its slot from its block table), then attend over ctx_b tokens.
  * Equal to mkv_append at those slots followed by
- * mkv_decode_attention_planned. Replaces model.rs:390-416 for one layer. */
+ * mkv_decode_attention_planned (tables as there: device, or both NULL for
+ * the plan's). Replaces model.rs:390-416 for one layer. */
 MKV_API int mkv_decode_step(mkv_pool *pool, const mkv_decode_plan *plan, int32_t layer,
                             const void *d_k_new, const void *d_v_new, const void *d_q, void *d_o,
                             const int32_t *d_block_indptr, const int32_t *d_block_ids,
@@ -241,9 +310,13 @@ MKV_API int mkv_decode_step(mkv_pool *pool, const mkv_decode_plan *plan, int32_t
  * lengths (>= 1: the appended token is in the suffix). A plan built this way
  * stores every sequence's result as partials for the step below.
  *
+ * mkv_decode_plan_build_shared_prefix: the same with the host tables of the
+ * suffixes and the prefix's u32 block ids, copied into the plan.
+ *
  * mkv_decode_step_shared_prefix: mkv_decode_step over prefix + suffix.
- * d_prefix_ids: the prefix's prefix_blocks block ids (device). The tables
- * d_block_indptr / d_block_ids hold each sequence's suffix blocks only;
+ * d_prefix_ids: the prefix's prefix_blocks block ids (device), or NULL for
+ * the plan's. The tables d_block_indptr / d_block_ids (device, or both NULL
+ * for the plan's) hold each sequence's suffix blocks only;
  * d_k_new / d_v_new (both or neither) go at suffix position suffix_len_b - 1.
  * Three launches: the prefix over all queries (f32 partials per key range in
  * the pool-owned workspace, grown on demand as for mkv_extend_attention),
@@ -253,6 +326,10 @@ MKV_API int mkv_decode_step(mkv_pool *pool, const mkv_decode_plan *plan, int32_t
  * tolerance (the partials merge in another order). Flags: MKV_ATTN_ZERO_SINK. */
 MKV_API int mkv_decode_plan_build_suffixes(mkv_decode_plan *plan, const int32_t *h_suffix_lens,
                                            int32_t num_seqs, int32_t pieces, void *stream);
+MKV_API int mkv_decode_plan_build_shared_prefix(mkv_decode_plan *plan, const uint32_t *h_prefix_ids,
+                                                int32_t prefix_blocks, const int32_t *h_suffix_lens,
+                                                const uint32_t *h_block_indptr, const uint32_t *h_block_ids,
+                                                int32_t num_seqs, int32_t pieces, void *stream);
 MKV_API int mkv_decode_step_shared_prefix(mkv_pool *pool, const mkv_decode_plan *plan,
                                           int32_t layer, const void *d_k_new, const void *d_v_new,
                                           const void *d_q, void *d_o, const int32_t *d_prefix_ids,

@@ -125,11 +125,14 @@ MKVH_API int mkvh_bm_admit(mkvh_block_manager *bm, uint64_t seq, const uint32_t 
  * a partly filled last block: parallel sampling / forked decoding. */
 MKVH_API int mkvh_bm_fork(mkvh_block_manager *bm, uint64_t parent, uint64_t child);
 /* Slots for n_new tokens at positions [len, len + n_new): a block is
- * allocated whenever a position starts one (decode-time growth), and if the
- * block about to be written is shared (refcount > 1) it is first copied to a
- * private block — the pair is returned in (cow_src, cow_dst) (0 or 1 pairs)
- * and must run (mkv_copy_blocks) before the append. The last holder of a
- * shared block writes in place. */
+ * allocated whenever a position starts one (decode-time growth). Every block
+ * in the written range that is shared (refcount > 1: a fork, including one
+ * made before the prompt was written) is replaced by a private block first.
+ * Only the block holding position len, when it already holds rows of this
+ * sequence (len % page_size != 0), needs its contents: that pair is
+ * returned in (cow_src, cow_dst) (0 or 1 pairs; required outputs when it
+ * occurs) and must run (mkv_copy_blocks) before the append. The last holder
+ * of a shared block writes in place. */
 MKVH_API int mkvh_bm_append(mkvh_block_manager *bm, uint64_t seq, int32_t n_new, int32_t *out_slots,
                             int32_t *out_cow_src, int32_t *out_cow_dst, int32_t *out_n_cow);
 /* Prefill complete (scheduler.rs:117): full pages enter the tree; the tree
@@ -143,7 +146,9 @@ MKVH_API int mkvh_bm_release(mkvh_block_manager *bm, uint64_t seq);
 MKVH_API int mkvh_bm_evict(mkvh_block_manager *bm, int64_t target_pages, int64_t *out_freed_blocks);
 /* Compaction plan: every live block with id >= live_count moves to a free id
  * below live_count; block tables and tree pages are rewritten. Returns the
- * moves for mkv_copy_blocks (sources and destinations are disjoint). */
+ * moves for mkv_copy_blocks (sources and destinations are disjoint).
+ * out_src / out_dst (capacity cap) are required whenever a move is needed:
+ * otherwise nothing changes and MKVH_ERR_INVALID_ARGUMENT is returned. */
 MKVH_API int mkvh_bm_plan_compaction(mkvh_block_manager *bm, int32_t *out_src, int32_t *out_dst,
                                      int64_t cap, int64_t *out_n);
 MKVH_API int mkvh_bm_seq_len(const mkvh_block_manager *bm, uint64_t seq, int64_t *out_len);

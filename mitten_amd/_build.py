@@ -54,18 +54,27 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print(out)
 
 
-def device_cmd(out: str = DEVICE_LIB, extra: list[str] | None = None) -> list[str]:
-    hipcc = shutil.which("hipcc") or os.path.join(_rocm(), "bin", "hipcc")
+def _hipcc() -> str:
+    return shutil.which("hipcc") or os.path.join(_rocm(), "bin", "hipcc")
+
+
+# Packed FP32 (v_pk_*_f32) stays off for all device code.
+_DEVICE_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden", "-Wall",
+                 "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def device_obj_cmd(src: str, obj: str, extra: list[str] | None = None) -> list[str]:
+    """One translation unit of the device library -> object (host code plus
+    its embedded gfx950 code object)."""
+    return ([_hipcc(), f"--offload-arch={ARCH}"] + _DEVICE_FLAGS + [f"-I{INCLUDE}"] + (extra or []) +
+            ["-c", os.path.join(CSRC, src), "-o", obj])
+
+
+def device_link_cmd(objs: list[str], out: str = DEVICE_LIB) -> list[str]:
     rpaths = [p for p in (_torch_libdir(), os.path.join(_rocm(), "lib")) if p]
-    cmd = [hipcc, f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
-           "-fvisibility=hidden", "-Wall",
-           # Packed FP32 (v_pk_*_f32) stays off for all device code.
-           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-           f"-I{INCLUDE}"]
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC"]
     cmd += [f"-Wl,-rpath,{p}" for p in rpaths]
-    cmd += extra or []
-    cmd += [os.path.join(CSRC, s) for s in DEVICE_SOURCES] + ["-o", out]
-    return cmd
+    return cmd + objs + ["-o", out]
 
 
 def host_cmd(out: str = HOST_LIB, extra: list[str] | None = None) -> list[str]:
@@ -78,14 +87,25 @@ def host_cmd(out: str = HOST_LIB, extra: list[str] | None = None) -> list[str]:
 
 
 def build(verbose: bool = False) -> None:
-    """Compile both libraries (always recompiles)."""
+    """Compile both libraries (always recompiles). The device sources compile
+    in parallel, one hipcc per file, and are linked into one library."""
+    import tempfile
+    from concurrent.futures import ThreadPoolExecutor
+
     os.makedirs(LIBDIR, exist_ok=True)
-    jobs = [(device_cmd(DEVICE_LIB + ".tmp"), DEVICE_LIB)]
-    if all(os.path.exists(os.path.join(CSRC, s)) for s in HOST_SOURCES):
-        jobs.insert(0, (host_cmd(HOST_LIB + ".tmp"), HOST_LIB))
-    for cmd, out in jobs:
-        _run(cmd, verbose)
-        os.replace(out + ".tmp", out)
+    with tempfile.TemporaryDirectory(prefix="mkv_build_") as tmp:
+        objs = [os.path.join(tmp, os.path.splitext(os.path.basename(s))[0] + ".o") for s in DEVICE_SOURCES]
+        cmds = [device_obj_cmd(s, o) for s, o in zip(DEVICE_SOURCES, objs)]
+        have_host = all(os.path.exists(os.path.join(CSRC, s)) for s in HOST_SOURCES)
+        if have_host:
+            cmds.append(host_cmd(HOST_LIB + ".tmp"))
+        with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
+            for f in [ex.submit(_run, c, verbose) for c in cmds]:
+                f.result()
+        _run(device_link_cmd(objs, DEVICE_LIB + ".tmp"), verbose)
+    os.replace(DEVICE_LIB + ".tmp", DEVICE_LIB)
+    if have_host:
+        os.replace(HOST_LIB + ".tmp", HOST_LIB)
 
 
 if __name__ == "__main__":

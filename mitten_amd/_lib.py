@@ -52,6 +52,7 @@ class WireHeaderC(ctypes.Structure):
 DESC_P = ctypes.POINTER(PoolDescC)
 WIRE_P = ctypes.POINTER(WireHeaderC)
 I32P = ctypes.POINTER(i32)
+U32P = ctypes.POINTER(u32)
 
 DEVICE_SIGNATURES = {
     "mkv_pool_required_bytes": (c_int, [DESC_P, ctypes.POINTER(u64)]),
@@ -80,6 +81,16 @@ DEVICE_SIGNATURES = {
     "mkv_wire_import": (c_int, [P, P, i32, i32, i32, P, P, P, P]),
     "mkv_wire_header_init": (c_int, [DESC_P, i32, i32, i32, i64, WIRE_P]),
     "mkv_wire_header_check": (c_int, [DESC_P, WIRE_P]),
+    "mkv_append_host": (c_int, [P, i32, P, P, U32P, i32, P]),
+    "mkv_append_all_layers_host": (c_int, [P, P, P, U32P, i32, P]),
+    "mkv_gather_host": (c_int, [P, i32, U32P, U32P, I32P, i32, P, P, i64, P]),
+    "mkv_copy_blocks_host": (c_int, [P, U32P, U32P, i32, P]),
+    "mkv_extend_attention_host": (c_int, [P, i32, P, P, I32P, I32P, U32P, U32P, i32, f32, u32, P]),
+    "mkv_qk_norm_rope_append_host": (c_int, [P, i32, P, P, P, P, P, P, i32, f32, I32P, U32P, i32, P, u32, P]),
+    "mkv_wire_export_host": (c_int, [P, U32P, i32, i32, i32, P, P, P]),
+    "mkv_wire_import_host": (c_int, [P, U32P, i32, i32, i32, P, P, P, P]),
+    "mkv_decode_plan_build_tables": (c_int, [P, I32P, U32P, U32P, i32, i32, P]),
+    "mkv_decode_plan_build_shared_prefix": (c_int, [P, U32P, i32, I32P, U32P, U32P, i32, i32, P]),
     "mkv_validate_slots": (c_int, [DESC_P, I32P, i32]),
     "mkv_validate_block_tables": (c_int, [DESC_P, I32P, I32P, I32P, i32, i32]),
     "mkv_validate_copy_pairs": (c_int, [DESC_P, I32P, I32P, i32]),
@@ -118,9 +129,7 @@ def device_lib():
             import torch  # noqa: F401
         except ImportError:
             pass
-        # MITTEN_KV_LIBRARY selects another build of the same library
-        # (for example a variant compiled with other tuning constants).
-        _device = _load(os.environ.get("MITTEN_KV_LIBRARY", _build.DEVICE_LIB), DEVICE_SIGNATURES)
+        _device = _load(_build.DEVICE_LIB, DEVICE_SIGNATURES)
     return _device
 
 

@@ -597,25 +597,36 @@ int mkvh_bm_append(mkvh_block_manager *bm, uint64_t seq, int32_t n_new, int32_t 
   const int64_t ps = m->ps;
   const int64_t end = s.len + n_new;
   const int64_t grow = std::max<int64_t>(0, (end + ps - 1) / ps - (int64_t)s.blocks.size());
+  // Every block this append writes that another holder shares (a fork, or
+  // blocks reserved at admission and shared before they were written) gets
+  // a private block first. Only the block holding position len with rows
+  // already written (len % ps != 0) needs its contents copied: the others
+  // hold none of this sequence's rows yet.
   const int64_t j0 = s.len / ps;
-  const bool cow = n_new > 0 && j0 < (int64_t)s.blocks.size() && m->pool.refcnt[s.blocks[j0]] > 1;
-  const int64_t need = grow + (cow ? 1 : 0);
+  const int64_t j_end = n_new > 0 ? std::min<int64_t>((end + ps - 1) / ps, (int64_t)s.blocks.size()) : j0;
+  std::vector<int64_t> shared;
+  for (int64_t j = j0; j < j_end; j++)
+    if (m->pool.refcnt[s.blocks[j]] > 1) shared.push_back(j);
+  const bool copy_needed = !shared.empty() && shared[0] == j0 && s.len % ps != 0;
+  if (copy_needed && !(out_cow_src && out_cow_dst))
+    return fail(MKVH_ERR_INVALID_ARGUMENT, "append writes a shared partial block: pass the copy-pair outputs");
+  const int64_t need = grow + (int64_t)shared.size();
   m->make_room(need);
   if ((int64_t)m->pool.free_stack.size() < need)
     return fail(MKVH_ERR_EXHAUSTED, "append needs %lld blocks, %zu free", (long long)need, m->pool.free_stack.size());
   *out_n_cow = 0;
-  if (cow) {
+  for (int64_t j : shared) {
     uint32_t fresh;
     m->pool.allocate(seq, &fresh);
-    const uint32_t old = s.blocks[j0];
+    const uint32_t old = s.blocks[j];
     bool freed = false;
     m->pool.release(old, &freed);
-    s.blocks[j0] = fresh;
-    if (out_cow_src && out_cow_dst) {
+    s.blocks[j] = fresh;
+    if (j * ps < s.len) {  // rows [j*ps, len) of this block are written: copy them
       out_cow_src[0] = (int32_t)old;
       out_cow_dst[0] = (int32_t)fresh;
+      *out_n_cow = 1;
     }
-    *out_n_cow = 1;
   }
   for (int64_t p = s.len; p < end; p++) {
     if (p / ps == (int64_t)s.blocks.size()) {
@@ -686,6 +697,8 @@ int mkvh_bm_plan_compaction(mkvh_block_manager *bm, int32_t *out_src, int32_t *o
     if (pool.in_use[b]) movers.push_back((uint32_t)b);
   if ((int64_t)movers.size() > cap)
     return fail(MKVH_ERR_BUFFER_TOO_SMALL, "compaction needs room for %zu moves", movers.size());
+  if (!movers.empty() && !(out_src && out_dst))
+    return fail(MKVH_ERR_INVALID_ARGUMENT, "compaction moves %zu blocks: pass out_src and out_dst", movers.size());
   std::vector<int64_t> remap(N, -1);
   for (size_t i = 0; i < movers.size(); i++) {
     const uint32_t s = movers[i], d = holes[i];
@@ -696,10 +709,8 @@ int mkvh_bm_plan_compaction(mkvh_block_manager *bm, int32_t *out_src, int32_t *o
     pool.in_use[s] = 0;
     pool.refcnt[s] = 0;
     pool.owner[s] = 0;
-    if (out_src && out_dst) {
-      out_src[i] = (int32_t)s;
-      out_dst[i] = (int32_t)d;
-    }
+    out_src[i] = (int32_t)s;
+    out_dst[i] = (int32_t)d;
   }
   for (auto &kv : m->seqs)
     for (uint32_t &b : kv.second.blocks)

@@ -34,6 +34,7 @@
 //     agent-scope release/acquire per piece, which measured slower).
 #include <algorithm>
 #include <cmath>
+#include <cstring>
 #include <new>
 #include <vector>
 
@@ -1483,14 +1484,14 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
 #pragma unroll
       for (int r = 0; r < NR; r++) kq[r] = *reinterpret_cast<const u32x4 *>(tk + k_rd[r]);
       f32x4 S = {0.f, 0.f, 0.f, 0.f};
-      // Where one workgroup fills a CU (two sub-tiles, or head_dim 256) the
-      // score MFMAs issue at raised wave priority, so a wave that reaches
-      // them overtakes the waves busy with exponentials and the matrix pipe
-      // stays fed (8 x 512 after 4k: 455 -> 435-445 us at priority 1, about
+      // Where one workgroup fills a CU (two sub-tiles, or head_dim 256 with
+      // 8 or more waves) the score MFMAs issue at raised wave priority, so a
+      // wave that reaches them overtakes the waves busy with exponentials
+      // and the matrix pipe stays fed (8 x 512 after 4k: 455 -> 435-445 us at priority 1, about
       // 1% more at 3; head_dim 256: 259 -> 255 us). The same around the PV
       // products or the load issue gained nothing, and with one sub-tile at
       // head_dim <= 128 (two workgroups per CU) it cost 16-token chunks 15%.
-      constexpr bool kPrio = TP == 2 || D == 256;
+      constexpr bool kPrio = TP == 2 || (D == 256 && W >= 8);
       if constexpr (kPrio) __builtin_amdgcn_s_setprio(3);
 #pragma unroll
       for (int r = 0; r < NR; r++)
@@ -1753,7 +1754,8 @@ struct Plan {
   int32_t B = 0, P = 0, BP = 0, total = 0, n_merge = 0;
   int32_t *d_meta = nullptr;  // ctx[B] | seq_blk0[B+1] | piece_f0[P+1] | piece_seq[P] |
                               // seq_piece0[B] | seq_npiece[B] | merge_seqs[n_merge] |
-                              // flat_seq[total] | flat_meta[total]
+                              // flat_seq[total] | flat_meta[total] | flat_id[total] |
+                              // prefix_ids[n_prefix]
   size_t meta_cap = 0;        // ints
   int32_t *h_meta = nullptr;  // pinned staging
   size_t h_cap = 0;
@@ -1762,11 +1764,10 @@ struct Plan {
   void *d_ws = nullptr;
   uint64_t ws_cap = 0;
   uint64_t ws_ml_bytes = 0;   // offset of the o rows inside d_ws
-  int32_t *d_flat_id = nullptr;  // [total] block ids in piece order
-  size_t flat_cap = 0;
-  const int32_t *bound_indptr = nullptr;  // tables flat_id was built from
-  const int32_t *bound_ids = nullptr;
-  bool all_partial = false;  // every sequence stores partials (built for a shared prefix's suffixes)
+  size_t flat_off = 0;        // offset (ints) of flat_id inside d_meta
+  bool has_tables = false;    // flat_id holds the block ids given at build time
+  int32_t n_prefix = 0;       // shared-prefix ids given at build time (0: none)
+  bool all_partial = false;   // every sequence stores partials (built for a shared prefix's suffixes)
 };
 
 static PlanDev plan_dev(const Plan *pl) {
@@ -1780,7 +1781,7 @@ static PlanDev plan_dev(const Plan *pl) {
   d.merge_seqs = d.seq_npiece + pl->B;
   d.flat_seq = d.merge_seqs + pl->n_merge;
   d.flat_meta = d.flat_seq + pl->total;
-  d.flat_id = pl->d_flat_id;
+  d.flat_id = pl->d_meta + pl->flat_off;
   d.B = pl->B;
   d.P = pl->P;
   d.total_blocks = pl->total;
@@ -1902,7 +1903,6 @@ extern "C" int mkv_decode_plan_destroy(mkv_decode_plan *plan) {
   if (pl->d_meta) (void)hipFree(pl->d_meta);
   if (pl->h_meta) (void)hipHostFree(pl->h_meta);
   if (pl->d_ws) (void)hipFree(pl->d_ws);
-  if (pl->d_flat_id) (void)hipFree(pl->d_flat_id);
   if (pl->uploaded) (void)hipEventDestroy(pl->uploaded);
   delete pl;
   return MKV_OK;
@@ -1962,13 +1962,33 @@ static int64_t coop_resident(Pool *p) {
   return p->coop_slots;
 }
 
+// Host tables given to a plan build (the engine's form; all NULL when the
+// calls bring device tables).
+struct HostTables {
+  const uint32_t *indptr = nullptr;  // [B+1]
+  const uint32_t *ids = nullptr;
+  const uint32_t *prefix = nullptr;  // shared prefix [n_prefix]
+  int32_t n_prefix = 0;
+};
+
 static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t num_seqs, int32_t pieces,
-                      bool all_partial, void *stream) {
+                      bool all_partial, const HostTables &ht, void *stream) {
   if (!plan) return set_error(MKV_ERR_INVALID_ARGUMENT, "plan is NULL");
   Plan *pl = reinterpret_cast<Plan *>(plan);
   const Geom &g = pl->pool->g;
   if (num_seqs < 1 || !h_ctx_lens) return set_error(MKV_ERR_INVALID_ARGUMENT, "need num_seqs >= 1 context lengths");
   if (pieces < 0) return set_error(MKV_ERR_INVALID_ARGUMENT, "pieces must be >= 0");
+  if (ht.indptr || ht.ids) {
+    int rc = check_host_tables(g, ht.indptr, ht.ids, h_ctx_lens, num_seqs, nullptr);
+    if (rc) return rc;
+  }
+  if (ht.n_prefix < 0 || (ht.n_prefix > 0 && !ht.prefix))
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "bad prefix ids");
+  if (ht.n_prefix > INT32_MAX / (2 * kPageSize)) return set_error(MKV_ERR_INVALID_ARGUMENT, "prefix too long");
+  for (int32_t i = 0; i < ht.n_prefix; i++)
+    if (ht.prefix[i] >= (uint64_t)g.nblocks)
+      return set_error(MKV_ERR_INVALID_ARGUMENT, "prefix block id %u (entry %d) outside the pool of %lld",
+                       ht.prefix[i], i, (long long)g.nblocks);
   int64_t total = 0;
   for (int32_t b = 0; b < num_seqs; b++) {
     if (h_ctx_lens[b] < 1) return set_error(MKV_ERR_INVALID_ARGUMENT, "ctx_len[%d] = %d < 1", b, h_ctx_lens[b]);
@@ -2035,7 +2055,7 @@ static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t 
   DeviceGuard guard(pl->pool->device);
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
   const size_t n_ints = (size_t)num_seqs + (num_seqs + 1) + (P + 1) + P + 3 * (size_t)num_seqs +
-                        2 * (size_t)total;
+                        3 * (size_t)total + ht.n_prefix;
   // Staging: wait for the previous upload to leave the pinned buffer.
   if (pl->pending) {
     MKV_CHECK_HIP(hipEventSynchronize(pl->uploaded));
@@ -2078,9 +2098,21 @@ static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t 
       fmeta[blk0[b] + j] = (last ? ctx[b] - kPageSize * j : kPageSize) | (last ? kMetaLast : 0) | single;
     }
   }
-  const size_t used = (size_t)num_seqs + (num_seqs + 1) + (P + 1) + P + 2 * (size_t)num_seqs + n_merge +
-                      2 * (size_t)total;
-  if (pl->meta_cap < used) {
+  // Block ids in piece order (flattened order: sequence b's first
+  // ceil(ctx_b / 16) table entries at seq_blk0[b]), then the prefix ids.
+  const size_t flat_off = (size_t)num_seqs + (num_seqs + 1) + (P + 1) + P + 2 * (size_t)num_seqs + n_merge +
+                          2 * (size_t)total;
+  const bool tables = ht.indptr != nullptr;
+  if (tables) {
+    int32_t *fid = pl->h_meta + flat_off;
+    for (int32_t b = 0; b < num_seqs; b++) {
+      const uint32_t *t = ht.ids + ht.indptr[b];
+      for (int32_t j = 0, nb = blk0[b + 1] - blk0[b]; j < nb; j++) fid[blk0[b] + j] = (int32_t)t[j];
+    }
+    for (int32_t i = 0; i < ht.n_prefix; i++) fid[total + i] = (int32_t)ht.prefix[i];
+  }
+  const size_t used = flat_off + (tables ? (size_t)total + ht.n_prefix : 0);
+  if (pl->meta_cap < flat_off + total + ht.n_prefix) {
     MKV_CHECK_HIP(hipStreamSynchronize(hs));  // earlier launches may read the old buffer
     if (pl->d_meta) MKV_CHECK_HIP(hipFree(pl->d_meta));
     pl->d_meta = nullptr;
@@ -2101,15 +2133,9 @@ static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t 
     pl->ws_cap = need;
   }
   pl->ws_ml_bytes = ml;
-  if (pl->flat_cap < (size_t)total) {
-    MKV_CHECK_HIP(hipStreamSynchronize(hs));
-    if (pl->d_flat_id) MKV_CHECK_HIP(hipFree(pl->d_flat_id));
-    pl->d_flat_id = nullptr;
-    pl->flat_cap = 0;
-    MKV_CHECK_HIP(hipMalloc(reinterpret_cast<void **>(&pl->d_flat_id), (size_t)total * 4));
-    pl->flat_cap = (size_t)total;
-  }
-  pl->bound_indptr = pl->bound_ids = nullptr;  // block ids are re-read at first use
+  pl->flat_off = flat_off;
+  pl->has_tables = tables;
+  pl->n_prefix = ht.n_prefix;
   MKV_CHECK_HIP(hipMemcpyAsync(pl->d_meta, pl->h_meta, used * 4, hipMemcpyHostToDevice, hs));
   MKV_CHECK_HIP(hipEventRecord(pl->uploaded, hs));
   pl->pending = true;
@@ -2124,12 +2150,36 @@ static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t 
 
 extern "C" int mkv_decode_plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t num_seqs,
                                      int32_t pieces, void *stream) {
-  return plan_build(plan, h_ctx_lens, num_seqs, pieces, false, stream);
+  return plan_build(plan, h_ctx_lens, num_seqs, pieces, false, HostTables(), stream);
 }
 
 extern "C" int mkv_decode_plan_build_suffixes(mkv_decode_plan *plan, const int32_t *h_suffix_lens,
                                               int32_t num_seqs, int32_t pieces, void *stream) {
-  return plan_build(plan, h_suffix_lens, num_seqs, pieces, true, stream);
+  return plan_build(plan, h_suffix_lens, num_seqs, pieces, true, HostTables(), stream);
+}
+
+extern "C" int mkv_decode_plan_build_tables(mkv_decode_plan *plan, const int32_t *h_ctx_lens,
+                                            const uint32_t *h_block_indptr, const uint32_t *h_block_ids,
+                                            int32_t num_seqs, int32_t pieces, void *stream) {
+  if (!h_block_indptr) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL block_indptr");
+  HostTables ht;
+  ht.indptr = h_block_indptr;
+  ht.ids = h_block_ids;
+  return plan_build(plan, h_ctx_lens, num_seqs, pieces, false, ht, stream);
+}
+
+extern "C" int mkv_decode_plan_build_shared_prefix(mkv_decode_plan *plan, const uint32_t *h_prefix_ids,
+                                                   int32_t prefix_blocks, const int32_t *h_suffix_lens,
+                                                   const uint32_t *h_block_indptr, const uint32_t *h_block_ids,
+                                                   int32_t num_seqs, int32_t pieces, void *stream) {
+  if (!h_block_indptr) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL block_indptr");
+  if (!h_prefix_ids || prefix_blocks < 1) return set_error(MKV_ERR_INVALID_ARGUMENT, "need a prefix of >= 1 block ids");
+  HostTables ht;
+  ht.indptr = h_block_indptr;
+  ht.ids = h_block_ids;
+  ht.prefix = h_prefix_ids;
+  ht.n_prefix = prefix_blocks;
+  return plan_build(plan, h_suffix_lens, num_seqs, pieces, true, ht, stream);
 }
 
 extern "C" int mkv_decode_plan_info(const mkv_decode_plan *plan, int32_t *out_pieces,
@@ -2152,32 +2202,40 @@ static int launch_planned(Pool *p, const Plan *pl, int32_t layer, const void *d_
   bool use_mfma = false;
   int rc = check_common(p, layer, flags, scale, use_mfma);
   if (rc) return rc;
-  if (!d_q || !d_o || !d_block_indptr || !d_block_ids)
-    return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL device pointer");
+  if (!d_q || !d_o) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL device pointer");
+  const bool dev_tables = d_block_indptr || d_block_ids;
+  if (dev_tables && !(d_block_indptr && d_block_ids))
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "give both device table arrays, or neither");
+  if (!dev_tables && !pl->has_tables)
+    return set_error(MKV_ERR_INVALID_ARGUMENT,
+                     "no block tables: pass device tables, or build the plan with its host tables");
   if (!aligned16(d_q) || !aligned16(d_o) || !aligned16(d_k_new) || !aligned16(d_v_new))
     return set_error(MKV_ERR_INVALID_ARGUMENT, "q, o and new K/V rows must be 16-byte aligned");
   DeviceGuard guard(p->device);
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  const PlanDev pd = plan_dev(pl);
+  if (dev_tables) {
+    // Device tables are read on every call: the MFMA kernels' piece-order
+    // ids are gathered from them here, so a table rewritten in place between
+    // calls is seen by the next call.
+    if (use_mfma) hipLaunchKernelGGL(flatten_ids_kernel, dim3((unsigned)((pl->total + 255) / 256)), dim3(256), 0, hs, pd,
+                       d_block_indptr, d_block_ids, g.nblocks, p->d_err);
+    MKV_CHECK_LAUNCH("flatten_ids_kernel");
+  } else {
+    // The plan's own tables: flattened ids indexed by seq_blk0 form a CSR
+    // table of exactly ceil(ctx_b / 16) ids per sequence.
+    d_block_indptr = pd.seq_blk0;
+    d_block_ids = pd.flat_id;
+  }
   KArgs a = make_kargs(p, layer, d_q, d_o, d_block_indptr, d_block_ids, scale, flags, use_mfma);
   a.new_k = reinterpret_cast<const uint8_t *>(d_k_new);
   a.new_v = reinterpret_cast<const uint8_t *>(d_v_new);
   a.ws_ml = reinterpret_cast<float *>(pl->d_ws);
   a.ws_o = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(pl->d_ws) + pl->ws_ml_bytes);
-  const PlanDev pd = plan_dev(pl);
   const int hcs = g.Hkv * a.nqc;
   const int wpw = std::min(4, hcs);
   const dim3 grid((unsigned)pl->P, (unsigned)((hcs + wpw - 1) / wpw)), block(64 * wpw);
   if (use_mfma) {
-    // Block ids in piece order, read once per plan from the tables of its
-    // first call (the tables are fixed for the step the plan describes).
-    Plan *mpl = const_cast<Plan *>(pl);
-    if (mpl->bound_indptr != d_block_indptr || mpl->bound_ids != d_block_ids) {
-      hipLaunchKernelGGL(flatten_ids_kernel, dim3((unsigned)((pl->total + 255) / 256)), dim3(256), 0, hs, pd,
-                         d_block_indptr, d_block_ids, g.nblocks, p->d_err);
-      MKV_CHECK_LAUNCH("flatten_ids_kernel");
-      mpl->bound_indptr = d_block_indptr;
-      mpl->bound_ids = d_block_ids;
-    }
     // Cooperative kernel: Q rows of one sequence (Hq * D * 2 bytes) must fit
     // the QL loads per lane its ring slots carry.
     const int qlanes = 64 * g.Hkv;
@@ -2270,7 +2328,14 @@ extern "C" int mkv_decode_step_shared_prefix(mkv_pool *pool, const mkv_decode_pl
   if (pl->B < 1) return set_error(MKV_ERR_INVALID_ARGUMENT, "plan was never built");
   if (!pl->all_partial)
     return set_error(MKV_ERR_INVALID_ARGUMENT, "the plan must be built with mkv_decode_plan_build_suffixes");
-  if (!d_prefix_ids || prefix_blocks < 1 || prefix_blocks > INT32_MAX / (2 * kPageSize))
+  if (!d_prefix_ids) {  // the prefix given at build time
+    if (!pl->has_tables || pl->n_prefix < 1)
+      return set_error(MKV_ERR_INVALID_ARGUMENT,
+                       "no prefix ids: pass device ids, or build the plan with mkv_decode_plan_build_shared_prefix");
+    d_prefix_ids = pl->d_meta + pl->flat_off + pl->total;
+    prefix_blocks = pl->n_prefix;
+  }
+  if (prefix_blocks < 1 || prefix_blocks > INT32_MAX / (2 * kPageSize))
     return set_error(MKV_ERR_INVALID_ARGUMENT, "need a prefix of >= 1 block ids");
   if ((d_k_new == nullptr) != (d_v_new == nullptr))
     return set_error(MKV_ERR_INVALID_ARGUMENT, "give both new K and V rows, or neither");
@@ -2280,8 +2345,12 @@ extern "C" int mkv_decode_step_shared_prefix(mkv_pool *pool, const mkv_decode_pl
   if (!use_mfma || g.Hq / g.Hkv > kQChunkMfma)
     return set_error(MKV_ERR_INVALID_ARGUMENT,
                      "shared-prefix decode needs bf16 KV, head_dim 64/128/256 and at most 16 query heads per KV head");
-  if (!d_q || !d_o || !d_block_indptr || !d_block_ids)
-    return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL device pointer");
+  if (!d_q || !d_o) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL device pointer");
+  if ((d_block_indptr == nullptr) != (d_block_ids == nullptr))
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "give both device table arrays, or neither");
+  if (!d_block_indptr && !pl->has_tables)
+    return set_error(MKV_ERR_INVALID_ARGUMENT,
+                     "no suffix tables: pass device tables, or build the plan with its host tables");
   if (!aligned16(d_q) || !aligned16(d_o)) return set_error(MKV_ERR_INVALID_ARGUMENT, "q and o must be 16-byte aligned");
   DeviceGuard guard(p->device);
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
@@ -2367,6 +2436,49 @@ extern "C" int mkv_extend_attention(mkv_pool *pool, int32_t layer, const void *d
   return launch_ext_tiles(p, a, e, 4, hs);
 }
 
+extern "C" int mkv_extend_attention_host(mkv_pool *pool, int32_t layer, const void *d_q, void *d_o,
+                                         const int32_t *h_q_lens, const int32_t *h_ctx_lens,
+                                         const uint32_t *h_block_indptr, const uint32_t *h_block_ids,
+                                         int32_t num_seqs, float scale, uint32_t flags, void *stream) {
+  if (!pool) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL pool");
+  Pool *p = reinterpret_cast<Pool *>(pool);
+  if (num_seqs < 0) return set_error(MKV_ERR_INVALID_ARGUMENT, "num_seqs < 0");
+  if (num_seqs == 0) return MKV_OK;
+  if (!h_q_lens) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL q_lens");
+  int32_t max_ctx = 0;
+  int rc = check_host_tables(p->g, h_block_indptr, h_block_ids, h_ctx_lens, num_seqs, &max_ctx);
+  if (rc) return rc;
+  int32_t max_q = 0;
+  int64_t rows = 0;
+  for (int32_t b = 0; b < num_seqs; b++) {
+    if (h_q_lens[b] < 0 || h_q_lens[b] > h_ctx_lens[b])
+      return set_error(MKV_ERR_INVALID_ARGUMENT, "sequence %d: %d new tokens outside [0, ctx %d]", b, h_q_lens[b],
+                       h_ctx_lens[b]);
+    max_q = std::max(max_q, h_q_lens[b]);
+    rows += h_q_lens[b];
+  }
+  if (rows > INT32_MAX) return set_error(MKV_ERR_INVALID_ARGUMENT, "more than 2^31 - 1 query rows");
+  if (max_q == 0) return MKV_OK;
+  const size_t nids = h_block_indptr[num_seqs];
+  const size_t n = 3 * (size_t)num_seqs + 2 + nids;  // q_indptr | indptr | ctx | ids
+  DeviceGuard guard(p->device);
+  hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  MetaSlot *sl = nullptr;
+  if ((rc = meta_acquire(p, n, hs, &sl))) return rc;
+  int32_t *qp = sl->h, *ip = qp + num_seqs + 1, *cl = ip + num_seqs + 1, *ix = cl + num_seqs;
+  qp[0] = 0;
+  for (int32_t b = 0; b < num_seqs; b++) qp[b + 1] = qp[b] + h_q_lens[b];
+  for (int32_t b = 0; b <= num_seqs; b++) ip[b] = (int32_t)h_block_indptr[b];
+  std::memcpy(cl, h_ctx_lens, (size_t)num_seqs * 4);
+  if (nids) std::memcpy(ix, h_block_ids, nids * 4);
+  if ((rc = meta_upload(sl, n, hs))) return rc;
+  const int32_t *d = sl->d;
+  rc = mkv_extend_attention(pool, layer, d_q, d_o, d, d + num_seqs + 1, d + 3 * num_seqs + 2, d + 2 * num_seqs + 2,
+                            num_seqs, max_q, max_ctx, scale, flags, stream);
+  const int rr = meta_release(sl, hs);
+  return rc ? rc : rr;
+}
+
 // MFMA query tiles of the extend kernel for e (B, max_q, max_ctx, causal,
 // partial and the sequence arguments set): picks the instantiation and the
 // key-range split (at most split_cap), grows the pool workspace when
@@ -2385,7 +2497,10 @@ static int launch_ext_tiles(Pool *p, KArgs &a, ExtArgs &e, int split_cap, hipStr
   // (head_dim <= 128) and chunks are longer than one sub-tile. Measured at
   // Qwen-7B heads: 8 x 512 after 4k 526 -> 480 us, 8 x 2,048 prompts 560 ->
   // 534 us; 16-token chunks would leave half the waves idle (168 -> 220 us).
-  const int WG = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : G <= 8 ? 8 : 16;
+  // At head_dim 256 a workgroup has at least 4 waves: waves past G only
+  // share the loads, and one or two waves would each carry 16-32 loads per
+  // ring stage (register spills).
+  const int WG = G <= 1 && g.D < 256 ? 1 : G <= 2 && g.D < 256 ? 2 : G <= 4 ? 4 : G <= 8 ? 8 : 16;
   const int TP = (WG <= 8 && g.D <= 128 && max_q_len > 16) ? 2 : 1;
   const int W = WG * TP;
   const int64_t tiles = ((int64_t)max_q_len + 16 * TP - 1) / (16 * TP);
@@ -2404,7 +2519,13 @@ static int launch_ext_tiles(Pool *p, KArgs &a, ExtArgs &e, int split_cap, hipStr
   switch (g.D) {
     case 64: if (TP == 2) MKV_EXT_FN(64, 2); else MKV_EXT_FN(64, 1); break;
     case 128: if (TP == 2) MKV_EXT_FN(128, 2); else MKV_EXT_FN(128, 1); break;
-    default: MKV_EXT_FN(256, 1); break;
+    default:
+      switch (W) {
+        case 4: fn = reinterpret_cast<const void *>(&attn_extend_kernel<256, 4, kExtKB, kExtR, 1>); break;
+        case 8: fn = reinterpret_cast<const void *>(&attn_extend_kernel<256, 8, kExtKB, kExtR, 1>); break;
+        default: fn = reinterpret_cast<const void *>(&attn_extend_kernel<256, 16, kExtKB, kExtR, 1>); break;
+      }
+      break;
   }
 #undef MKV_EXT_FN
   // When the launch leaves resident workgroup slots empty (short chunks over

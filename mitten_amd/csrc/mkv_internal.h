@@ -25,6 +25,20 @@ struct Geom {
   int64_t plane_bytes; // nblocks * block_bytes (one layer, K or V)
 };
 
+// Host metadata staging for the *_host entry points. The caller's host
+// arrays are copied into a pinned slot before the call returns and uploaded
+// on the caller's stream ahead of the launch that reads them. Slots are used
+// round-robin; a slot is reused once the stream has passed the launches that
+// read it (its `done` event), so the wait almost never blocks.
+constexpr int kMetaSlots = 8;
+struct MetaSlot {
+  int32_t *h = nullptr;  // pinned host
+  int32_t *d = nullptr;  // device
+  size_t cap = 0;        // int32 elements of both
+  hipEvent_t done = nullptr;
+  bool pending = false;
+};
+
 struct Pool {
   mkv_pool_desc desc;
   Geom g;
@@ -37,7 +51,25 @@ struct Pool {
   int64_t coop_slots = -1;   // resident workgroups of the decode kernel (-1: not yet queried)
   int cus = 0;               // compute units of the device (0: not yet queried)
   int ext_per_cu[3][5][2] = {};  // resident extend workgroups per CU by (head_dim, waves, sub-tiles); 0: not yet queried
+  MetaSlot meta[kMetaSlots];
+  int meta_next = 0;
 };
+
+// Next staging slot with room for n int32 values (waits for its previous
+// readers, grows it when needed). Fill s->h[0..n), then meta_upload, launch,
+// meta_release.
+int meta_acquire(Pool *p, size_t n, hipStream_t hs, MetaSlot **out);
+int meta_upload(MetaSlot *s, size_t n, hipStream_t hs);
+int meta_release(MetaSlot *s, hipStream_t hs);
+void meta_free(Pool *p);
+
+// Host-side checks of the engine's u32 metadata against the pool (pure CPU).
+int check_host_slots(const Geom &g, const uint32_t *slots, int32_t n);
+// Tables of num_seqs sequences: indptr monotone from 0, every id < nblocks,
+// table b holds >= ceil(len_b / page) ids, 1 <= len_b. Returns the largest
+// len in *max_len (when non-NULL).
+int check_host_tables(const Geom &g, const uint32_t *indptr, const uint32_t *ids, const int32_t *lens,
+                      int32_t num_seqs, int32_t *max_len);
 
 // Thread-local last-error message and status helpers.
 int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));

@@ -5,6 +5,7 @@
 // 16-byte chunks (global_load_dwordx4 / global_store_dwordx4), consecutive
 // lanes touch consecutive chunks of one contiguous row or block, and every
 // slot / block id is range-checked before it is dereferenced.
+#include <algorithm>
 #include <cstring>
 #include <new>
 #include <vector>
@@ -71,31 +72,51 @@ static Geom make_geom(const mkv_pool_desc *d) {
 
 // ---- kernels ------------------------------------------------------------------
 
-// grid.x covers num_tokens * 2 * chunks_per_row 16-byte chunks; grid.y = layers.
+// grid.y = layer. The chunk space of a launch is num_tokens * 2 * cpr
+// 16-byte chunks (token-major, then K/V, then the row's chunks); a thread
+// takes kAppendPer chunks 256 apart per pass, issues all their loads and the
+// slot ids of their tokens, then the stores. Loads and stores are
+// nontemporal (a row is moved once). Indices are 32-bit (the host keeps the
+// chunk count of one launch below 2^31).
+constexpr int kAppendPer = 8;
+
 __global__ void __launch_bounds__(256)
-append_kernel(uint8_t *__restrict__ pool, int32_t layer0, const uint4 *__restrict__ k,
-              const uint4 *__restrict__ v, const int32_t *__restrict__ slots, int32_t n_tok,
-              int64_t src_layer_stride, Geom g, uint32_t *__restrict__ d_err) {
-  const int cpr = (int)(g.row_bytes >> 4);
-  const int64_t total = (int64_t)n_tok * 2 * cpr;
-  const int64_t nslots = g.nblocks * g.ps;
+append_kernel(uint8_t *__restrict__ pool, int32_t layer0, const uint8_t *__restrict__ k,
+              const uint8_t *__restrict__ v, const int32_t *__restrict__ slots, uint32_t total,
+              uint32_t cpr, int64_t src_layer_stride, Geom g, uint32_t *__restrict__ d_err) {
+  const uint32_t per_tok = 2 * cpr;
+  const uint32_t nslots = (uint32_t)(g.nblocks * kPageSize);  // < 2^31 (checked at pool creation)
   const int layer = layer0 + (int)blockIdx.y;
-  uint8_t *layer_base = pool + (int64_t)layer * 2 * g.plane_bytes;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t t = i / (2 * cpr);
-    const int rem = (int)(i - t * 2 * cpr);
-    const int kv = rem >= cpr;
-    const int c = rem - kv * cpr;
-    const int32_t s = slots[t];
-    if (s < 0 || s >= nslots) {
-      if (c == 0 && kv == 0) record_error(d_err, MKV_DEVERR_SLOT);
-      continue;
+  uint8_t *const kbase = pool + (int64_t)layer * 2 * g.plane_bytes;
+  const int64_t src_off = (int64_t)blockIdx.y * src_layer_stride;
+  const uint32_t stride = gridDim.x * 256u * kAppendPer;
+  for (uint32_t base = blockIdx.x * 256u * kAppendPer + threadIdx.x; base < total; base += stride) {
+    u32x4v r[kAppendPer];
+    int32_t sl[kAppendPer];
+#pragma unroll
+    for (int u = 0; u < kAppendPer; u++) {  // clamped past the end: loaded, never stored
+      const uint32_t c = min(base + u * 256u, total - 1);
+      const uint32_t t = c / per_tok, rem = c - t * per_tok;
+      const uint32_t kv = rem >= cpr, cc = rem - kv * cpr;
+      r[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4v *>(
+          (kv ? v : k) + src_off + ((int64_t)t * cpr + cc) * 16));
+      sl[u] = slots[t];
     }
-    const uint4 *src = (kv ? v : k) + (int64_t)blockIdx.y * src_layer_stride + t * cpr + c;
-    uint8_t *dst = layer_base + kv * g.plane_bytes + (int64_t)(s / kPageSize) * g.block_bytes +
-                   (int64_t)(s % kPageSize) * g.row_bytes;
-    reinterpret_cast<uint4 *>(dst)[c] = *src;
+#pragma unroll
+    for (int u = 0; u < kAppendPer; u++) {
+      const uint32_t c = base + u * 256u;
+      if (c >= total) break;
+      const uint32_t t = c / per_tok, rem = c - t * per_tok;
+      const uint32_t kv = rem >= cpr, cc = rem - kv * cpr;
+      const uint32_t s = (uint32_t)sl[u];
+      if (s >= nslots) {  // negative ids wrap above nslots
+        if (rem == 0) record_error(d_err, MKV_DEVERR_SLOT);
+        continue;
+      }
+      uint8_t *dst = kbase + kv * g.plane_bytes + (int64_t)(s / kPageSize) * g.block_bytes +
+                     (int64_t)(s % kPageSize) * g.row_bytes;
+      __builtin_nontemporal_store(r[u], reinterpret_cast<u32x4v *>(dst) + cc);
+    }
   }
 }
 
@@ -195,6 +216,92 @@ copy_blocks_kernel(uint8_t *__restrict__ pool, const int32_t *__restrict__ src,
   }
 }
 
+// ---- host metadata staging ----------------------------------------------------------
+
+int meta_acquire(Pool *p, size_t n, hipStream_t hs, MetaSlot **out) {
+  MetaSlot *sl = &p->meta[p->meta_next];
+  p->meta_next = (p->meta_next + 1) % kMetaSlots;
+  if (!sl->done) MKV_CHECK_HIP(hipEventCreateWithFlags(&sl->done, hipEventDisableTiming));
+  if (sl->pending) {  // the launches that read this slot last time are done
+    MKV_CHECK_HIP(hipEventSynchronize(sl->done));
+    sl->pending = false;
+  }
+  n = std::max<size_t>(n, 1);
+  if (sl->cap < n) {
+    const size_t cap = std::max<size_t>(n, 4096);
+    if (sl->h) MKV_CHECK_HIP(hipHostFree(sl->h));
+    if (sl->d) MKV_CHECK_HIP(hipFree(sl->d));
+    sl->h = nullptr;
+    sl->d = nullptr;
+    sl->cap = 0;
+    MKV_CHECK_HIP(hipHostMalloc(reinterpret_cast<void **>(&sl->h), cap * 4));
+    MKV_CHECK_HIP(hipMalloc(reinterpret_cast<void **>(&sl->d), cap * 4));
+    sl->cap = cap;
+  }
+  (void)hs;
+  *out = sl;
+  return MKV_OK;
+}
+
+int meta_upload(MetaSlot *sl, size_t n, hipStream_t hs) {
+  if (n) MKV_CHECK_HIP(hipMemcpyAsync(sl->d, sl->h, n * 4, hipMemcpyHostToDevice, hs));
+  return MKV_OK;
+}
+
+int meta_release(MetaSlot *sl, hipStream_t hs) {
+  MKV_CHECK_HIP(hipEventRecord(sl->done, hs));
+  sl->pending = true;
+  return MKV_OK;
+}
+
+void meta_free(Pool *p) {
+  for (MetaSlot &sl : p->meta) {
+    if (sl.h) (void)hipHostFree(sl.h);
+    if (sl.d) (void)hipFree(sl.d);
+    if (sl.done) (void)hipEventDestroy(sl.done);
+    sl = MetaSlot();
+  }
+}
+
+int check_host_slots(const Geom &g, const uint32_t *slots, int32_t n) {
+  if (n < 0) return set_error(MKV_ERR_INVALID_ARGUMENT, "num_tokens < 0");
+  if (n > 0 && !slots) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL slot mapping");
+  const uint64_t nslots = (uint64_t)g.nblocks * kPageSize;
+  for (int32_t i = 0; i < n; i++)
+    if (slots[i] >= nslots)
+      return set_error(MKV_ERR_INVALID_ARGUMENT, "slot[%d] = %u outside [0, %llu)", i, slots[i],
+                       (unsigned long long)nslots);
+  return MKV_OK;
+}
+
+int check_host_tables(const Geom &g, const uint32_t *indptr, const uint32_t *ids, const int32_t *lens,
+                      int32_t num_seqs, int32_t *max_len) {
+  if (num_seqs < 0) return set_error(MKV_ERR_INVALID_ARGUMENT, "num_seqs < 0");
+  if (!indptr || !lens) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL indptr or lengths");
+  if (indptr[0] != 0) return set_error(MKV_ERR_INVALID_ARGUMENT, "block_indptr[0] = %u, expected 0", indptr[0]);
+  if (indptr[num_seqs] > (uint32_t)INT32_MAX)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "more than 2^31 - 1 block ids");
+  if (indptr[num_seqs] > 0 && !ids) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL block ids");
+  int32_t mx = 0;
+  for (int32_t b = 0; b < num_seqs; b++) {
+    if (indptr[b + 1] < indptr[b])
+      return set_error(MKV_ERR_INVALID_ARGUMENT, "block_indptr not monotone at %d", b);
+    const int32_t n = lens[b];
+    if (n < 1) return set_error(MKV_ERR_INVALID_ARGUMENT, "length[%d] = %d < 1", b, n);
+    const uint32_t need = (uint32_t)((n + kPageSize - 1) / kPageSize);
+    if (indptr[b + 1] - indptr[b] < need)
+      return set_error(MKV_ERR_INVALID_ARGUMENT, "sequence %d: %u blocks cannot hold %d tokens", b,
+                       indptr[b + 1] - indptr[b], n);
+    for (uint32_t i = indptr[b]; i < indptr[b] + need; i++)
+      if (ids[i] >= (uint64_t)g.nblocks)
+        return set_error(MKV_ERR_INVALID_ARGUMENT, "sequence %d: block id %u (table entry %u) outside the pool of %lld",
+                         b, ids[i], i - indptr[b], (long long)g.nblocks);
+    mx = std::max(mx, n);
+  }
+  if (max_len) *max_len = mx;
+  return MKV_OK;
+}
+
 }  // namespace mkv
 
 using namespace mkv;
@@ -254,6 +361,7 @@ extern "C" int mkv_pool_destroy(mkv_pool *pool) {
   DeviceGuard guard(p->device);
   (void)hipDeviceSynchronize();
   if (p->ws) (void)hipFree(p->ws);
+  meta_free(p);
   (void)hipFree(p->d_err);
   (void)hipFree(p->data);
   delete p;
@@ -306,14 +414,21 @@ static int launch_append(Pool *p, int32_t layer0, int32_t nlayers, const void *d
     return set_error(MKV_ERR_INVALID_ARGUMENT, "K/V source must be 16-byte aligned");
   DeviceGuard guard(p->device);
   const int64_t cpr = p->g.row_bytes >> 4;
-  const int64_t total = (int64_t)n * 2 * cpr;
-  const int threads = 256;
-  const int64_t blocks = std::min<int64_t>((total + threads - 1) / threads, 65536);
-  hipLaunchKernelGGL(append_kernel, dim3((unsigned)blocks, (unsigned)nlayers), dim3(threads), 0,
-                     reinterpret_cast<hipStream_t>(stream), p->data, layer0,
-                     reinterpret_cast<const uint4 *>(d_k), reinterpret_cast<const uint4 *>(d_v),
-                     d_slots, n, (int64_t)n * cpr, p->g, p->d_err);
-  MKV_CHECK_LAUNCH("append_kernel");
+  hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  // Launches of at most 2^30 chunks, so 32-bit chunk indices never overflow.
+  const int64_t tok_per_launch = std::max<int64_t>(1, ((int64_t)1 << 30) / (2 * cpr));
+  for (int64_t t0 = 0; t0 < n; t0 += tok_per_launch) {
+    const int64_t nt = std::min<int64_t>(tok_per_launch, n - t0);
+    const int64_t total = nt * 2 * cpr;
+    const int64_t per_wg = 256 * kAppendPer;
+    const int64_t wgs = std::min<int64_t>((total + per_wg - 1) / per_wg, 8192);
+    const int64_t off = t0 * p->g.row_bytes;
+    hipLaunchKernelGGL(append_kernel, dim3((unsigned)wgs, (unsigned)nlayers), dim3(256), 0, hs, p->data, layer0,
+                       reinterpret_cast<const uint8_t *>(d_k) + off, reinterpret_cast<const uint8_t *>(d_v) + off,
+                       d_slots + t0, (uint32_t)total, (uint32_t)cpr, (int64_t)n * p->g.row_bytes, p->g,
+                       p->d_err);
+    MKV_CHECK_LAUNCH("append_kernel");
+  }
   return MKV_OK;
 }
 
@@ -376,6 +491,111 @@ extern "C" int mkv_copy_blocks(mkv_pool *pool, const int32_t *d_src_blocks,
                      p->g, p->d_err);
   MKV_CHECK_LAUNCH("copy_blocks_kernel");
   return MKV_OK;
+}
+
+// ---- C ABI: host metadata (the engine's u32 form) --------------------------------------
+
+extern "C" int mkv_append_host(mkv_pool *pool, int32_t layer, const void *d_k, const void *d_v,
+                               const uint32_t *h_slot_mapping, int32_t num_tokens, void *stream) {
+  if (!pool) return set_error(MKV_ERR_INVALID_ARGUMENT, "pool is NULL");
+  Pool *p = reinterpret_cast<Pool *>(pool);
+  int rc = check_layer(p, layer);
+  if (rc) return rc;
+  if ((rc = check_host_slots(p->g, h_slot_mapping, num_tokens))) return rc;
+  if (num_tokens == 0) return MKV_OK;
+  if (!d_k || !d_v) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL device pointer");
+  DeviceGuard guard(p->device);
+  hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  MetaSlot *sl = nullptr;
+  if ((rc = meta_acquire(p, num_tokens, hs, &sl))) return rc;
+  std::memcpy(sl->h, h_slot_mapping, (size_t)num_tokens * 4);
+  if ((rc = meta_upload(sl, num_tokens, hs))) return rc;
+  rc = launch_append(p, layer, 1, d_k, d_v, sl->d, num_tokens, stream);
+  const int rr = meta_release(sl, hs);
+  return rc ? rc : rr;
+}
+
+extern "C" int mkv_append_all_layers_host(mkv_pool *pool, const void *d_k, const void *d_v,
+                                          const uint32_t *h_slot_mapping, int32_t num_tokens, void *stream) {
+  if (!pool) return set_error(MKV_ERR_INVALID_ARGUMENT, "pool is NULL");
+  Pool *p = reinterpret_cast<Pool *>(pool);
+  int rc = check_host_slots(p->g, h_slot_mapping, num_tokens);
+  if (rc) return rc;
+  if (num_tokens == 0) return MKV_OK;
+  if (!d_k || !d_v) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL device pointer");
+  DeviceGuard guard(p->device);
+  hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  MetaSlot *sl = nullptr;
+  if ((rc = meta_acquire(p, num_tokens, hs, &sl))) return rc;
+  std::memcpy(sl->h, h_slot_mapping, (size_t)num_tokens * 4);
+  if ((rc = meta_upload(sl, num_tokens, hs))) return rc;
+  rc = launch_append(p, 0, p->g.L, d_k, d_v, sl->d, num_tokens, stream);
+  const int rr = meta_release(sl, hs);
+  return rc ? rc : rr;
+}
+
+extern "C" int mkv_gather_host(mkv_pool *pool, int32_t layer, const uint32_t *h_block_indptr,
+                               const uint32_t *h_block_ids, const int32_t *h_ctx_lens, int32_t num_seqs,
+                               void *d_out_k, void *d_out_v, int64_t out_capacity_tokens, void *stream) {
+  if (!pool) return set_error(MKV_ERR_INVALID_ARGUMENT, "pool is NULL");
+  Pool *p = reinterpret_cast<Pool *>(pool);
+  int rc = check_layer(p, layer);
+  if (rc) return rc;
+  if (num_seqs < 0 || out_capacity_tokens < 0)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "num_seqs and out_capacity_tokens must be >= 0");
+  if (num_seqs == 0) return MKV_OK;
+  if (num_seqs > 65535) return set_error(MKV_ERR_INVALID_ARGUMENT, "num_seqs > 65535");
+  int32_t max_ctx = 0;
+  if ((rc = check_host_tables(p->g, h_block_indptr, h_block_ids, h_ctx_lens, num_seqs, &max_ctx))) return rc;
+  int64_t tokens = 0;
+  for (int32_t b = 0; b < num_seqs; b++) tokens += h_ctx_lens[b];
+  if (tokens > out_capacity_tokens)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "outputs hold %lld tokens, the tables give %lld",
+                     (long long)out_capacity_tokens, (long long)tokens);
+  if (tokens > INT32_MAX) return set_error(MKV_ERR_INVALID_ARGUMENT, "more than 2^31 - 1 tokens");
+  const size_t nids = h_block_indptr[num_seqs];
+  const size_t n = 2 * ((size_t)num_seqs + 1) + nids;  // indptr | ctx_indptr | ids
+  DeviceGuard guard(p->device);
+  hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  MetaSlot *sl = nullptr;
+  if ((rc = meta_acquire(p, n, hs, &sl))) return rc;
+  int32_t *ip = sl->h, *cp = ip + num_seqs + 1, *ix = cp + num_seqs + 1;
+  cp[0] = 0;
+  for (int32_t b = 0; b <= num_seqs; b++) ip[b] = (int32_t)h_block_indptr[b];
+  for (int32_t b = 0; b < num_seqs; b++) cp[b + 1] = cp[b] + h_ctx_lens[b];
+  if (nids) std::memcpy(ix, h_block_ids, nids * 4);
+  if ((rc = meta_upload(sl, n, hs))) return rc;
+  rc = mkv_gather(pool, layer, sl->d, sl->d + 2 * (num_seqs + 1), sl->d + num_seqs + 1, num_seqs, max_ctx,
+                  d_out_k, d_out_v, out_capacity_tokens, stream);
+  const int rr = meta_release(sl, hs);
+  return rc ? rc : rr;
+}
+
+extern "C" int mkv_copy_blocks_host(mkv_pool *pool, const uint32_t *h_src_blocks, const uint32_t *h_dst_blocks,
+                                    int32_t num_pairs, void *stream) {
+  if (!pool) return set_error(MKV_ERR_INVALID_ARGUMENT, "pool is NULL");
+  Pool *p = reinterpret_cast<Pool *>(pool);
+  if (num_pairs < 0) return set_error(MKV_ERR_INVALID_ARGUMENT, "num_pairs < 0");
+  if (num_pairs == 0) return MKV_OK;
+  if (!h_src_blocks || !h_dst_blocks) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL block arrays");
+  for (int32_t i = 0; i < num_pairs; i++)
+    if (h_src_blocks[i] >= (uint64_t)p->g.nblocks || h_dst_blocks[i] >= (uint64_t)p->g.nblocks)
+      return set_error(MKV_ERR_INVALID_ARGUMENT, "pair %d (%u -> %u) outside the pool of %lld blocks", i,
+                       h_src_blocks[i], h_dst_blocks[i], (long long)p->g.nblocks);
+  DeviceGuard guard(p->device);
+  hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  MetaSlot *sl = nullptr;
+  int rc = meta_acquire(p, 2 * (size_t)num_pairs, hs, &sl);
+  if (rc) return rc;
+  std::memcpy(sl->h, h_src_blocks, (size_t)num_pairs * 4);
+  std::memcpy(sl->h + num_pairs, h_dst_blocks, (size_t)num_pairs * 4);
+  // Distinct destinations, no block both a source and a destination: the
+  // copies of one launch then do not depend on each other's order.
+  if ((rc = mkv_validate_copy_pairs(&p->desc, sl->h, sl->h + num_pairs, num_pairs))) return rc;
+  if ((rc = meta_upload(sl, 2 * (size_t)num_pairs, hs))) return rc;
+  rc = mkv_copy_blocks(pool, sl->d, sl->d + num_pairs, num_pairs, stream);
+  const int rr = meta_release(sl, hs);
+  return rc ? rc : rr;
 }
 
 // ---- C ABI: host validation ------------------------------------------------------------

@@ -14,6 +14,8 @@
 // by a shuffle.
 // Arithmetic is f32 in the reference's operation order, with no contraction
 // into FMAs; a bf16 pool gets one round-to-nearest-even per output element.
+#include <cstring>
+
 #include "mkv_internal.h"
 
 namespace mkv {
@@ -450,4 +452,30 @@ extern "C" int mkv_qk_norm_rope_append(mkv_pool *pool, int32_t layer, const void
 #undef MKV_PREP
   MKV_CHECK_LAUNCH("qk_norm_rope_append_kernel");
   return MKV_OK;
+}
+
+extern "C" int mkv_qk_norm_rope_append_host(mkv_pool *pool, int32_t layer, const void *d_q, const void *d_k,
+                                            const void *d_v, const float *d_q_norm_w, const float *d_k_norm_w,
+                                            const float *d_inv_freq, int32_t rotary_dim, float eps,
+                                            const int32_t *h_positions, const uint32_t *h_slot_mapping,
+                                            int32_t num_tokens, void *d_q_out, uint32_t flags, void *stream) {
+  if (!pool) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL pool");
+  Pool *p = reinterpret_cast<Pool *>(pool);
+  int rc = check_host_slots(p->g, h_slot_mapping, num_tokens);
+  if (rc) return rc;
+  if (num_tokens == 0) return MKV_OK;
+  if (!h_positions) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL positions");
+  for (int32_t t = 0; t < num_tokens; t++)
+    if (h_positions[t] < 0) return set_error(MKV_ERR_INVALID_ARGUMENT, "position[%d] = %d < 0", t, h_positions[t]);
+  DeviceGuard guard(p->device);
+  hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  MetaSlot *sl = nullptr;
+  if ((rc = meta_acquire(p, 2 * (size_t)num_tokens, hs, &sl))) return rc;
+  std::memcpy(sl->h, h_positions, (size_t)num_tokens * 4);
+  std::memcpy(sl->h + num_tokens, h_slot_mapping, (size_t)num_tokens * 4);
+  if ((rc = meta_upload(sl, 2 * (size_t)num_tokens, hs))) return rc;
+  rc = mkv_qk_norm_rope_append(pool, layer, d_q, d_k, d_v, d_q_norm_w, d_k_norm_w, d_inv_freq, rotary_dim, eps,
+                               sl->d, sl->d + num_tokens, num_tokens, d_q_out, flags, stream);
+  const int rr = meta_release(sl, hs);
+  return rc ? rc : rr;
 }

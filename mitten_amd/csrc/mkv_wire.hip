@@ -17,6 +17,7 @@
 // mix is a bijection, so any single-word change alters the sum, and the
 // index term makes it position-sensitive.
 #include <cstring>
+#include <vector>
 
 #include "mkv_internal.h"
 
@@ -175,6 +176,59 @@ extern "C" int mkv_wire_import(mkv_pool *pool, const int32_t *d_block_ids, int32
                      reinterpret_cast<const unsigned long long *>(d_expected), num_blocks, p->d_err);
   MKV_CHECK_LAUNCH("wire_compare_kernel");
   return MKV_OK;
+}
+
+// ---- host block ids (the engine's u32 pages) ----------------------------------
+
+static int stage_wire_ids(Pool *p, const uint32_t *h_ids, int32_t n, bool distinct, hipStream_t hs, MetaSlot **out) {
+  if (n < 0) return set_error(MKV_ERR_INVALID_ARGUMENT, "num_blocks < 0");
+  if (n > 0 && !h_ids) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL block ids");
+  std::vector<uint8_t> seen(distinct ? (size_t)p->g.nblocks : 0, 0);
+  for (int32_t i = 0; i < n; i++) {
+    if (h_ids[i] >= (uint64_t)p->g.nblocks)
+      return set_error(MKV_ERR_INVALID_ARGUMENT, "block id %u (entry %d) outside the pool of %lld", h_ids[i], i,
+                       (long long)p->g.nblocks);
+    if (distinct) {
+      if (seen[h_ids[i]]) return set_error(MKV_ERR_INVALID_ARGUMENT, "destination block %u repeats", h_ids[i]);
+      seen[h_ids[i]] = 1;
+    }
+  }
+  int rc = meta_acquire(p, n, hs, out);
+  if (rc) return rc;
+  if (n) std::memcpy((*out)->h, h_ids, (size_t)n * 4);
+  return meta_upload(*out, n, hs);
+}
+
+extern "C" int mkv_wire_export_host(mkv_pool *pool, const uint32_t *h_block_ids, int32_t num_blocks,
+                                    int32_t layer_begin, int32_t num_layers, void *d_payload, uint64_t *d_checksums,
+                                    void *stream) {
+  if (!pool) return set_error(MKV_ERR_INVALID_ARGUMENT, "pool is NULL");
+  Pool *p = reinterpret_cast<Pool *>(pool);
+  if (num_blocks == 0) return MKV_OK;
+  DeviceGuard guard(p->device);
+  hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  MetaSlot *sl = nullptr;
+  int rc = stage_wire_ids(p, h_block_ids, num_blocks, false, hs, &sl);
+  if (rc) return rc;
+  rc = mkv_wire_export(pool, sl->d, num_blocks, layer_begin, num_layers, d_payload, d_checksums, stream);
+  const int rr = meta_release(sl, hs);
+  return rc ? rc : rr;
+}
+
+extern "C" int mkv_wire_import_host(mkv_pool *pool, const uint32_t *h_block_ids, int32_t num_blocks,
+                                    int32_t layer_begin, int32_t num_layers, const void *d_payload,
+                                    const uint64_t *d_expected, uint64_t *d_checksums, void *stream) {
+  if (!pool) return set_error(MKV_ERR_INVALID_ARGUMENT, "pool is NULL");
+  Pool *p = reinterpret_cast<Pool *>(pool);
+  if (num_blocks == 0) return MKV_OK;
+  DeviceGuard guard(p->device);
+  hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  MetaSlot *sl = nullptr;
+  int rc = stage_wire_ids(p, h_block_ids, num_blocks, true, hs, &sl);
+  if (rc) return rc;
+  rc = mkv_wire_import(pool, sl->d, num_blocks, layer_begin, num_layers, d_payload, d_expected, d_checksums, stream);
+  const int rr = meta_release(sl, hs);
+  return rc ? rc : rr;
 }
 
 // ---- header (host only) -------------------------------------------------------

@@ -127,6 +127,35 @@ def _i32p(a: np.ndarray):
     return a.ctypes.data_as(_lib.I32P)
 
 
+def _u32p(a: np.ndarray):
+    return a.ctypes.data_as(_lib.U32P)
+
+
+def _is_host(x) -> bool:
+    """Host metadata (numpy array, list, or a CPU tensor): goes through the
+    *_host entry points, which validate and copy it before returning."""
+    if isinstance(x, (np.ndarray, list, tuple)):
+        return True
+    try:
+        import torch
+    except ImportError:
+        return False
+    return isinstance(x, torch.Tensor) and not x.is_cuda
+
+
+def _host_u32(x, name: str) -> np.ndarray:
+    """Engine page ids / slots (u32). Negative values cannot be u32 ids."""
+    a = np.asarray(x.numpy() if hasattr(x, "numpy") else x)
+    if a.size and a.dtype.kind == "i" and int(a.min()) < 0:
+        raise BackendError(MKV_ERR_INVALID_ARGUMENT, f"{name} holds a negative id")
+    return np.ascontiguousarray(a, np.uint32).reshape(-1)
+
+
+def _host_i32(x) -> np.ndarray:
+    a = np.asarray(x.numpy() if hasattr(x, "numpy") else x)
+    return np.ascontiguousarray(a, np.int32).reshape(-1)
+
+
 def validate_slots(desc: PoolDesc, slots) -> None:
     s = np.ascontiguousarray(slots, np.int32)
     _raise(_lib.device_lib().mkv_validate_slots(ctypes.byref(desc.c()), _i32p(s), s.size))
@@ -164,6 +193,11 @@ def _stream_handle(stream) -> ctypes.c_void_p:
 
 def _dptr(t) -> ctypes.c_void_p:
     return ctypes.c_void_p(t.data_ptr())
+
+
+def _tptr(t) -> ctypes.c_void_p:
+    """Device pointer of an optional tensor (NULL for None)."""
+    return ctypes.c_void_p(0) if t is None else ctypes.c_void_p(t.data_ptr())
 
 
 class DeviceKvPool:
@@ -231,22 +265,38 @@ class DeviceKvPool:
 
     # -- operations -----------------------------------------------------------------------
     def append(self, layer: int, k, v, slot_mapping, stream=None) -> None:
+        """slot_mapping: device int32 tensor, or host u32 slots (numpy/list:
+        mkv_append_host validates and copies them)."""
         d = self.desc
-        n = slot_mapping.shape[0]
-        self._i32(slot_mapping, "slot_mapping", n)
+        host = _is_host(slot_mapping)
+        sm = _host_u32(slot_mapping, "slot_mapping") if host else slot_mapping
+        n = sm.shape[0]
+        if not host:
+            self._i32(sm, "slot_mapping", n)
         self._check_tensor(k, (n, d.num_kv_heads, d.head_dim), "k")
         self._check_tensor(v, (n, d.num_kv_heads, d.head_dim), "v")
-        _raise(self._lib.mkv_append(self._h, layer, _dptr(k), _dptr(v), _dptr(slot_mapping), n,
-                                    _stream_handle(stream)))
+        if host:
+            _raise(self._lib.mkv_append_host(self._h, layer, _dptr(k), _dptr(v), _u32p(sm), n,
+                                             _stream_handle(stream)))
+        else:
+            _raise(self._lib.mkv_append(self._h, layer, _dptr(k), _dptr(v), _dptr(sm), n,
+                                        _stream_handle(stream)))
 
     def append_all_layers(self, k, v, slot_mapping, stream=None) -> None:
         d = self.desc
-        n = slot_mapping.shape[0]
-        self._i32(slot_mapping, "slot_mapping", n)
+        host = _is_host(slot_mapping)
+        sm = _host_u32(slot_mapping, "slot_mapping") if host else slot_mapping
+        n = sm.shape[0]
+        if not host:
+            self._i32(sm, "slot_mapping", n)
         self._check_tensor(k, (d.num_layers, n, d.num_kv_heads, d.head_dim), "k")
         self._check_tensor(v, (d.num_layers, n, d.num_kv_heads, d.head_dim), "v")
-        _raise(self._lib.mkv_append_all_layers(self._h, _dptr(k), _dptr(v), _dptr(slot_mapping), n,
-                                               _stream_handle(stream)))
+        if host:
+            _raise(self._lib.mkv_append_all_layers_host(self._h, _dptr(k), _dptr(v), _u32p(sm), n,
+                                                        _stream_handle(stream)))
+        else:
+            _raise(self._lib.mkv_append_all_layers(self._h, _dptr(k), _dptr(v), _dptr(sm), n,
+                                                   _stream_handle(stream)))
 
     def gather(self, layer: int, block_indptr, block_ids, ctx_indptr, max_ctx_len: int,
                out_k=None, out_v=None, total_tokens: int | None = None, stream=None):
@@ -276,7 +326,38 @@ class DeviceKvPool:
                                     cap, _stream_handle(stream)))
         return out_k, out_v
 
+    def gather_host(self, layer: int, block_indptr, block_ids, ctx_lens, out_k=None, out_v=None, stream=None):
+        """gather with host tables (u32 CSR) and host context lengths
+        (mkv_gather_host). Returns (k, v) flat, as gather()."""
+        torch = _torch()
+        d = self.desc
+        ip, ix = _host_u32(block_indptr, "block_indptr"), _host_u32(block_ids, "block_ids")
+        cl = _host_i32(ctx_lens)
+        B = cl.size
+        if ip.size != B + 1:
+            raise BackendError(MKV_ERR_INVALID_ARGUMENT, "block_indptr must have num_seqs + 1 entries")
+        n = int(cl.astype(np.int64).sum()) * d.num_kv_heads * d.head_dim
+        dev = torch.device(f"cuda:{self.device}")
+        if out_k is None:
+            out_k = torch.empty(max(n, 1), dtype=self.torch_dtype, device=dev)
+        if out_v is None:
+            out_v = torch.empty(max(n, 1), dtype=self.torch_dtype, device=dev)
+        self._check_tensor(out_k, None, "out_k")
+        self._check_tensor(out_v, None, "out_v")
+        cap = min(out_k.numel(), out_v.numel()) // (d.num_kv_heads * d.head_dim)
+        _raise(self._lib.mkv_gather_host(self._h, layer, _u32p(ip), _u32p(ix) if ix.size else None, _i32p(cl), B,
+                                         _dptr(out_k), _dptr(out_v), cap, _stream_handle(stream)))
+        return out_k, out_v
+
     def copy_blocks(self, src, dst, stream=None) -> None:
+        """src, dst: device int32 tensors, or host u32 ids (mkv_copy_blocks_host,
+        which also checks that the pairs do not overlap)."""
+        if _is_host(src) or _is_host(dst):
+            s_, d_ = _host_u32(src, "src"), _host_u32(dst, "dst")
+            if s_.size != d_.size:
+                raise BackendError(MKV_ERR_INVALID_ARGUMENT, "src and dst differ in length")
+            _raise(self._lib.mkv_copy_blocks_host(self._h, _u32p(s_), _u32p(d_), s_.size, _stream_handle(stream)))
+            return
         n = src.shape[0]
         self._i32(src, "src", n)
         self._i32(dst, "dst", n)
@@ -349,6 +430,29 @@ class DeviceKvPool:
             _dptr(ctx_lens), B, max_q_len, max_ctx_len, scale, flags, _stream_handle(stream)))
         return out
 
+    def extend_attention_host(self, layer: int, q, q_lens, ctx_lens, block_indptr, block_ids, out=None,
+                              scale: float | None = None, zero_sink: bool = False, stream=None):
+        """extend_attention with host metadata (mkv_extend_attention_host):
+        sequence b's q_lens[b] query rows follow sequence b-1's in q."""
+        torch = _torch()
+        d = self.desc
+        ql, cl = _host_i32(q_lens), _host_i32(ctx_lens)
+        ip, ix = _host_u32(block_indptr, "block_indptr"), _host_u32(block_ids, "block_ids")
+        T = int(ql.astype(np.int64).sum())
+        self._check_tensor(q, (T, d.num_q_heads, d.head_dim), "q")
+        if out is None:
+            out = torch.empty_like(q)
+        self._check_tensor(out, (T, d.num_q_heads, d.head_dim), "out")
+        if ql.size != cl.size or ip.size != cl.size + 1:
+            raise BackendError(MKV_ERR_INVALID_ARGUMENT, "q_lens, ctx_lens and block_indptr disagree on num_seqs")
+        if scale is None:
+            scale = float(np.float32(d.head_dim ** -0.5))
+        flags = ATTN_ZERO_SINK if zero_sink else 0
+        _raise(self._lib.mkv_extend_attention_host(
+            self._h, layer, _dptr(q), _dptr(out), _i32p(ql), _i32p(cl), _u32p(ip), _u32p(ix) if ix.size else None,
+            cl.size, scale, flags, _stream_handle(stream)))
+        return out
+
     def qk_norm_rope_append(self, layer: int, q, k, v, positions, slot_mapping, q_norm_w=None,
                             k_norm_w=None, inv_freq=None, eps: float = 1e-6, gated: bool = True,
                             out=None, stream=None):
@@ -359,9 +463,18 @@ class DeviceKvPool:
         Weights None skips the norm; inv_freq None skips RoPE."""
         torch = _torch()
         d = self.desc
+        host = _is_host(slot_mapping)
+        if host != _is_host(positions):
+            raise BackendError(MKV_ERR_INVALID_ARGUMENT, "positions and slot_mapping must both be host or device")
+        if host:
+            slot_mapping, positions = _host_u32(slot_mapping, "slot_mapping"), _host_i32(positions)
         n = slot_mapping.shape[0]
-        self._i32(slot_mapping, "slot_mapping", n)
-        self._i32(positions, "positions", n)
+        if host:
+            if positions.size != n:
+                raise BackendError(MKV_ERR_INVALID_ARGUMENT, "positions and slot_mapping differ in length")
+        else:
+            self._i32(slot_mapping, "slot_mapping", n)
+            self._i32(positions, "positions", n)
         qshape = (n, d.num_q_heads, 2, d.head_dim) if gated else (n, d.num_q_heads, d.head_dim)
         self._check_tensor(q, qshape, "q")
         self._check_tensor(k, (n, d.num_kv_heads, d.head_dim), "k")
@@ -382,10 +495,12 @@ class DeviceKvPool:
             out = torch.empty((n, d.num_q_heads, d.head_dim), dtype=self.torch_dtype, device=q.device)
         self._check_tensor(out, (n, d.num_q_heads, d.head_dim), "out")
         nul = ctypes.c_void_p(0)
-        _raise(self._lib.mkv_qk_norm_rope_append(
+        fn = self._lib.mkv_qk_norm_rope_append_host if host else self._lib.mkv_qk_norm_rope_append
+        _raise(fn(
             self._h, layer, _dptr(q), _dptr(k), _dptr(v),
             nul if q_norm_w is None else _dptr(q_norm_w), nul if k_norm_w is None else _dptr(k_norm_w),
-            nul if inv_freq is None else _dptr(inv_freq), rd, eps, _dptr(positions), _dptr(slot_mapping),
+            nul if inv_freq is None else _dptr(inv_freq), rd, eps,
+            _i32p(positions) if host else _dptr(positions), _u32p(slot_mapping) if host else _dptr(slot_mapping),
             n, _dptr(out), flags, _stream_handle(stream)))
         return out
 
@@ -400,18 +515,27 @@ class DeviceKvPool:
         layers [layer_begin, layer_begin + num_layers) of each block, K and V,
         block-major, with the per-block sum64 checksum (mkv_wire_export)."""
         torch = _torch()
+        host = _is_host(block_ids)
+        if host:
+            block_ids = _host_u32(block_ids, "block_ids")
         n = block_ids.shape[0]
         nl = self.desc.num_layers - layer_begin if num_layers is None else num_layers
-        self._i32(block_ids, "block_ids", n)
+        if not host:
+            self._i32(block_ids, "block_ids", n)
+        dev = torch.device(f"cuda:{self.device}")
         nbytes = n * self.wire_block_bytes(nl)
         if payload is None:
-            payload = torch.empty(nbytes, dtype=torch.uint8, device=block_ids.device)
+            payload = torch.empty(nbytes, dtype=torch.uint8, device=dev)
         if checksums is None:
-            checksums = torch.empty(n, dtype=torch.int64, device=block_ids.device)
+            checksums = torch.empty(n, dtype=torch.int64, device=dev)
         self._check_tensor(payload, (nbytes,), "payload", dtype=torch.uint8)
         self._check_tensor(checksums, (n,), "checksums", dtype=torch.int64)
-        _raise(self._lib.mkv_wire_export(self._h, _dptr(block_ids), n, layer_begin, nl, _dptr(payload),
-                                         _dptr(checksums), _stream_handle(stream)))
+        if host:
+            _raise(self._lib.mkv_wire_export_host(self._h, _u32p(block_ids), n, layer_begin, nl, _dptr(payload),
+                                                  _dptr(checksums), _stream_handle(stream)))
+        else:
+            _raise(self._lib.mkv_wire_export(self._h, _dptr(block_ids), n, layer_begin, nl, _dptr(payload),
+                                             _dptr(checksums), _stream_handle(stream)))
         return payload, checksums
 
     def wire_import(self, block_ids, payload, layer_begin: int = 0, num_layers: int | None = None,
@@ -420,25 +544,33 @@ class DeviceKvPool:
         of the payload as received. With `expected`, a mismatch is reported by
         check() as DeviceIndexError with DEVERR_CHECKSUM."""
         torch = _torch()
+        host = _is_host(block_ids)
+        if host:
+            block_ids = _host_u32(block_ids, "block_ids")
         n = block_ids.shape[0]
         nl = self.desc.num_layers - layer_begin if num_layers is None else num_layers
-        self._i32(block_ids, "block_ids", n)
+        if not host:
+            self._i32(block_ids, "block_ids", n)
         self._check_tensor(payload, (n * self.wire_block_bytes(nl),), "payload", dtype=torch.uint8)
         if expected is not None:
             self._check_tensor(expected, (n,), "expected", dtype=torch.int64)
         if checksums is None:
-            checksums = torch.empty(n, dtype=torch.int64, device=block_ids.device)
+            checksums = torch.empty(n, dtype=torch.int64, device=payload.device)
         self._check_tensor(checksums, (n,), "checksums", dtype=torch.int64)
-        _raise(self._lib.mkv_wire_import(self._h, _dptr(block_ids), n, layer_begin, nl, _dptr(payload),
-                                         ctypes.c_void_p(0) if expected is None else _dptr(expected),
-                                         _dptr(checksums), _stream_handle(stream)))
+        fn = self._lib.mkv_wire_import_host if host else self._lib.mkv_wire_import
+        _raise(fn(self._h, _u32p(block_ids) if host else _dptr(block_ids), n, layer_begin, nl, _dptr(payload),
+                  ctypes.c_void_p(0) if expected is None else _dptr(expected),
+                  _dptr(checksums), _stream_handle(stream)))
         return checksums
 
-    def plan(self, ctx_lens, pieces: int = 0, stream=None) -> "DecodePlan":
+    def plan(self, ctx_lens, pieces: int = 0, stream=None, block_indptr=None, block_ids=None) -> "DecodePlan":
         """Work plan of one decode step from host context lengths (tokens
-        attended per sequence, including the token appended this step)."""
+        attended per sequence, including the token appended this step). With
+        the batch's host page tables (u32 CSR block_indptr / block_ids) the
+        plan holds them (mkv_decode_plan_build_tables) and the step's calls
+        pass no tables."""
         p = DecodePlan(self)
-        p.build(ctx_lens, pieces, stream)
+        p.build(ctx_lens, pieces, stream, block_indptr, block_ids)
         return p
 
     def plan_suffixes(self, suffix_lens, pieces: int = 0, stream=None) -> "DecodePlan":
@@ -447,6 +579,14 @@ class DeviceKvPool:
         decode_step_shared_prefix."""
         p = DecodePlan(self, suffixes=True)
         p.build(suffix_lens, pieces, stream)
+        return p
+
+    def plan_shared_prefix(self, prefix_ids, suffix_lens, block_indptr, block_ids, pieces: int = 0,
+                           stream=None) -> "DecodePlan":
+        """plan_suffixes holding the host tables of the suffixes and the
+        prefix's u32 block ids (mkv_decode_plan_build_shared_prefix)."""
+        p = DecodePlan(self, suffixes=True)
+        p.build(suffix_lens, pieces, stream, block_indptr, block_ids, prefix_ids)
         return p
 
     def decode_step_shared_prefix(self, layer: int, plan, k_new, v_new, q, prefix_ids, block_indptr, block_ids,
@@ -460,7 +600,10 @@ class DeviceKvPool:
         if not getattr(plan, "suffixes", False):
             raise BackendError(MKV_ERR_INVALID_ARGUMENT, "the plan must come from plan_suffixes")
         out, scale, flags = self._planned_args(plan, q, block_indptr, block_ids, out, scale, zero_sink, kernel)
-        self._i32(prefix_ids, "prefix_ids")
+        if prefix_ids is not None:
+            self._i32(prefix_ids, "prefix_ids")
+        elif not plan.has_prefix:
+            raise BackendError(MKV_ERR_INVALID_ARGUMENT, "no prefix ids: pass them, or plan with plan_shared_prefix")
         B = plan.num_seqs
         if (k_new is None) != (v_new is None):
             raise ValueError("give both k_new and v_new, or neither")
@@ -469,8 +612,9 @@ class DeviceKvPool:
             self._check_tensor(v_new, (B, d.num_kv_heads, d.head_dim), "v_new")
         _raise(self._lib.mkv_decode_step_shared_prefix(
             self._h, plan._h, layer, _dptr(k_new) if k_new is not None else None,
-            _dptr(v_new) if v_new is not None else None, _dptr(q), _dptr(out), _dptr(prefix_ids),
-            int(prefix_ids.shape[0]), _dptr(block_indptr), _dptr(block_ids), scale, flags, _stream_handle(stream)))
+            _dptr(v_new) if v_new is not None else None, _dptr(q), _dptr(out), _tptr(prefix_ids),
+            0 if prefix_ids is None else int(prefix_ids.shape[0]), _tptr(block_indptr), _tptr(block_ids), scale,
+            flags, _stream_handle(stream)))
         return out
 
     def _planned_args(self, plan, q, block_indptr, block_ids, out, scale, zero_sink, kernel, cached_loads=False):
@@ -479,8 +623,14 @@ class DeviceKvPool:
             raise BackendError(MKV_ERR_INVALID_ARGUMENT, "plan belongs to another pool")
         B = plan.num_seqs
         self._check_tensor(q, (B, d.num_q_heads, d.head_dim), "q")
-        self._i32(block_indptr, "block_indptr", B + 1)
-        self._i32(block_ids, "block_ids")
+        if (block_indptr is None) != (block_ids is None):
+            raise BackendError(MKV_ERR_INVALID_ARGUMENT, "give both device table tensors, or neither")
+        if block_indptr is None:
+            if not plan.has_tables:
+                raise BackendError(MKV_ERR_INVALID_ARGUMENT, "no tables: pass device tables, or plan with host tables")
+        else:
+            self._i32(block_indptr, "block_indptr", B + 1)
+            self._i32(block_ids, "block_ids")
         torch = _torch()
         if out is None:
             out = torch.empty_like(q)
@@ -508,7 +658,7 @@ class DeviceKvPool:
         out, scale, flags = self._planned_args(plan, q, block_indptr, block_ids, out, scale, zero_sink, kernel,
                                                cached_loads)
         _raise(self._lib.mkv_decode_attention_planned(
-            self._h, plan._h, layer, _dptr(q), _dptr(out), _dptr(block_indptr), _dptr(block_ids),
+            self._h, plan._h, layer, _dptr(q), _dptr(out), _tptr(block_indptr), _tptr(block_ids),
             scale, flags, _stream_handle(stream)))
         return out
 
@@ -525,7 +675,7 @@ class DeviceKvPool:
         self._check_tensor(v_new, (B, d.num_kv_heads, d.head_dim), "v_new")
         _raise(self._lib.mkv_decode_step(
             self._h, plan._h, layer, _dptr(k_new), _dptr(v_new), _dptr(q), _dptr(out),
-            _dptr(block_indptr), _dptr(block_ids), scale, flags, _stream_handle(stream)))
+            _tptr(block_indptr), _tptr(block_ids), scale, flags, _stream_handle(stream)))
         return out
 
     def bind_decode_step(self, plan, k_new, v_new, q, block_indptr, block_ids, out,
@@ -549,7 +699,7 @@ class DeviceKvPool:
         kv_stride = B * d.num_kv_heads * d.head_dim * d.elem_bytes
         qo_stride = B * d.num_q_heads * d.head_dim * d.elem_bytes
         kb, vb, qb, ob = k_new.data_ptr(), v_new.data_ptr(), q.data_ptr(), out.data_ptr()
-        ip, ix = _dptr(block_indptr), _dptr(block_ids)
+        ip, ix = _tptr(block_indptr), _tptr(block_ids)
         args = [(h, ph, layer, ctypes.c_void_p(kb + layer * kv_stride), ctypes.c_void_p(vb + layer * kv_stride),
                  ctypes.c_void_p(qb + layer * qo_stride), ctypes.c_void_p(ob + layer * qo_stride), ip, ix,
                  scale, flags, sh) for layer in range(L)]
@@ -575,14 +725,17 @@ class DeviceKvPool:
         self._check_tensor(v_new, (L, B, d.num_kv_heads, d.head_dim), "v_new")
         self._check_tensor(q, (L, B, d.num_q_heads, d.head_dim), "q")
         self._check_tensor(out, (L, B, d.num_q_heads, d.head_dim), "out")
-        self._i32(prefix_ids, "prefix_ids")
+        if prefix_ids is not None:
+            self._i32(prefix_ids, "prefix_ids")
+        elif not plan.has_prefix:
+            raise BackendError(MKV_ERR_INVALID_ARGUMENT, "no prefix ids: pass them, or plan with plan_shared_prefix")
         _, scale, flags = self._planned_args(plan, q[0], block_indptr, block_ids, out[0], scale, zero_sink, None)
         fn = self._lib.mkv_decode_step_shared_prefix
         kv_stride = B * d.num_kv_heads * d.head_dim * d.elem_bytes
         qo_stride = B * d.num_q_heads * d.head_dim * d.elem_bytes
         kb, vb, qb, ob = k_new.data_ptr(), v_new.data_ptr(), q.data_ptr(), out.data_ptr()
-        pre, npre = _dptr(prefix_ids), int(prefix_ids.shape[0])
-        ip, ix, sh = _dptr(block_indptr), _dptr(block_ids), _stream_handle(stream)
+        pre, npre = _tptr(prefix_ids), 0 if prefix_ids is None else int(prefix_ids.shape[0])
+        ip, ix, sh = _tptr(block_indptr), _tptr(block_ids), _stream_handle(stream)
         args = [(self._h, plan._h, layer, ctypes.c_void_p(kb + layer * kv_stride),
                  ctypes.c_void_p(vb + layer * kv_stride), ctypes.c_void_p(qb + layer * qo_stride),
                  ctypes.c_void_p(ob + layer * qo_stride), pre, npre, ip, ix, scale, flags, sh) for layer in range(L)]
@@ -648,13 +801,43 @@ class DecodePlan:
         _raise(self._lib.mkv_decode_plan_create(pool._h, ctypes.byref(h)))
         self._h = h
         self.num_seqs = 0
+        self.has_tables = False
+        self.has_prefix = False
 
-    def build(self, ctx_lens, pieces: int = 0, stream=None) -> None:
-        c = np.ascontiguousarray(ctx_lens, np.int32)
-        self._ctx = c  # the upload is asynchronous; keep the host copy alive
-        fn = self._lib.mkv_decode_plan_build_suffixes if self.suffixes else self._lib.mkv_decode_plan_build
-        _raise(fn(self._h, _i32p(c), c.size, pieces, _stream_handle(stream)))
+    def build(self, ctx_lens, pieces: int = 0, stream=None, block_indptr=None, block_ids=None,
+              prefix_ids=None) -> None:
+        """ctx_lens: host lengths. block_indptr / block_ids: the batch's host
+        page tables (u32 CSR), held by the plan; prefix_ids: a shared prefix's
+        host block ids (suffix plans only). The library copies them before
+        returning."""
+        c = _host_i32(ctx_lens)
+        sh = _stream_handle(stream)
+        if (block_indptr is None) != (block_ids is None):
+            raise BackendError(MKV_ERR_INVALID_ARGUMENT, "give both block_indptr and block_ids, or neither")
+        if block_indptr is None:
+            if prefix_ids is not None:
+                raise BackendError(MKV_ERR_INVALID_ARGUMENT, "prefix ids need the suffix tables")
+            fn = self._lib.mkv_decode_plan_build_suffixes if self.suffixes else self._lib.mkv_decode_plan_build
+            _raise(fn(self._h, _i32p(c), c.size, pieces, sh))
+        else:
+            ip, ix = _host_u32(block_indptr, "block_indptr"), _host_u32(block_ids, "block_ids")
+            if ip.size != c.size + 1:
+                raise BackendError(MKV_ERR_INVALID_ARGUMENT, "block_indptr must have num_seqs + 1 entries")
+            ixp = _u32p(ix) if ix.size else None
+            if self.suffixes:
+                if prefix_ids is None:
+                    raise BackendError(MKV_ERR_INVALID_ARGUMENT, "a suffix plan with tables needs the prefix ids")
+                pre = _host_u32(prefix_ids, "prefix_ids")
+                _raise(self._lib.mkv_decode_plan_build_shared_prefix(
+                    self._h, _u32p(pre), pre.size, _i32p(c), _u32p(ip), ixp, c.size, pieces, sh))
+            else:
+                if prefix_ids is not None:
+                    raise BackendError(MKV_ERR_INVALID_ARGUMENT, "prefix ids belong to a suffix plan")
+                _raise(self._lib.mkv_decode_plan_build_tables(self._h, _i32p(c), _u32p(ip), ixp, c.size, pieces,
+                                                              sh))
         self.num_seqs = int(c.size)
+        self.has_tables = block_indptr is not None
+        self.has_prefix = prefix_ids is not None
 
     def info(self):
         p, bp, m = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()

@@ -486,6 +486,29 @@ ORC_API int orc_ref_faithful_decode(float **kcache, float **vcache, int64_t T, i
   return 0;
 }
 
+/* orc_ref_faithful_decode on malloc'd copies of the caller's caches
+ * ([Hkv][T][D] each), which it grows and frees as the reference does; the
+ * caller's arrays are unchanged. For the tests that check the baseline
+ * against orc_decode_attention_f32. */
+ORC_API int orc_ref_faithful_decode_copy(const float *kcache, const float *vcache, int64_t T, int32_t Hkv,
+                                         int32_t Hq, int32_t D, const float *k_new, const float *v_new,
+                                         const float *q, float scale, float *out) {
+  const size_t n = (size_t)Hkv * (size_t)(T > 0 ? T : 1) * (size_t)D;
+  float *kc = (float *)malloc(sizeof(float) * n);
+  float *vc = (float *)malloc(sizeof(float) * n);
+  if (!kc || !vc) {
+    free(kc);
+    free(vc);
+    return -1;
+  }
+  memcpy(kc, kcache, sizeof(float) * (size_t)Hkv * (size_t)T * (size_t)D);
+  memcpy(vc, vcache, sizeof(float) * (size_t)Hkv * (size_t)T * (size_t)D);
+  const int rc = orc_ref_faithful_decode(&kc, &vc, T, Hkv, Hq, D, k_new, v_new, q, scale, out);
+  free(kc);
+  free(vc);
+  return rc;
+}
+
 /* Thread count the OpenMP runtime will use (1 without OpenMP). */
 ORC_API int orc_num_threads(void) {
 #ifdef _OPENMP

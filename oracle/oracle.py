@@ -68,6 +68,7 @@ def lib():
                                                         f64, ctypes.c_int, P]),
             "orc_ref_faithful_decode": (ctypes.c_int, [P, P, i64, i32, i32, i32, P, P, P, f32, P]),
             "orc_ref_faithful_batch": (ctypes.c_double, [P, i32, i32, i32, i32, ctypes.c_uint64]),
+            "orc_ref_faithful_decode_copy": (ctypes.c_int, [P, P, i64, i32, i32, i32, P, P, P, f32, P]),
             "orc_num_threads": (ctypes.c_int, []),
             "orc_set_num_threads": (None, [ctypes.c_int]),
         }
@@ -305,6 +306,24 @@ def ref_faithful_batch(ctx, Hkv: int, Hq: int, D: int, seed: int = 1) -> float:
     sequence; ctx[b] counts the appended token."""
     c = np.ascontiguousarray(ctx, np.int32)
     return lib().orc_ref_faithful_batch(_p(c), c.size, Hkv, Hq, D, ctypes.c_uint64(seed))
+
+
+def ref_faithful_decode(kcache: np.ndarray, vcache: np.ndarray, k_new: np.ndarray, v_new: np.ndarray,
+                        q: np.ndarray, scale: float | None = None) -> np.ndarray:
+    """The timed CPU baseline's decode of one sequence (contiguous caches
+    [Hkv, T, D] grown by a copy, repeat_kv materialised, mask, softmax, two
+    matmuls: model.rs:390-416). Returns o [Hq, D]."""
+    kc, vc = np.ascontiguousarray(kcache, np.float32), np.ascontiguousarray(vcache, np.float32)
+    Hkv, T, D = kc.shape
+    q = np.ascontiguousarray(q, np.float32)
+    Hq = q.shape[0]
+    kn, vn = np.ascontiguousarray(k_new, np.float32), np.ascontiguousarray(v_new, np.float32)
+    if scale is None:
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    out = np.empty((Hq, D), np.float32)
+    if lib().orc_ref_faithful_decode_copy(_p(kc), _p(vc), T, Hkv, Hq, D, _p(kn), _p(vn), _p(q), scale, _p(out)):
+        raise MemoryError("orc_ref_faithful_decode_copy")
+    return out
 
 
 def num_threads() -> int:

@@ -19,13 +19,15 @@ from tests.helpers import assert_attention_close, bits, normal, odesc, to_device
 pytestmark = pytest.mark.gpu
 
 SHAPES = {
-    # name: (Hq, Hkv, D): query heads per KV head G = 7, 8, 7, 4, 16, 1
+    # name: (Hq, Hkv, D): query heads per KV head G = 7, 8, 7, 4, 16, 1, 4, 16
     "qwen7b": (28, 4, 128),
     "gemma2b": (8, 1, 256),
     "qwen0.5b": (14, 2, 64),
     "llama8b": (32, 8, 128),
     "g16": (64, 4, 128),
     "mha": (4, 4, 64),
+    "d256-g4": (16, 4, 256),   # head_dim 256 with 4 waves per workgroup
+    "d256-g16": (16, 1, 256),  # head_dim 256 with 16 waves per workgroup
 }
 # Shapes the MFMA tile kernel does not take (per-token segments instead).
 SEGMENT_SHAPES = {

@@ -23,6 +23,8 @@ SHAPES = {
     "qwen0.5b": (1, 14, 2, 64),
     "llama8b": (1, 32, 8, 128),  # suffixes on the per-head stream kernel
     "g16": (1, 64, 4, 128),
+    "d256-g4": (1, 16, 4, 256),   # head_dim 256: 4-wave prefix workgroups, 4 KV heads per suffix workgroup
+    "d256-g16": (1, 16, 1, 256),  # head_dim 256: 16-wave prefix workgroups, per-head suffix kernel
 }
 
 

@@ -247,6 +247,63 @@ def test_fork_then_copy_on_write_of_shared_partial_block():
     bm.check_invariants()
 
 
+def test_fork_before_the_prompt_is_written_gives_private_blocks():
+    """Admission reserves ceil(n/16) blocks; a fork made before any of them is
+    written shares them all. Each sequence's append must then write only
+    blocks it alone holds, and nothing needs copying (no rows exist yet)."""
+    bm = BlockManager(16, 16)
+    bm.admit(1, _tokens(21, 40))
+    bm.fork(1, 2)
+    assert all(bm.refcount(b) == 2 for b in bm.table(1))
+    s1, c1 = bm.append(1, 40)
+    s2, c2 = bm.append(2, 40)
+    assert c1 == [] and c2 == []
+    assert set(s1.tolist()).isdisjoint(s2.tolist())
+    for s in (s1, s2):
+        assert all(bm.refcount(int(x) // 16) == 1 for x in s)
+    assert set(bm.table(1).tolist()).isdisjoint(bm.table(2).tolist())
+    bm.check_invariants()
+
+
+def test_fork_during_prefill_copies_only_the_partial_block():
+    """Fork after 20 of 40 prompt tokens: block 0 is full (shared, never
+    written again), block 1 holds 4 rows (copy on write), block 2 holds none
+    (a fresh private block, no copy)."""
+    bm = BlockManager(16, 16)
+    bm.admit(1, _tokens(22, 40))
+    bm.append(1, 20)
+    t = bm.table(1).copy()
+    bm.fork(1, 2)
+    s2, c2 = bm.append(2, 20)
+    assert c2 == [(int(t[1]), int(bm.table(2)[1]))]
+    t2 = bm.table(2)
+    assert t2[0] == t[0] and t2[1] != t[1] and t2[2] != t[2]
+    s1, c1 = bm.append(1, 20)  # now the last holder of blocks 1 and 2: in place
+    assert c1 == [] and list(bm.table(1)) == list(t)
+    assert set(s1.tolist()).isdisjoint(s2.tolist())
+    assert bm.refcount(int(t[0])) == 2
+    bm.check_invariants()
+
+
+def test_compaction_without_outputs_is_refused_and_changes_nothing():
+    import ctypes
+
+    from mitten_amd import host as hm
+
+    bm = BlockManager(40, 16)
+    for s in range(6):
+        bm.admit(s, _tokens(30 + s, 40))
+        bm.append(s, 40)
+    bm.release(1)
+    tables = {s: bm.table(s).copy() for s in (0, 2, 3, 4, 5)}
+    n = ctypes.c_int64()
+    st = hm._lib_h().mkvh_bm_plan_compaction(bm._h, None, None, 40, ctypes.byref(n))
+    assert st != 0 and b"out_src" in hm._lib_h().mkvh_last_error()
+    for s, t in tables.items():
+        assert list(bm.table(s)) == list(t)
+    bm.check_invariants()
+
+
 def test_compaction_moves_tail_blocks_into_holes():
     bm = BlockManager(40, 16)
     for s in range(8):
@@ -325,10 +382,19 @@ def test_random_lifecycle_keeps_invariants():
             next_id += 1
         elif op == 1:
             s = int(rng.choice(sorted(live)))
+            if rng.integers(0, 3) == 0:  # fork it, then let either side write
+                c = next_id
+                bm.fork(s, c)
+                prompts[c] = prompts[s]
+                live.add(c)
+                next_id += 1
+                s = int(rng.choice([s, c]))
             try:
-                bm.append(s, int(rng.integers(1, 20)))
+                slots, _ = bm.append(s, int(rng.integers(1, 20)))
             except OutOfBlocks:
                 pass
+            else:  # every block written is held by the writer alone
+                assert all(bm.refcount(int(x) // 16) == 1 for x in slots)
         elif op == 2:
             s = int(rng.choice(sorted(live)))
             bm.promote(s, prompts[s])

@@ -476,3 +476,53 @@ def test_extend_checks_detect_planted_mistakes():
     }
     for name, w in wrong.items():
         assert np.max(np.abs(good - w)) > 1e-3, name
+
+
+# ---------------------------------------------- the timed CPU baseline ----
+
+@pytest.mark.parametrize("Hq,Hkv,D", [(14, 2, 64), (28, 4, 128), (8, 1, 256)])
+@pytest.mark.parametrize("T", [0, 1, 16, 999, 16384])
+def test_ref_faithful_baseline_matches_the_oracle(Hq, Hkv, D, T):
+    """The reference-faithful restatement timed as the CPU baseline (a
+    contiguous cache grown by a copy, repeat_kv, mask, softmax, two matmuls)
+    computes the same attention as the parity oracle: the cache laid out in
+    pool blocks with the new token appended, decoded over T + 1 tokens,
+    within 1e-5 (f32). Context lengths 1 .. 16k + 1 at the three
+    configurations' head shapes (model.rs:390-416)."""
+    rng = np.random.default_rng(T * 7 + D)
+    kc = rng.standard_normal((Hkv, T, D), dtype=np.float32)
+    vc = rng.standard_normal((Hkv, T, D), dtype=np.float32)
+    kn = rng.standard_normal((Hkv, D), dtype=np.float32)
+    vn = rng.standard_normal((Hkv, D), dtype=np.float32)
+    q = rng.standard_normal((Hq, D), dtype=np.float32)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    got = orc.ref_faithful_decode(kc, vc, kn, vn, q, scale)
+    T1 = T + 1
+    nb = (T1 + 15) // 16
+    k_all = np.zeros((Hkv, nb * 16, D), np.float32)
+    v_all = np.zeros((Hkv, nb * 16, D), np.float32)
+    k_all[:, :T], k_all[:, T] = kc, kn
+    v_all[:, :T], v_all[:, T] = vc, vn
+    pool = np.empty((1, 2, nb, 16, Hkv, D), np.float32)
+    pool[0, 0] = k_all.reshape(Hkv, nb, 16, D).transpose(1, 2, 0, 3)
+    pool[0, 1] = v_all.reshape(Hkv, nb, 16, D).transpose(1, 2, 0, 3)
+    perm = np.random.default_rng(T).permutation(nb).astype(np.int32)  # a shuffled table over shuffled blocks
+    shuffled = np.empty_like(pool)
+    shuffled[0, :, perm] = pool[0, :, np.arange(nb)]
+    d = orc.desc(1, Hkv, D, nb, 4)
+    ref = orc.decode_attention(d, shuffled, 0, q[None], np.array([0, nb], np.int32), perm,
+                               np.array([T1], np.int32), scale=scale)[0]
+    assert np.max(np.abs(got - ref)) <= 1e-5
+
+
+def test_ref_faithful_baseline_planted_mistake_fails():
+    """The check above catches a baseline that drops the appended token:
+    attending over the old cache only moves the result far past 1e-5."""
+    rng = np.random.default_rng(3)
+    Hq, Hkv, D, T = 28, 4, 128, 40
+    kc, vc = rng.standard_normal((Hkv, T, D), dtype=np.float32), rng.standard_normal((Hkv, T, D), dtype=np.float32)
+    kn, vn = rng.standard_normal((Hkv, D), dtype=np.float32), rng.standard_normal((Hkv, D), dtype=np.float32)
+    q = rng.standard_normal((Hq, D), dtype=np.float32)
+    full = orc.ref_faithful_decode(kc, vc, kn, vn, q)
+    dropped = orc.ref_faithful_decode(kc[:, :-1], vc[:, :-1], kc[:, -1], vc[:, -1], q)
+    assert np.max(np.abs(full - dropped)) > 1e-2
