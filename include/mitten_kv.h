@@ -202,6 +202,24 @@ MKV_API int mkv_decode_attention_workspace_size(const mkv_pool *pool, int32_t nu
                                         int32_t max_ctx_len, int32_t split_tokens,
                                         uint64_t *out_bytes);
 
+/* mkv_decode_attention without any allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments and results as mkv_decode_attention with a
+ * caller workspace, except that the split-K partials live in a static device
+ * array of MKV_STATIC_SCRATCH_BYTES that the library holds on each GPU it
+ * runs on until the process ends (its address is looked up when the first
+ * pool is created on that GPU). It calls no hipMalloc / hipFree. With
+ * split_tokens = 0 the split is the library's choice, reduced until its
+ * partials fit the array; an explicit split_tokens whose partials do not fit
+ * is refused (MKV_ERR_INVALID_ARGUMENT). Every call on one GPU shares the
+ * array: calls that overlap on one GPU (other streams or threads) race. */
+#define MKV_STATIC_SCRATCH_BYTES (64ull << 20)
+MKV_API int mkv_decode_attention_static(mkv_pool *pool, int32_t layer, const void *d_q, void *d_o,
+                                        const int32_t *d_block_indptr, const int32_t *d_block_ids,
+                                        const int32_t *d_ctx_lens, int32_t num_seqs, int32_t max_ctx_len,
+                                        float scale, uint32_t flags, int32_t split_tokens, void *stream);
+
 /* ---- host metadata (the engine's u32 form) ------------------------------- */
 
 /* mkv_append with a host slot mapping (slot = page * page_size + offset, as

@@ -67,6 +67,7 @@ DEVICE_SIGNATURES = {
     "mkv_copy_blocks": (c_int, [P, P, P, i32, P]),
     "mkv_decode_attention": (c_int, [P, i32, P, P, P, P, P, i32, i32, f32, u32, i32, P, u64, P]),
     "mkv_decode_attention_workspace_size": (c_int, [P, i32, i32, i32, ctypes.POINTER(u64)]),
+    "mkv_decode_attention_static": (c_int, [P, i32, P, P, P, P, P, i32, i32, f32, u32, i32, P]),
     "mkv_decode_plan_create": (c_int, [P, ctypes.POINTER(P)]),
     "mkv_decode_plan_destroy": (c_int, [P]),
     "mkv_decode_plan_build": (c_int, [P, I32P, i32, i32, P]),

@@ -35,6 +35,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <vector>
 
@@ -1808,14 +1809,15 @@ extern "C" int mkv_decode_attention_workspace_size(const mkv_pool *pool, int32_t
   return MKV_OK;
 }
 
-extern "C" int mkv_decode_attention(mkv_pool *pool, int32_t layer, const void *d_q, void *d_o,
-                                    const int32_t *d_block_indptr, const int32_t *d_block_ids,
-                                    const int32_t *d_ctx_lens, int32_t num_seqs,
-                                    int32_t max_ctx_len, float scale, uint32_t flags,
-                                    int32_t split_tokens, void *d_workspace,
-                                    uint64_t workspace_bytes, void *stream) {
-  if (!pool) return set_error(MKV_ERR_INVALID_ARGUMENT, "pool is NULL");
-  Pool *p = reinterpret_cast<Pool *>(pool);
+// The split-grid decode of mkv_decode_attention. ws / ws_bytes: the
+// caller's workspace, or NULL to use (and grow) the pool-owned one; with
+// fixed_ws the given buffer is the only one and nothing is allocated: an
+// automatic split count shrinks until its partials fit, and an explicit one
+// whose partials do not fit is refused.
+static int decode_split(Pool *p, int32_t layer, const void *d_q, void *d_o, const int32_t *d_block_indptr,
+                        const int32_t *d_block_ids, const int32_t *d_ctx_lens, int32_t num_seqs, int32_t max_ctx_len,
+                        float scale, uint32_t flags, int32_t split_tokens, void *ws, uint64_t ws_bytes, bool fixed_ws,
+                        void *stream) {
   const Geom &g = p->g;
   bool use_mfma = false;
   int rc = check_common(p, layer, flags, scale, use_mfma);
@@ -1830,17 +1832,27 @@ extern "C" int mkv_decode_attention(mkv_pool *pool, int32_t layer, const void *d
     return set_error(MKV_ERR_INVALID_ARGUMENT, "q and o must be 16-byte aligned");
   if (split_tokens < 0 || split_tokens % kPageSize)
     return set_error(MKV_ERR_INVALID_ARGUMENT, "split_tokens must be a multiple of %d", kPageSize);
-  const int st = split_tokens ? split_tokens : choose_split(g, num_seqs, max_ctx_len);
-  const int S = (max_ctx_len + st - 1) / st;
-  const uint64_t need = split_ws_bytes(g, num_seqs, S);
+  int st = split_tokens ? split_tokens : choose_split(g, num_seqs, max_ctx_len);
+  int S = (max_ctx_len + st - 1) / st;
+  uint64_t need = split_ws_bytes(g, num_seqs, S);
+  if (fixed_ws && need > ws_bytes) {
+    if (split_tokens)
+      return set_error(MKV_ERR_INVALID_ARGUMENT, "split-K partials of %llu bytes exceed the %llu-byte scratch",
+                       (unsigned long long)need, (unsigned long long)ws_bytes);
+    while (S > 1 && need > ws_bytes) {  // fewer, longer splits until the partials fit (S = 1 needs none)
+      S = (S + 1) / 2;
+      st = ((max_ctx_len + S - 1) / S + kPageSize - 1) / kPageSize * kPageSize;
+      S = (max_ctx_len + st - 1) / st;
+      need = split_ws_bytes(g, num_seqs, S);
+    }
+  }
   DeviceGuard guard(p->device);
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
-  void *ws = d_workspace;
   if (need) {
     if (ws) {
-      if (workspace_bytes < need)
+      if (ws_bytes < need)
         return set_error(MKV_ERR_INVALID_ARGUMENT, "workspace of %llu bytes < %llu needed",
-                         (unsigned long long)workspace_bytes, (unsigned long long)need);
+                         (unsigned long long)ws_bytes, (unsigned long long)need);
     } else {
       if (p->ws_bytes < need) {
         MKV_CHECK_HIP(hipStreamSynchronize(hs));  // earlier launches may read the old buffer
@@ -1875,6 +1887,67 @@ extern "C" int mkv_decode_attention(mkv_pool *pool, int32_t layer, const void *d
     MKV_CHECK_LAUNCH("merge_split_kernel");
   }
   return MKV_OK;
+}
+
+extern "C" int mkv_decode_attention(mkv_pool *pool, int32_t layer, const void *d_q, void *d_o,
+                                    const int32_t *d_block_indptr, const int32_t *d_block_ids,
+                                    const int32_t *d_ctx_lens, int32_t num_seqs,
+                                    int32_t max_ctx_len, float scale, uint32_t flags,
+                                    int32_t split_tokens, void *d_workspace,
+                                    uint64_t workspace_bytes, void *stream) {
+  if (!pool) return set_error(MKV_ERR_INVALID_ARGUMENT, "pool is NULL");
+  return decode_split(reinterpret_cast<Pool *>(pool), layer, d_q, d_o, d_block_indptr, d_block_ids, d_ctx_lens,
+                      num_seqs, max_ctx_len, scale, flags, split_tokens, d_workspace, workspace_bytes, false,
+                      stream);
+}
+
+// ---- C ABI: split grid without allocation ------------------------------------------
+//
+// mkv_decode_attention_static keeps its split-K partials in `scratch`, a
+// file-scope device array: each GPU holds its own copy (kStaticScratchBytes)
+// from the moment the library's code is loaded on it until the process
+// ends. In host code `scratch` names a host-side stand-in, not the device
+// memory: its device address on each GPU comes from hipGetSymbolAddress,
+// looked up once per device when the first pool is created there (with that
+// device current) and kept in g_scratch, and only that address is passed to
+// the kernels. No partial needs to start at zero: the split kernel writes
+// every partial the merge then reads. Calls on one GPU share the array, so
+// calls that overlap on one GPU (other streams, other threads) race.
+
+constexpr uint64_t kStaticScratchBytes = MKV_STATIC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+static void *g_scratch[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+int mkv::static_scratch_setup(int device) {
+  if (device < 0 || device >= kMaxDevices)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "device %d beyond the %d this library tracks", device, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[device]) return MKV_OK;
+  DeviceGuard guard(device);
+  if (!guard.ok) return set_error(MKV_ERR_HIP, "hipSetDevice(%d) failed", device);
+  void *ptr = nullptr;
+  MKV_CHECK_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+  if (!ptr) return set_error(MKV_ERR_HIP, "hipGetSymbolAddress returned NULL for the static scratch");
+  g_scratch[device] = ptr;
+  return MKV_OK;
+}
+
+extern "C" int mkv_decode_attention_static(mkv_pool *pool, int32_t layer, const void *d_q, void *d_o,
+                                           const int32_t *d_block_indptr, const int32_t *d_block_ids,
+                                           const int32_t *d_ctx_lens, int32_t num_seqs, int32_t max_ctx_len,
+                                           float scale, uint32_t flags, int32_t split_tokens, void *stream) {
+  if (!pool) return set_error(MKV_ERR_INVALID_ARGUMENT, "pool is NULL");
+  Pool *p = reinterpret_cast<Pool *>(pool);
+  void *ws = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (p->device >= 0 && p->device < kMaxDevices) ws = g_scratch[p->device];
+  }
+  if (!ws) return set_error(MKV_ERR_HIP, "the static scratch of device %d was not set up", p->device);
+  return decode_split(p, layer, d_q, d_o, d_block_indptr, d_block_ids, d_ctx_lens, num_seqs, max_ctx_len, scale,
+                      flags, split_tokens, ws, kStaticScratchBytes, true, stream);
 }
 
 // ---- C ABI: plan --------------------------------------------------------------------

@@ -63,6 +63,10 @@ int meta_upload(MetaSlot *s, size_t n, hipStream_t hs);
 int meta_release(MetaSlot *s, hipStream_t hs);
 void meta_free(Pool *p);
 
+// Looks up this device's address of the static scratch of
+// mkv_decode_attention_static (once per device; called by mkv_pool_create).
+int static_scratch_setup(int device);
+
 // Host-side checks of the engine's u32 metadata against the pool (pure CPU).
 int check_host_slots(const Geom &g, const uint32_t *slots, int32_t n);
 // Tables of num_seqs sequences: indptr monotone from 0, every id < nblocks,

@@ -329,6 +329,8 @@ extern "C" int mkv_pool_create(const mkv_pool_desc *desc, int device, mkv_pool *
     return set_error(MKV_ERR_INVALID_ARGUMENT, "device %d out of range (%d devices)", device, ndev);
   DeviceGuard guard(device);
   if (!guard.ok) return set_error(MKV_ERR_HIP, "hipSetDevice(%d) failed", device);
+  int rs = static_scratch_setup(device);  // once per device: the no-allocation entry point's scratch
+  if (rs) return rs;
   Pool *p = new (std::nothrow) Pool();
   if (!p) return set_error(MKV_ERR_OUT_OF_MEMORY, "host allocation failed");
   p->desc = *desc;

@@ -403,6 +403,35 @@ class DeviceKvPool:
             _stream_handle(stream)))
         return out
 
+    def decode_attention_static(self, layer: int, q, block_indptr, block_ids, ctx_lens, max_ctx_len: int,
+                                scale: float | None = None, zero_sink: bool = False, out=None,
+                                split_tokens: int = 0, kernel: str | None = None, stream=None):
+        """decode_attention with its split-K partials in the library's static
+        device scratch (mkv_decode_attention_static): nothing is allocated."""
+        torch = _torch()
+        d = self.desc
+        B = q.shape[0]
+        self._check_tensor(q, (B, d.num_q_heads, d.head_dim), "q")
+        self._i32(block_indptr, "block_indptr", B + 1)
+        self._i32(block_ids, "block_ids")
+        self._i32(ctx_lens, "ctx_lens", B)
+        if out is None:
+            out = torch.empty_like(q)
+        self._check_tensor(out, (B, d.num_q_heads, d.head_dim), "out")
+        if scale is None:
+            scale = float(np.float32(d.head_dim ** -0.5))
+        flags = ATTN_ZERO_SINK if zero_sink else 0
+        if kernel == "valu":
+            flags |= ATTN_FORCE_VALU
+        elif kernel == "mfma":
+            flags |= ATTN_FORCE_MFMA
+        elif kernel is not None:
+            raise ValueError(f"unknown kernel {kernel!r}")
+        _raise(self._lib.mkv_decode_attention_static(
+            self._h, layer, _dptr(q), _dptr(out), _dptr(block_indptr), _dptr(block_ids), _dptr(ctx_lens), B,
+            max_ctx_len, scale, flags, split_tokens, _stream_handle(stream)))
+        return out
+
     # -- planned path -------------------------------------------------------------------------
     def extend_attention(self, layer: int, q, q_indptr, block_indptr, block_ids, ctx_lens,
                          max_q_len: int, max_ctx_len: int, out=None, scale: float | None = None,
