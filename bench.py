@@ -15,6 +15,13 @@ timed on a bounded sample on this host).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 
+The default run also measures the other configurations, each on its own
+pool at full size, and nests their figures under "configs" (step time,
+GB/s, % of peak, roofline, traffic source): the f32 Qwen2.5-0.5B step with
+its block-table gather, the Gemma-2B MQA step, the radix-shared-prefix
+scenario (its 32 decode steps, copy-on-write copies and compaction moves)
+and the 200 GB pool-pressure step. `--no-configs` skips them.
+
 `--op prep` measures the fused pre-attention kernel instead (q/k RMSNorm +
 NeoX RoPE + K/V append, mkv_qk_norm_rope_append) on a prefill chunk of
 `--tokens` tokens at the same head geometry, and prints its own JSON line.
@@ -61,6 +68,8 @@ def parse():
     ap.add_argument("--split-tokens", type=int, default=0)
     ap.add_argument("--kernel", choices=["auto", "mfma", "valu"], default="auto")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", dest="configs", action="store_false",
+                    help="headline only: skip the other configurations' nested lines")
     ap.add_argument("--no-launch-events", action="store_true",
                     help="time the steps without per-launch HIP events (roofline fields null)")
     ap.add_argument("--cpu-layers", type=int, default=5,
@@ -104,10 +113,11 @@ def copy_calibration():
     print(json.dumps({"copy_bytes": n}), flush=True)
 
 
-def profiled_traffic(config: str, mode: str):
-    """HBM bytes per launch from the committed rocprofv3 PMC summary of this
-    workload (FETCH_SIZE and WRITE_SIZE, scaled by a 1 GiB copy kernel)."""
-    path = os.path.join(ROOT, "profiles", f"decode_{mode}_{config}_hbm_traffic.md")
+def profiled_traffic(key: str):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary of a
+    workload (profiles/<key>_hbm_traffic.md: FETCH_SIZE and WRITE_SIZE,
+    scaled by a 1 GiB copy kernel), or (None, None) when there is none."""
+    path = os.path.join(ROOT, "profiles", f"{key}_hbm_traffic.md")
     try:
         with open(path) as f:
             for line in f:
@@ -577,8 +587,9 @@ def bench_extend(args):
 
 def _decode_step_run(pool, plan, batch, L, Hq, Hkv, D, seed, dev, stream, pre_layer=None, cached_loads=False):
     """Q and new K/V rows of every layer, and a step function: the host plan
-    of the step, then per layer `pre_layer(layer)` (if given) and the fused
-    append + attention."""
+    of the step (with its host page tables), then per layer `pre_layer(layer)`
+    (if given) and the fused append + attention. step(events) records
+    events[layer] before each layer and events[L] after the last."""
     import torch
 
     gen = torch.Generator(device=dev)
@@ -593,43 +604,56 @@ def _decode_step_run(pool, plan, batch, L, Hq, Hkv, D, seed, dev, stream, pre_la
     plan.build(ctx_host, 0, stream=stream, block_indptr=ip, block_ids=ix)
     run_layer = pool.bind_decode_step(plan, kn, vn, q, None, None, out, stream=stream, cached_loads=cached_loads)
 
-    def step():
+    def step(events=None):
         # The engine's per-step call: host page tables (u32 CSR) into the plan.
         plan.build(ctx_host, 0, stream=stream, block_indptr=ip, block_ids=ix)
         for layer in range(L):
+            if events is not None:
+                events[layer].record(stream)
             if pre_layer is not None:
                 pre_layer(layer)
             run_layer(layer)
+        if events is not None:
+            events[L].record(stream)
 
     return step
 
 
-def _time_steps(step, steps, warmup, stream):
-    """Wall-clock seconds per step over `steps` steps after `warmup`, and the
-    HIP-event average of one step on `stream`."""
+def _time_steps(step, steps, warmup, stream, L=None, every=4):
+    """Wall-clock seconds per step over `steps` steps after `warmup`, the
+    HIP-event average of one step on `stream`, and (with L) the average of
+    one layer's bracket from per-layer events on every `every`-th step."""
     import torch
 
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    lay = {i: [torch.cuda.Event(enable_timing=True) for _ in range(L + 1)]
+           for i in range(0, steps, every)} if L else {}
     t0 = time.perf_counter()
-    for a_, b_ in evs:
+    for i, (a_, b_) in enumerate(evs):
         a_.record(stream)
-        step()
+        if L:
+            step(lay.get(i))
+        else:
+            step()
         b_.record(stream)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / steps
     ev = float(np.mean([a_.elapsed_time(b_) for a_, b_ in evs])) / 1e3
-    return wall, ev
+    if not L:
+        return wall, ev
+    layer_s = float(np.mean([e[j].elapsed_time(e[j + 1]) for e in lay.values() for j in range(L)])) / 1e3
+    return wall, ev, layer_s
 
 
 def _time_copies(pool, src, dst, reps, stream):
-    """HIP-event average seconds of one copy_blocks launch of the pairs."""
+    """HIP-event average seconds of one copy_blocks launch of the host pairs
+    (mkv_copy_blocks_host: validated, uploaded, launched)."""
     import torch
 
-    dev = torch.device("cuda:0")
-    s_, d_ = (torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(dev) for a in (src, dst))
+    s_, d_ = np.ascontiguousarray(src, np.uint32), np.ascontiguousarray(dst, np.uint32)
     pool.copy_blocks(s_, d_, stream=stream)
     torch.cuda.synchronize()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
@@ -642,20 +666,22 @@ def _time_copies(pool, src, dst, reps, stream):
     return float(np.mean([a_.elapsed_time(b_) for a_, b_ in evs])) / 1e3
 
 
-def bench_shared(args):
-    """Decode step over a radix-shared prefix (the prefix-sharing
-    configuration): 256 sequences share a 4,100-token prefix after
-    copy-on-write, so the prefix's 256 full blocks are the same ids in every
-    table and each sequence owns its copy of the partial block and a suffix
-    of ~U{64..1024} tokens. One step = the host plan, then fused append +
-    attention for all 28 layers, as in the headline. GB/s is reported on
-    unique bytes (every shared block counted once: the HBM figure) and on
-    logical bytes (each sequence's whole context, what per-sequence caches
-    would read). The value is mkv_decode_step_shared_prefix's step; the
-    same step through mkv_decode_step over the whole tables (cached and
-    non-temporal loads) is timed beside it. The copy-on-write copies (255 partial blocks) and a
-    compaction's batched moves (a fifth of the blocks) are timed as
-    copy_blocks launches over all layers, in GB/s of the moved bytes."""
+def bench_shared(steps, warmup, cpu=True):
+    """The radix-sharing configuration, driven by the host block manager
+    (wl.RadixSharingScenario) at Qwen2.5-7B shapes, all 28 layers: 256
+    sequences share a 4,100-token prefix (255 copy-on-write copies of its
+    partial block, timed as one copy_blocks launch over all layers), append
+    suffixes ~U{64..1024}, then run the configuration's 32 decode steps, each
+    with its own tables from the block manager: the plan holds the step's
+    host tables split at the shared prefix (mkv_decode_plan_build_shared_prefix)
+    and every layer runs mkv_decode_step_shared_prefix (the prefix read once
+    for all sequences on MFMA tiles, the suffixes through the plan, merged)
+    with the fused append. After them a third of the sequences finish, LRU
+    eviction frees 20% of the blocks and the compaction's block moves (from
+    the block manager's plan) are timed as one copy_blocks launch. GB/s is
+    on unique bytes (each shared block counted once: the HBM figure) and on
+    logical bytes (each sequence's whole context). `steps` is ignored: the
+    configuration's 32 decode steps are the timed steps."""
     import torch
 
     from mitten_amd import DeviceKvPool, PoolDesc
@@ -663,120 +689,147 @@ def bench_shared(args):
 
     cfg = wl.CONFIGS["qwen2.5-7b"]
     L, Hq, Hkv, D = cfg["num_layers"], cfg["num_q_heads"], cfg["num_kv_heads"], cfg["head_dim"]
-    seqs, prefix = 256, 4100
-    batch = wl.shared_prefix_batch(seqs, prefix, 64, 1024, wl.SplitMix64(wl.BASE_SEED + 3))
-    desc = PoolDesc(L, Hkv, Hq, D, batch.num_blocks, "bf16")
+    sc = wl.RadixSharingScenario()
+    bm, B = sc.bm, sc.num_seqs
+    desc = PoolDesc(L, Hkv, Hq, D, sc.num_blocks, "bf16")
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream()
     row = 2 * Hkv * D * 2  # K and V bytes of one token in one layer
-    qo_meta = wl.algorithmic_bytes_attention(batch, Hq, Hkv, D, 2) - batch.total_tokens * row
-    app = wl.algorithmic_bytes_append(seqs, Hkv, D, 2)
-    logical = L * (batch.total_tokens * row + qo_meta + app)
-    unique = L * (batch.meta["unique_tokens"] * row + qo_meta + app)
+    per_pair = L * 2 * 16 * Hkv * D * 2 * 2 + 8
     with DeviceKvPool(desc) as pool:
         gen = torch.Generator(device=dev)
         gen.manual_seed(wl.BASE_SEED + 3)
         view = pool.tensor()
-        for layer in range(L):
+        for layer in range(L):  # N(0,1) K/V in every slot (the prefill's contents)
             view[layer].normal_(generator=gen)
         del view
-        plan = pool.plan(batch.ctx_lens, stream=stream)
-        # The tables share the prefix's blocks, so the loads go through the
-        # caches (MKV_ATTN_CACHED_LOADS), as an engine would ask when its
-        # radix cache hands out shared blocks; the non-temporal default is
-        # timed beside it.
-        step = _decode_step_run(pool, plan, batch, L, Hq, Hkv, D, wl.BASE_SEED + 33, dev, stream,
-                                cached_loads=True)
-        wall, ev = _time_steps(step, args.steps, args.warmup, stream)
-        step_nt = _decode_step_run(pool, plan, batch, L, Hq, Hkv, D, wl.BASE_SEED + 33, dev, stream)
-        wall_nt, _ = _time_steps(step_nt, args.steps, args.warmup, stream)
-        pool.check()
-        info = plan.info()
-        plan.close()
-        # The shared-prefix step (mkv_decode_step_shared_prefix): the prefix
-        # read once for all 256 sequences on MFMA tiles, the suffixes through
-        # a suffix plan, both merged.
-        full = prefix // 16
-        ip = batch.block_indptr
-        sptr = (ip - full * np.arange(seqs + 1)).astype(np.int32)
-        sids = np.concatenate([batch.block_ids[ip[b] + full:ip[b + 1]] for b in range(seqs)]).astype(np.int32)
-        slen = (batch.ctx_lens - 16 * full).astype(np.int32)
-        i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(dev)
-        splan = pool.plan_suffixes(slen, stream=stream)
+        sc.prefill_prefix()
+        cow_src, cow_dst, _ = sc.fork_and_suffixes()
+        cow_s = _time_copies(pool, cow_src, cow_dst, 10, stream)
+        # The 32 decode steps' metadata, from the block manager.
+        metas = []
+        for _ in range(sc.decode_steps):
+            sc.decode_step()
+            ip, ids, ctx = bm.batch(sc.seqs)
+            pre, sptr, sids, slen = bm.batch_shared_prefix(sc.seqs)
+            shared_tok = 16 * int(pre.size)
+            unique_tok = int(ctx.sum()) - (B - 1) * shared_tok
+            metas.append(dict(ip=ip, ids=ids, ctx=ctx, pre=pre.astype(np.uint32), sptr=sptr.astype(np.uint32),
+                              sids=sids.astype(np.uint32), slen=slen, unique_tok=unique_tok))
         gen2 = torch.Generator(device=dev)
         gen2.manual_seed(wl.BASE_SEED + 33)
         bf = lambda *shape: torch.randn(shape, generator=gen2, device=dev, dtype=torch.float32).to(torch.bfloat16)
-        q, kn, vn = bf(L, seqs, Hq, D), bf(L, seqs, Hkv, D), bf(L, seqs, Hkv, D)
+        q, kn, vn = bf(L, B, Hq, D), bf(L, B, Hkv, D), bf(L, B, Hkv, D)
         out = torch.empty_like(q)
-        run_sp = pool.bind_decode_step_shared_prefix(splan, kn, vn, q, i32(batch.meta["shared_blocks"]), i32(sptr),
-                                                     i32(sids), out, stream=stream)
+        m0 = metas[0]
+        splan = pool.plan_shared_prefix(m0["pre"], m0["slen"], m0["sptr"], m0["sids"], stream=stream)
+        run_sp = pool.bind_decode_step_shared_prefix(splan, kn, vn, q, None, None, None, out, stream=stream)
+        cursor = [0]
 
-        def step_sp():
-            splan.build(slen, 0, stream=stream)
+        def step(events=None):
+            m = metas[cursor[0] % len(metas)]
+            cursor[0] += 1
+            splan.build(m["slen"], 0, stream=stream, block_indptr=m["sptr"], block_ids=m["sids"],
+                        prefix_ids=m["pre"])
             for layer in range(L):
+                if events is not None:
+                    events[layer].record(stream)
                 run_sp(layer)
+            if events is not None:
+                events[L].record(stream)
 
-        wall_sp, ev_sp = _time_steps(step_sp, args.steps, args.warmup, stream)
+        for _ in range(warmup):  # the first step's metadata, rewritten by the timed first step
+            cursor[0] = 0
+            step()
+        cursor[0] = 0
+        wall, ev_step, layer_s = _time_steps(step, len(metas), 0, stream, L=L)
         pool.check()
+        info = splan.info()
         splan.close()
-        # Copy-on-write: the last holder keeps the prefix's partial block, the
-        # other 255 sequences get copies. Compaction: a fifth of the blocks
-        # move from the top of the id space into holes below it.
-        own = batch.meta["own_first"]
-        cow_src, cow_dst = np.full(seqs - 1, own[0], np.int32), own[1:].astype(np.int32)
-        n_mv = batch.num_blocks // 5
-        mv_src = np.arange(batch.num_blocks - n_mv, batch.num_blocks, dtype=np.int32)
-        mv_dst = wl.permutation(batch.num_blocks - n_mv, wl.SplitMix64(wl.BASE_SEED + 35))[:n_mv].astype(np.int32)
-        per_pair = L * 2 * 16 * Hkv * D * 2 * 2 + 8
-        cow_s = _time_copies(pool, cow_src, cow_dst, args.steps, stream)
-        mv_s = _time_copies(pool, mv_src, mv_dst, args.steps, stream)
+        qo_meta = 2 * B * Hq * D * 2 + 4 * (B + 1) + 4 * B
+        app = wl.algorithmic_bytes_append(B, Hkv, D, 2)
+        unique = float(np.mean([L * (m["unique_tok"] * row + qo_meta + 4 * int(m["sids"].size + m["pre"].size) + app)
+                                for m in metas]))
+        logical = float(np.mean([L * (int(m["ctx"].sum()) * row + qo_meta + 4 * int(m["ids"].size) + app)
+                                 for m in metas]))
+        compare = None
+        if cpu:  # the same last step through mkv_decode_step over the whole tables
+            last = metas[-1]
+            plan = pool.plan(last["ctx"], stream=stream, block_indptr=last["ip"].astype(np.uint32),
+                             block_ids=last["ids"].astype(np.uint32))
+            lb = wl.DecodeBatch(last["ctx"], last["ip"], last["ids"], np.zeros(B, np.int32), sc.num_blocks)
+            step_c = _decode_step_run(pool, plan, lb, L, Hq, Hkv, D, wl.BASE_SEED + 33, dev, stream, cached_loads=True)
+            wall_c, _ = _time_steps(step_c, 8, 2, stream)
+            step_nt = _decode_step_run(pool, plan, lb, L, Hq, Hkv, D, wl.BASE_SEED + 33, dev, stream)
+            wall_nt, _ = _time_steps(step_nt, 8, 2, stream)
+            plan.close()
+            pool.check()
+            compare = {"whole_tables_cached_loads": {"entry": "mkv_decode_step, MKV_ATTN_CACHED_LOADS",
+                                                     "ms_per_step": round(wall_c * 1e3, 4)},
+                       "whole_tables_nontemporal": {"entry": "mkv_decode_step", "ms_per_step": round(wall_nt * 1e3, 4)}}
+        # A third of the sequences finish, eviction frees 20% of the blocks,
+        # and the compaction's moves pack the pool.
+        done, freed, live_before = sc.finish_and_evict()
+        mv_src, mv_dst = sc.compaction()
+        mv_s = _time_copies(pool, mv_src, mv_dst, 10, stream)
+        bm.check_invariants()
+    layer_unique = unique / L
     result = {
         "metric": "shared-prefix decode step: HBM GB/s on unique bytes (% peak); effective GB/s on logical bytes",
-        "value": round(unique / wall_sp / 1e9, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(wall_sp * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "value": round(unique / wall / 1e9, 2), "unit": "GB/s", "n_gpus": 1, "steps": len(metas),
+        "warmup": warmup, "ms_per_step": round(wall * 1e3, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic: N(0,1) K/V/Q from a seed; shared prefix ids and own blocks from a seeded permutation",
-        "config": {"workload": f"radix-shared decode step: {seqs} sequences over one {prefix}-token prefix "
-                               f"(suffixes U[64, 1024]), Qwen2.5-7B heads, {L} layers",
+        "data": "synthetic: N(0,1) K/V/Q from a seed; tables from the host block manager (fork, copy-on-write, "
+                "growth, eviction, compaction)",
+        "config": {"workload": f"radix-shared decode: {B} sequences over one {sc.prefix}-token prefix (suffixes "
+                               f"U[64, 1024]), {sc.decode_steps} decode steps, Qwen2.5-7B heads, {L} layers",
                    "layers": L, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "block_size": 16,
-                   "sequences": seqs, "prefix_tokens": prefix, "shared_blocks": int(batch.meta["shared_blocks"].size),
-                   "tokens_attended": batch.total_tokens, "unique_tokens": batch.meta["unique_tokens"],
-                   "pool_blocks": batch.num_blocks, "plan": info},
-        "pct_peak": round(100.0 * unique / wall_sp / 1e9 / PEAK_HBM_GBS, 2),
-        "effective_gbs_logical": round(logical / wall_sp / 1e9, 2),
-        "logical_bytes_per_step": logical, "unique_bytes_per_step": unique,
-        "tokens_per_s": round(seqs / wall_sp, 1),
-        "step_us_hip_events": round(ev_sp * 1e6, 1),
+                   "sequences": B, "prefix_tokens": sc.prefix, "shared_blocks": int(metas[0]["pre"].size),
+                   "pool_blocks": sc.num_blocks, "plan": info,
+                   "metadata": "host page tables split at the shared prefix, held by the step's plan"},
+        "pct_peak": round(100.0 * unique / wall / 1e9 / PEAK_HBM_GBS, 2),
+        "effective_gbs_logical": round(logical / wall / 1e9, 2),
+        "logical_bytes_per_step": int(logical), "unique_bytes_per_step": int(unique),
+        "tokens_per_s": round(B / wall, 1),
+        "step_us_hip_events": round(ev_step * 1e6, 1),
+        "roofline": {"bound": "hbm", "achieved": round(layer_unique / layer_s / 1e9, 2), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(layer_unique / layer_s / 1e9 / PEAK_HBM_GBS, 4),
+                     "traffic": profiled_traffic("decode_step_radix_shared_prefix_qwen2.5-7b")[0],
+                     "traffic_source": profiled_traffic("decode_step_radix_shared_prefix_qwen2.5-7b")[1],
+                     "kernel": "mkv_decode_step_shared_prefix (prefix tiles + suffix plan + merge, per layer)",
+                     "bytes_per_launch": int(layer_unique), "avg_launch_us": round(layer_s * 1e6, 2)},
         "entry": "mkv_decode_step_shared_prefix (prefix once on MFMA tiles, suffix plan, merge)",
-        "whole_tables_cached_loads": {"entry": "mkv_decode_step, MKV_ATTN_CACHED_LOADS",
-                                      "ms_per_step": round(wall * 1e3, 4), "step_us_hip_events": round(ev * 1e6, 1),
-                                      "effective_gbs_logical": round(logical / wall / 1e9, 2),
-                                      "unique_gbs": round(unique / wall / 1e9, 2)},
-        "whole_tables_nontemporal": {"entry": "mkv_decode_step", "ms_per_step": round(wall_nt * 1e3, 4),
-                                     "effective_gbs_logical": round(logical / wall_nt / 1e9, 2),
-                                     "unique_gbs": round(unique / wall_nt / 1e9, 2)},
         "cow_copies": {"pairs": int(cow_src.size), "bytes": int(cow_src.size) * per_pair,
                        "avg_launch_us": round(cow_s * 1e6, 2),
                        "gbs": round(cow_src.size * per_pair / cow_s / 1e9, 2)},
-        "compaction_moves": {"pairs": int(n_mv), "bytes": int(n_mv) * per_pair,
+        "compaction_moves": {"pairs": int(mv_src.size), "bytes": int(mv_src.size) * per_pair,
+                             "finished_sequences": len(done), "blocks_freed_by_eviction": int(freed),
+                             "live_blocks_before": int(live_before),
                              "avg_launch_us": round(mv_s * 1e6, 2),
-                             "gbs": round(n_mv * per_pair / mv_s / 1e9, 2)},
+                             "gbs": round(mv_src.size * per_pair / mv_s / 1e9, 2)},
         "cpu_baseline": None,
     }
-    if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(cfg, batch, logical, 1)
+    if compare:
+        result.update(compare)
+    if cpu:
+        last = metas[-1]
+        lb = wl.DecodeBatch(last["ctx"], last["ip"], last["ids"], np.zeros(B, np.int32), sc.num_blocks)
+        result["cpu_baseline"] = cpu_baseline(cfg, lb, logical, 1)
         result["cpu_baseline"]["bytes"] = "logical (each sequence's whole context)"
-    print(json.dumps(result), flush=True)
+    torch.cuda.empty_cache()
+    return result
 
 
-def bench_pressure(args):
+def bench_pressure(steps, warmup, cpu=True):
     """One step of a pool under pressure (the pool-pressure configuration):
     the 217,982-block pool of a 200 GB budget (all 28 layers, Qwen2.5-7B
     heads), 512 sequences with log-normal lengths (median 2,048, sigma 1,
     capped at 32,768) in blocks from a seeded permutation of the pool. Per
-    step and layer, 8 sequences append a 512-token chunk (mkv_append) and
-    the other 504 run the fused append + decode attention; the chunks'
-    prefill attention is left out, as the configuration states."""
+    step and layer, 8 sequences append a 512-token chunk (mkv_append_host:
+    the slots are host u32 values, uploaded per call) and the other 504 run
+    the fused append + decode attention from a plan holding the step's host
+    tables; the chunks' prefill attention is left out, as the configuration
+    states."""
     import torch
 
     from mitten_amd import DeviceKvPool, PoolDesc
@@ -803,7 +856,7 @@ def bench_pressure(args):
         del view
         kc = torch.randn((L, n_chunk, Hkv, D), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
         vc = torch.randn((L, n_chunk, Hkv, D), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
-        cs = torch.from_numpy(chunk_slots).to(dev)
+        cs = chunk_slots.astype(np.uint32)
 
         def chunk_append(layer):
             pool.append(layer, kc[layer], vc[layer], cs, stream=stream)
@@ -811,15 +864,16 @@ def bench_pressure(args):
         plan = pool.plan(batch.ctx_lens, stream=stream)
         step = _decode_step_run(pool, plan, batch, L, Hq, Hkv, D, wl.BASE_SEED + 44, dev, stream,
                                 pre_layer=chunk_append)
-        wall, ev = _time_steps(step, args.steps, args.warmup, stream)
+        wall, ev, layer_s = _time_steps(step, steps, warmup, stream, L=L)
         pool.check()
         info = plan.info()
         plan.close()
         pool_bytes = pool.nbytes
+        del kc, vc
     result = {
         "metric": "pool-pressure step (chunk appends + fused decode step): achieved HBM GB/s (% peak)",
-        "value": round(step_bytes / wall / 1e9, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(wall * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "value": round(step_bytes / wall / 1e9, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps,
+        "warmup": warmup, "ms_per_step": round(wall * 1e3, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic: N(0,1) K/V/Q from a seed; log-normal lengths and block ids from a seeded permutation",
         "config": {"workload": f"pool-pressure step: {nblocks}-block pool ({pool_bytes / 1e9:.1f} GB), {seqs} "
@@ -828,15 +882,183 @@ def bench_pressure(args):
                    "layers": L, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "block_size": 16,
                    "pool_blocks": nblocks, "pool_bytes": pool_bytes, "sequences": seqs,
                    "tokens_held": int(lengths.sum()), "decode_sequences": batch.num_seqs,
-                   "tokens_attended": batch.total_tokens, "chunk_tokens": n_chunk, "plan": info},
+                   "tokens_attended": batch.total_tokens, "chunk_tokens": n_chunk, "plan": info,
+                   "metadata": "host u32 chunk slots per append; host page tables held by the step's plan"},
         "pct_peak": round(100.0 * step_bytes / wall / 1e9 / PEAK_HBM_GBS, 2),
         "step_bytes": step_bytes, "tokens_per_s": round((batch.num_seqs + n_chunk) / wall, 1),
         "step_us_hip_events": round(ev * 1e6, 1),
+        "roofline": {"bound": "hbm", "achieved": round(step_bytes / L / layer_s / 1e9, 2), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(step_bytes / L / layer_s / 1e9 / PEAK_HBM_GBS, 4),
+                     "traffic": profiled_traffic("pool_pressure_step_qwen2.5-7b")[0],
+                     "traffic_source": profiled_traffic("pool_pressure_step_qwen2.5-7b")[1],
+                     "kernel": "mkv_append_host (chunks) + mkv_decode_step (per layer)",
+                     "bytes_per_launch": step_bytes // L, "avg_launch_us": round(layer_s * 1e6, 2)},
         "cpu_baseline": None,
     }
-    if not args.no_cpu_baseline:
+    if cpu:
         result["cpu_baseline"] = cpu_baseline(cfg, batch, step_bytes, 1, paged=False)
-    print(json.dumps(result), flush=True)
+    torch.cuda.empty_cache()
+    return result
+
+
+def decode_config(name: str, steps: int, warmup: int, mode: str = "step", pieces: int = 0,
+                  kernel: str | None = None, split_tokens: int = 0, launch_events: bool = True):
+    """One decode-step configuration (wl.CONFIGS[name]) on a fresh pool.
+    A step is, per layer: append of every sequence's new K/V row + paged
+    decode attention (`mode` step: one fused mkv_decode_step per layer from a
+    plan holding the step's host page tables; planned: mkv_append +
+    mkv_decode_attention_planned; split: mkv_append + mkv_decode_attention).
+    The f32 Qwen2.5-0.5B configuration also gathers every layer's block
+    tables into contiguous per-sequence caches (mkv_gather_host), as its
+    step states. Returns (result dict, batch, step_bytes); the pool is freed."""
+    import torch
+
+    from mitten_amd import DeviceKvPool, PoolDesc
+    from mitten_amd import workloads as wl
+
+    cfg = wl.CONFIGS[name]
+    batch = wl.config_batch(name)
+    L, Hq, Hkv, D, dt = cfg["num_layers"], cfg["num_q_heads"], cfg["num_kv_heads"], cfg["head_dim"], cfg["dtype"]
+    B = batch.num_seqs
+    with_gather = name == "qwen2.5-0.5b"
+    desc = PoolDesc(L, Hkv, Hq, D, batch.num_blocks, dt)
+    dev = torch.device("cuda:0")
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    es = desc.elem_bytes
+
+    pool = DeviceKvPool(desc)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(batch.seed)
+    view = pool.tensor()
+    for layer in range(L):  # N(0,1) K/V in every slot, one layer at a time
+        view[layer].normal_(generator=gen)
+    del view
+    q = torch.randn((L, B, Hq, D), generator=gen, device=dev, dtype=torch.float32).to(tdt)
+    k_new = torch.randn((L, B, Hkv, D), generator=gen, device=dev, dtype=torch.float32).to(tdt)
+    v_new = torch.randn((L, B, Hkv, D), generator=gen, device=dev, dtype=torch.float32).to(tdt)
+    out = torch.empty_like(q)
+    i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(dev)
+    indptr, ids, ctx, slots = (i32(batch.block_indptr), i32(batch.block_ids), i32(batch.ctx_lens),
+                               i32(batch.slot_mapping))
+    max_ctx = batch.max_ctx
+    ws = torch.empty(max(1, pool.workspace_size(B, max_ctx, split_tokens)), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    gk = torch.empty(batch.total_tokens * Hkv * D, dtype=tdt, device=dev) if with_gather else None
+    gv = torch.empty_like(gk) if with_gather else None
+
+    attn_bytes = wl.algorithmic_bytes_attention(batch, Hq, Hkv, D, es)
+    app_bytes = wl.algorithmic_bytes_append(B, Hkv, D, es)
+    gather_bytes = (4 * batch.total_tokens * Hkv * D * es + 4 * int(batch.block_ids.size)) if with_gather else 0
+    step_bytes = L * (attn_bytes + app_bytes + gather_bytes)
+    # Bytes of the work the HIP events bracket per layer: the fused step moves
+    # the append's bytes too, and the gather follows it in the same bracket.
+    launch_bytes = attn_bytes + (app_bytes if mode == "step" else 0) + gather_bytes
+
+    ctx_host = batch.ctx_lens.copy()
+    ip_h, ids_h = batch.block_indptr.astype(np.uint32), batch.block_ids.astype(np.uint32)
+    plan = pool.plan(ctx_host, pieces=pieces, stream=stream, block_indptr=ip_h, block_ids=ids_h)
+
+    run_layer = pool.bind_decode_step(plan, k_new, v_new, q, None, None, out, kernel=kernel, stream=stream)
+
+    def step(events=None):
+        """events: None, or L+1 timing events recorded between layers."""
+        if mode != "split":
+            # The engine's one call per step: host lengths and host page
+            # tables (u32 CSR), validated, copied and uploaded with the plan.
+            plan.build(ctx_host, pieces, stream=stream, block_indptr=ip_h, block_ids=ids_h)
+        for layer in range(L):
+            if mode != "step":
+                pool.append(layer, k_new[layer], v_new[layer], slots, stream=stream)
+            if events is not None:
+                events[layer].record(stream)
+            if mode == "step":
+                run_layer(layer)
+            elif mode == "planned":
+                pool.decode_attention_planned(layer, plan, q[layer], None, None, out=out[layer],
+                                              kernel=kernel, stream=stream)
+            else:
+                pool.decode_attention(layer, q[layer], indptr, ids, ctx, max_ctx, out=out[layer],
+                                      split_tokens=split_tokens, workspace=ws, kernel=kernel,
+                                      stream=stream)
+            if with_gather:
+                pool.gather_host(layer, ip_h, ids_h, ctx_host, out_k=gk, out_v=gv, stream=stream)
+        if events is not None:
+            events[L].record(stream)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    pool.check()
+
+    # Launch timing: an event chain around every layer's launch on every
+    # EVENT_EVERY-th timed step (events cost GPU time; sampling keeps the
+    # timed steps close to unperturbed).
+    EVENT_EVERY = 4
+    timed = [s_ for s_ in range(steps) if s_ % EVENT_EVERY == 0 and launch_events]
+    ev = {s_: [torch.cuda.Event(enable_timing=True) for _ in range(L + 1)] for s_ in timed}
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s_ in range(steps):
+        step(ev.get(s_))
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    pool.check()
+    elapsed = t1 - t0
+    ms_step = elapsed / steps * 1e3
+    attn_ms = [e[i].elapsed_time(e[i + 1]) for e in ev.values() for i in range(L)] or [float("nan")]
+    attn_avg_s = float(np.mean(attn_ms)) / 1e3
+    gbs = step_bytes / (elapsed / steps) / 1e9
+    attn_gbs = launch_bytes / attn_avg_s / 1e9
+    traffic, traffic_src = profiled_traffic(f"decode_{mode}_{name}")
+    kernel_name = {"step": "mkv_decode_step (append + attention + merge, per layer)",
+                   "planned": "mkv_decode_attention_planned (attention + merge, per layer)",
+                   "split": "mkv_decode_attention (attention + merge, per layer)"}[mode]
+    if with_gather:
+        kernel_name += " + mkv_gather_host"
+    result = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dt,
+        "data": "synthetic: N(0,1) K/V/Q from a seed; block tables from a seeded permutation of the pool",
+        "config": {"workload": f"{name} decode step (append + paged decode attention per layer"
+                               + (" + block-table gather" if with_gather else "") + ")",
+                   "layers": L, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "block_size": 16,
+                   "sequences": B, "ctx_range": [cfg["ctx_lo"], cfg["ctx_hi"]],
+                   "tokens_attended": batch.total_tokens, "pool_blocks": batch.num_blocks,
+                   "pool_bytes": pool.nbytes, "seed": batch.seed, "mode": mode,
+                   "plan": plan.info(), "split_tokens": split_tokens, "kernel": kernel or "auto",
+                   "metadata": "host page tables (u32 CSR) held by the step's plan"},
+        "pct_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
+        "tokens_per_s": round(B / (elapsed / steps), 1),
+        "step_bytes": step_bytes,
+        "roofline": {"bound": "hbm", "achieved": round(attn_gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(attn_gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src, "kernel": kernel_name,
+                     "bytes_per_launch": launch_bytes, "avg_launch_us": round(attn_avg_s * 1e6, 2),
+                     "launches_timed": len(attn_ms) if ev else 0},
+        "cpu_baseline": None,
+    }
+    plan.close()
+    pool.close()
+    del q, k_new, v_new, out, ws, gk, gv
+    torch.cuda.empty_cache()
+    return result, batch, step_bytes
+
+
+def _nested(r: dict) -> dict:
+    """The fields of a configuration's result kept in the headline line."""
+    keep = ("metric", "value", "unit", "ms_per_step", "pct_peak", "tokens_per_s", "steps", "warmup", "dtype",
+            "config", "roofline", "effective_gbs_logical", "step_bytes", "unique_bytes_per_step",
+            "logical_bytes_per_step", "cow_copies", "compaction_moves")
+    return {k: r[k] for k in keep if k in r}
 
 
 def main():
@@ -861,143 +1083,29 @@ def main():
         bench_extend(args)
         return
     if args.op == "shared":
-        bench_shared(args)
+        print(json.dumps(bench_shared(args.steps, args.warmup, cpu=not args.no_cpu_baseline)), flush=True)
         return
     if args.op == "pressure":
-        bench_pressure(args)
+        print(json.dumps(bench_pressure(args.steps, args.warmup, cpu=not args.no_cpu_baseline)), flush=True)
         return
-    import torch
-
-    from mitten_amd import DeviceKvPool, PoolDesc
     from mitten_amd import workloads as wl
 
-    cfg = wl.CONFIGS[args.config]
-    batch = wl.config_batch(args.config)
-    L, Hq, Hkv, D, dt = cfg["num_layers"], cfg["num_q_heads"], cfg["num_kv_heads"], cfg["head_dim"], cfg["dtype"]
-    B = batch.num_seqs
-    desc = PoolDesc(L, Hkv, Hq, D, batch.num_blocks, dt)
-    dev = torch.device("cuda:0")
-    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
-    es = desc.elem_bytes
-
-    pool = DeviceKvPool(desc)
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(batch.seed)
-    view = pool.tensor()
-    for layer in range(L):  # N(0,1) K/V in every slot, one layer at a time
-        view[layer].normal_(generator=gen)
-    del view
-    q = torch.randn((L, B, Hq, D), generator=gen, device=dev, dtype=torch.float32).to(tdt)
-    k_new = torch.randn((L, B, Hkv, D), generator=gen, device=dev, dtype=torch.float32).to(tdt)
-    v_new = torch.randn((L, B, Hkv, D), generator=gen, device=dev, dtype=torch.float32).to(tdt)
-    out = torch.empty_like(q)
-    i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(dev)
-    indptr, ids, ctx, slots = (i32(batch.block_indptr), i32(batch.block_ids), i32(batch.ctx_lens),
-                               i32(batch.slot_mapping))
-    max_ctx = batch.max_ctx
     kernel = None if args.kernel == "auto" else args.kernel
-    ws = torch.empty(max(1, pool.workspace_size(B, max_ctx, args.split_tokens)), dtype=torch.uint8, device=dev)
-    stream = torch.cuda.current_stream()
-
-    attn_bytes = wl.algorithmic_bytes_attention(batch, Hq, Hkv, D, es)
-    app_bytes = wl.algorithmic_bytes_append(B, Hkv, D, es)
-    step_bytes = L * (attn_bytes + app_bytes)
-    # Bytes of the launch the HIP events bracket: the fused step moves the
-    # append's bytes too.
-    launch_bytes = attn_bytes + (app_bytes if args.mode == "step" else 0)
-
-    ctx_host = batch.ctx_lens.copy()
-    ip_h, ids_h = batch.block_indptr.astype(np.uint32), batch.block_ids.astype(np.uint32)
-    plan = pool.plan(ctx_host, pieces=args.pieces, stream=stream, block_indptr=ip_h, block_ids=ids_h)
-
-    run_layer = pool.bind_decode_step(plan, k_new, v_new, q, None, None, out, kernel=kernel, stream=stream)
-
-    def step(events=None):
-        """events: None, or L+1 timing events recorded between launches (the
-        fused step has nothing else between consecutive layers)."""
-        if args.mode != "split":
-            # The engine's one call per step: host lengths and host page
-            # tables (u32 CSR), validated, copied and uploaded with the plan.
-            plan.build(ctx_host, args.pieces, stream=stream, block_indptr=ip_h, block_ids=ids_h)
-        for layer in range(L):
-            if args.mode != "step":
-                pool.append(layer, k_new[layer], v_new[layer], slots, stream=stream)
-            if events is not None:
-                events[layer].record(stream)
-            if args.mode == "step":
-                run_layer(layer)
-            elif args.mode == "planned":
-                pool.decode_attention_planned(layer, plan, q[layer], None, None, out=out[layer],
-                                              kernel=kernel, stream=stream)
-            else:
-                pool.decode_attention(layer, q[layer], indptr, ids, ctx, max_ctx, out=out[layer],
-                                      split_tokens=args.split_tokens, workspace=ws, kernel=kernel,
-                                      stream=stream)
-        if events is not None:
-            events[L].record(stream)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    pool.check()
-
-    # Launch timing: an event chain around every layer's launch on every
-    # EVENT_EVERY-th timed step (events cost GPU time; sampling keeps the
-    # timed steps close to unperturbed).
-    EVENT_EVERY = 4
-    timed = [s for s in range(args.steps) if s % EVENT_EVERY == 0 and not args.no_launch_events]
-    ev = {s: [torch.cuda.Event(enable_timing=True) for _ in range(L + 1)] for s in timed}
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for s in range(args.steps):
-        step(ev.get(s))
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    pool.check()
-    elapsed = t1 - t0
-    ms_step = elapsed / args.steps * 1e3
-    attn_ms = [e[i].elapsed_time(e[i + 1]) for e in ev.values() for i in range(L)] or [float("nan")]
-    attn_avg_s = float(np.mean(attn_ms)) / 1e3
-    gbs = step_bytes / (elapsed / args.steps) / 1e9
-    attn_gbs = launch_bytes / attn_avg_s / 1e9
-
-    traffic, traffic_src = profiled_traffic(args.config, args.mode)
-    result = {
-        "metric": METRIC,
-        "value": round(gbs, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": dt,
-        "data": "synthetic: N(0,1) K/V/Q from a seed; block tables from a seeded permutation of the pool",
-        "config": {"workload": f"{args.config} decode step (append + paged decode attention per layer)",
-                   "layers": L, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "block_size": 16,
-                   "sequences": B, "ctx_range": [cfg["ctx_lo"], cfg["ctx_hi"]],
-                   "tokens_attended": batch.total_tokens, "pool_blocks": batch.num_blocks,
-                   "pool_bytes": pool.nbytes, "seed": batch.seed, "mode": args.mode,
-                   "plan": plan.info(), "split_tokens": args.split_tokens, "kernel": args.kernel},
-        "pct_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
-        "tokens_per_s": round(B / (elapsed / args.steps), 1),
-        "step_bytes": step_bytes,
-        "roofline": {"bound": "hbm", "achieved": round(attn_gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(attn_gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
-                     "traffic_source": traffic_src,
-                     "kernel": {"step": "mkv_decode_step (append + attention + merge, per layer)",
-                                "planned": "mkv_decode_attention_planned (attention + merge, per layer)",
-                                "split": "mkv_decode_attention (attention + merge, per layer)"}[args.mode],
-                     "bytes_per_launch": launch_bytes, "avg_launch_us": round(attn_avg_s * 1e6, 2),
-                     "launches_timed": len(attn_ms) if ev else 0},
-        "cpu_baseline": None,
-    }
+    result, batch, step_bytes = decode_config(args.config, args.steps, args.warmup, args.mode, args.pieces, kernel,
+                                              args.split_tokens, not args.no_launch_events)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(cfg, batch, step_bytes, args.cpu_layers)
-    plan.close()
-    pool.close()
+        result["cpu_baseline"] = cpu_baseline(wl.CONFIGS[args.config], batch, step_bytes, args.cpu_layers)
+    if args.configs and args.config == "qwen2.5-7b" and args.mode == "step":
+        # The other configurations of the measurement table, each on its own
+        # pool at its full size, with fewer steps (their own lines come from
+        # --config / --op).
+        ks, kw = max(4, min(args.steps, 12)), max(1, min(args.warmup, 2))
+        nested = {}
+        for name in ("qwen2.5-0.5b", "gemma-2b-mqa"):
+            nested[name] = _nested(decode_config(name, ks, kw)[0])
+        nested["radix-shared-prefix"] = _nested(bench_shared(ks, kw, cpu=False))
+        nested["pool-pressure"] = _nested(bench_pressure(ks, kw, cpu=False))
+        result["configs"] = nested
     print(json.dumps(result), flush=True)
 
 

@@ -232,3 +232,97 @@ def algorithmic_bytes_prep(num_tokens: int, num_q_heads: int, num_kv_heads: int,
     slot ids, plus the norm weights and the frequency table."""
     rows = num_tokens * (2 * num_q_heads + 4 * num_kv_heads) * head_dim * elem_bytes
     return rows + 8 * num_tokens + (8 * head_dim if norm else 0) + 2 * rotary_dim
+
+
+def tokens(rng: SplitMix64, n: int) -> np.ndarray:
+    """n seeded token ids (u32, below 50,000)."""
+    return np.asarray([rng.bounded(50_000) for _ in range(n)], np.uint32)
+
+
+class RadixSharingScenario:
+    """The radix-sharing configuration, phase by phase, on the host block
+    manager (refcounted pool + radix tree), at Qwen2.5-7B shapes:
+
+    1. `prefill_prefix()`: sequence 0 is admitted with a `prefix`-token prompt
+       (4,100: 256 full blocks and a 4-token partial block), its K/V slots
+       returned, and the prompt promoted into the radix tree
+       (scheduler.rs:117, radix_cache.rs:287-294).
+    2. `fork_and_suffixes()`: sequences 1..n-1 fork sequence 0 and share
+       every prefix block, the partial one included; each then appends its
+       own suffix ~U{suffix_lo..suffix_hi} (a prefill chunk). The first
+       write into the shared partial block copies it (n - 1 copy pairs,
+       returned); sequence 0, its last holder, writes in place. Every prompt
+       (prefix + suffix) is then promoted.
+    3. `decode_step()`: every sequence appends one token; returns the slots.
+    4. `finish_and_evict()`: a third of the sequences finish (release: their
+       promoted pages stay in the tree, the rest are freed), then LRU
+       eviction of the tree (radix_cache.rs:243-282) until at least
+       `evict_frac` of the live blocks are freed.
+    5. `compaction()`: the block moves that pack the live blocks below the
+       live count (tables and tree pages rewritten), for copy_blocks.
+
+    Every result is a pure function of the seed."""
+
+    def __init__(self, num_seqs: int = 256, prefix: int = 4100, suffix_lo: int = 64, suffix_hi: int = 1024,
+                 decode_steps: int = 32, seed: int = BASE_SEED + 3, spare_blocks: int = 64):
+        from .host import BlockManager
+
+        rng = SplitMix64(seed)
+        self.num_seqs, self.prefix, self.decode_steps = num_seqs, prefix, decode_steps
+        self.suffix = [rng.uniform_int(suffix_lo, suffix_hi) for _ in range(num_seqs)]
+        self.prefix_tokens = tokens(rng, prefix)
+        self.prompts = [np.concatenate([self.prefix_tokens, tokens(rng, n)]) for n in self.suffix]
+        full = prefix // PAGE
+        part = prefix - full * PAGE
+        own = [(part + n + decode_steps + PAGE - 1) // PAGE for n in self.suffix]
+        self.num_blocks = full + sum(own) + spare_blocks
+        self.bm = BlockManager(self.num_blocks)
+        self.seqs = list(range(num_seqs))
+        self.live = list(self.seqs)
+        self.prefix_full_blocks = full
+
+    def prefill_prefix(self) -> np.ndarray:
+        bm = self.bm
+        assert bm.admit(0, self.prefix_tokens) == 0
+        slots, cow = bm.append(0, self.prefix)
+        assert cow == []
+        bm.promote(0, self.prefix_tokens)
+        return slots.astype(np.int32)
+
+    def fork_and_suffixes(self):
+        """(cow_src, cow_dst, slots): the copies to run first, then the
+        suffix tokens' slots in the order [1, .., n-1, 0]."""
+        bm = self.bm
+        for s in self.seqs[1:]:
+            bm.fork(0, s)
+        src, dst, slots = [], [], []
+        for s in self.seqs[1:] + [0]:
+            sl, cow = bm.append(s, self.suffix[s])
+            slots.append(sl)
+            for a, b in cow:
+                src.append(a)
+                dst.append(b)
+        for s in self.seqs:
+            bm.promote(s, self.prompts[s])
+        return (np.asarray(src, np.int32), np.asarray(dst, np.int32),
+                np.concatenate(slots).astype(np.int32))
+
+    def decode_step(self) -> np.ndarray:
+        return np.concatenate([self.bm.append(s, 1)[0] for s in self.live]).astype(np.int32)
+
+    def finish_and_evict(self, evict_frac: float = 0.2):
+        """(finished sequences, blocks freed, live blocks before)."""
+        bm = self.bm
+        done = self.seqs[::3]
+        for s in done:
+            bm.release(s)
+        self.live = [s for s in self.seqs if s not in set(done)]
+        live_before = bm.live_blocks()
+        target = int(np.ceil(evict_frac * live_before))
+        freed = 0
+        while freed < target and bm.cached_pages() > 0:
+            freed += bm.evict(max(1, min(256, target - freed)))
+        return done, freed, live_before
+
+    def compaction(self):
+        return self.bm.plan_compaction()

@@ -3,15 +3,18 @@ the host block manager drives the device pool through the C ABI, and every
 phase is checked against the oracle (bit-exact for appends, copies and
 gathers; within the attention tolerances for decode attention).
 
-* C1, Qwen2.5-0.5B f32: bulk prompt append, then decode steps of
+Every scenario passes its metadata in the engine's host form (u32 slots,
+page tables held by the step's plan).
+
+* C1, Qwen2.5-0.5B f32: bulk prompt append, then 64 decode steps of
   (append one token + gather + attention) over all 24 layers.
 * C4, radix sharing at Qwen-7B head shapes (2 of 28 layers): 256 sequences
   fork one 4,100-token prefix (256 full blocks + a 4-token partial block),
   copy-on-write of the shared partial block on the first append (255 copies,
-  the last holder writes in place), suffixes, decode steps, the
-  shared-prefix step over the block manager's tables (equal to the plain
-  attention), then 20% of the sequences finish and the pool is compacted by
-  batched block moves.
+  the last holder writes in place), suffixes ~U{64..1024}, 32 decode steps,
+  the shared-prefix step over the block manager's tables (equal to the plain
+  attention), then a third of the sequences finish, LRU eviction frees 20%
+  of the live blocks and the pool is compacted by batched block moves.
 * C5, pool pressure at Qwen-7B head shapes (1 of 28 layers): the
   217,982-block pool of a 200 GB budget, 512 sequences with log-normal
   lengths (median 2,048, sigma 1, capped at 32,768); per step 8 sequences
@@ -55,11 +58,18 @@ def _sub_batch(indptr, ids, ctx, rows):
 
 # --------------------------------------------------------------------- C1 ----
 
+def _u32(a):
+    return np.ascontiguousarray(a, np.uint32)
+
+
 def test_c1_prompt_append_prefill_then_decode_gather_attention():
+    """The configuration as stated: 8 prompts ~U{32..512}, then 64 decode
+    steps of (append + gather + attention) over all 24 layers, driven by the
+    block manager through the host-metadata entry points."""
     c = wl.CONFIGS["qwen2.5-0.5b"]
     L, Hq, Hkv, D = c["num_layers"], c["num_q_heads"], c["num_kv_heads"], c["head_dim"]
     rng = wl.SplitMix64(wl.BASE_SEED + c["index"])
-    B, steps = c["batch"], 16
+    B, steps = c["batch"], 64
     prompts = [rng.uniform_int(c["ctx_lo"], c["ctx_hi"]) for _ in range(B)]
     num_blocks = sum((p + steps + 15) // 16 for p in prompts) + 4
     desc = PoolDesc(L, Hkv, Hq, D, num_blocks, "f32")
@@ -78,7 +88,7 @@ def test_c1_prompt_append_prefill_then_decode_gather_attention():
         slots = np.concatenate(slots).astype(np.int32)
         k = normal(100, (L, slots.size, Hkv, D), "f32")
         v = normal(101, (L, slots.size, Hkv, D), "f32")
-        pool.append_all_layers(to_device(k), to_device(v), _i32(slots))
+        pool.append_all_layers(to_device(k), to_device(v), _u32(slots))
         for layer in range(L):
             assert orc.append(od, want, layer, k[layer], v[layer], slots) == -1
         pool.check()
@@ -89,33 +99,32 @@ def test_c1_prompt_append_prefill_then_decode_gather_attention():
         q_indptr = np.concatenate([[0], np.cumsum(prompts)]).astype(np.int32)
         for layer in (0, L - 1):
             qp = normal(4000 + layer, (int(q_indptr[-1]), Hq, D), "f32")
-            o = pool.extend_attention(layer, to_device(qp), _i32(q_indptr), _i32(indptr), _i32(ids), _i32(ctx),
-                                      max(prompts), int(ctx.max()))
+            o = pool.extend_attention_host(layer, to_device(qp), prompts, ctx, _u32(indptr), _u32(ids))
             pool.check()
             ref = orc.extend_attention(od, want, layer, qp, q_indptr, indptr, ids, ctx)
             assert_attention_close(to_host(o), ref, "f32")
+        plan = pool.plan(np.ones(B, np.int32))
         for step in range(steps):
             new = np.concatenate([bm.append(s, 1)[0] for s in range(B)]).astype(np.int32)
             indptr, ids, ctx = bm.batch(list(range(B)))
             assert np.array_equal(new, [ids[indptr[b] + (ctx[b] - 1) // 16] * 16 + (ctx[b] - 1) % 16
                                         for b in range(B)])
-            plan = pool.plan(ctx)
-            d_ptr, d_ids, d_cptr = _i32(indptr), _i32(ids), _i32(_ctx_indptr(ctx))
-            check_layers = range(L) if step == steps - 1 else (0, L - 1)
+            plan.build(ctx, block_indptr=_u32(indptr), block_ids=_u32(ids))
+            check_layers = range(L) if step in (0, steps - 1) else (0, L - 1)
             for layer in range(L):
                 kn = normal(1000 + 31 * step + layer, (B, Hkv, D), "f32")
                 vn = normal(2000 + 31 * step + layer, (B, Hkv, D), "f32")
                 q = normal(3000 + 31 * step + layer, (B, Hq, D), "f32")
-                o = pool.decode_step(layer, plan, to_device(kn), to_device(vn), to_device(q), d_ptr, d_ids)
+                o = pool.decode_step(layer, plan, to_device(kn), to_device(vn), to_device(q), None, None)
+                gk, gv = pool.gather_host(layer, _u32(indptr), _u32(ids), ctx)
                 assert orc.append(od, want, layer, kn, vn, new) == -1
                 if layer in check_layers:
-                    gk, gv = pool.gather(layer, d_ptr, d_ids, d_cptr, int(ctx.max()))
                     wk, wv = orc.gather(od, want, layer, indptr, ids, ctx)
                     assert np.array_equal(bits(to_host(gk)), bits(wk))
                     assert np.array_equal(bits(to_host(gv)), bits(wv))
                     ref = orc.decode_attention(od, want, layer, q, indptr, ids, ctx)
                     assert_attention_close(to_host(o), ref, "f32")
-            plan.close()
+        plan.close()
         pool.check()
         assert np.array_equal(bits(pool.read()), bits(want))
     bm.check_invariants()
@@ -123,125 +132,110 @@ def test_c1_prompt_append_prefill_then_decode_gather_attention():
 
 # --------------------------------------------------------------------- C4 ----
 
-C4_SEQS, C4_PREFIX = 256, 4100
 
-
-def test_c4_radix_sharing_cow_decode_and_compaction():
-    L, Hq, Hkv, D = 2, 28, 4, 128  # Qwen-7B heads, 2 of 28 layers
-    rng = wl.SplitMix64(wl.BASE_SEED + 3)
-    suffix = [rng.uniform_int(16, 128) for _ in range(C4_SEQS)]
-    dec_steps = 3
-    prefix_blocks = (C4_PREFIX + 15) // 16
-    num_blocks = prefix_blocks + sum((4 + s + dec_steps + 15) // 16 + 1 for s in suffix) + 64
-    desc = PoolDesc(L, Hkv, Hq, D, num_blocks, "bf16")
+def test_c4_radix_sharing_cow_decode_eviction_and_compaction():
+    """The radix-sharing configuration at its stated size (2 of 28 layers at
+    Qwen-7B heads): 256 sequences share a 4,100-token prefix (the partial
+    block copied on write 255 times), suffixes ~U{64..1024}, 32 decode steps
+    (the fused step over the block manager's tables; the shared-prefix step
+    checked against it), then a third of the sequences finish, LRU eviction
+    frees 20% of the live blocks, and the compaction's block moves pack the
+    pool. Pool bit-exact against the oracle after every phase; the live
+    sequences' gathers and attention bit-identical across the compaction."""
+    L, Hq, Hkv, D = 2, 28, 4, 128
+    sc = wl.RadixSharingScenario()
+    bm, seqs = sc.bm, sc.seqs
+    B = sc.num_seqs
+    desc = PoolDesc(L, Hkv, Hq, D, sc.num_blocks, "bf16")
     od = odesc(desc)
-    bm = BlockManager(num_blocks)
     want = np.zeros(desc.shape, np.uint16)
-    seqs = list(range(C4_SEQS))
     with DeviceKvPool(desc) as pool:
         pool.write(want)
-        # One prefill of the prefix, then every other sequence forks it.
-        assert bm.admit(0, _tokens(7, C4_PREFIX)) == 0
-        pslots, _ = bm.append(0, C4_PREFIX)
-        k = normal(200, (L, C4_PREFIX, Hkv, D), "bf16")
-        v = normal(201, (L, C4_PREFIX, Hkv, D), "bf16")
-        pool.append_all_layers(to_device(k), to_device(v), _i32(pslots))
+        # 1. The prefix, prefilled once.
+        pslots = sc.prefill_prefix()
+        k = normal(200, (L, pslots.size, Hkv, D), "bf16")
+        v = normal(201, (L, pslots.size, Hkv, D), "bf16")
+        pool.append_all_layers(to_device(k), to_device(v), _u32(pslots))
         for layer in range(L):
             assert orc.append(od, want, layer, k[layer], v[layer], pslots) == -1
-        for s in seqs[1:]:
-            bm.fork(0, s)
         shared = bm.table(0)
-        assert len(shared) == prefix_blocks and all(bm.refcount(b) == C4_SEQS for b in shared)
-        # First append of each sequence: the shared partial block is copied
-        # before the write, except by its last holder.
-        order = seqs[1:] + [0]
-        slots, src, dst = [], [], []
-        for s in order:
-            sl, cow = bm.append(s, suffix[s])
-            slots.append(sl)
-            for a, b in cow:
-                src.append(a)
-                dst.append(b)
-        assert len(src) == C4_SEQS - 1 and set(src) == {int(shared[-1])}
-        assert bm.table(0)[prefix_blocks - 1] == shared[-1]  # the last holder kept it
-        pool.copy_blocks(_i32(src), _i32(dst))
+        # 2. Forks, copy-on-write of the shared partial block, suffixes.
+        src, dst, slots = sc.fork_and_suffixes()
+        assert len(src) == B - 1 and set(src.tolist()) == {int(shared[-1])}
+        assert bm.table(0)[sc.prefix_full_blocks] == shared[-1]  # the last holder kept it
+        assert all(bm.refcount(int(b)) == B + 1 for b in shared[:-1])  # every sequence + the tree
+        pool.copy_blocks(_u32(src), _u32(dst))
         orc.copy_blocks(od, want, src, dst)
-        slots = np.concatenate(slots).astype(np.int32)
         k = normal(202, (L, slots.size, Hkv, D), "bf16")
         v = normal(203, (L, slots.size, Hkv, D), "bf16")
-        pool.append_all_layers(to_device(k), to_device(v), _i32(slots))
+        pool.append_all_layers(to_device(k), to_device(v), _u32(slots))
         for layer in range(L):
             assert orc.append(od, want, layer, k[layer], v[layer], slots) == -1
         pool.check()
         assert np.array_equal(bits(pool.read()), bits(want))
-        assert all(bm.refcount(b) == C4_SEQS for b in shared[:-1])
         bm.check_invariants()
-        # Decode steps over all 256 sequences (the full prefix is read by each).
-        sample = list(range(0, C4_SEQS, 16))
-        for step in range(dec_steps):
-            new = []
-            for s in seqs:
-                sl, cow = bm.append(s, 1)
-                assert cow == []
-                new.append(sl)
-            new = np.concatenate(new).astype(np.int32)
+        # 3. 32 decode steps over all 256 sequences.
+        sample = list(range(0, B, 16))
+        plan = pool.plan(np.ones(B, np.int32))
+        for step in range(sc.decode_steps):
+            new = sc.decode_step()
             indptr, ids, ctx = bm.batch(seqs)
-            plan = pool.plan(ctx)
-            d_ptr, d_ids = _i32(indptr), _i32(ids)
+            plan.build(ctx, block_indptr=_u32(indptr), block_ids=_u32(ids))
             for layer in range(L):
-                kn = normal(300 + 7 * step + layer, (C4_SEQS, Hkv, D), "bf16")
-                vn = normal(400 + 7 * step + layer, (C4_SEQS, Hkv, D), "bf16")
-                q = normal(500 + 7 * step + layer, (C4_SEQS, Hq, D), "bf16")
-                o = pool.decode_step(layer, plan, to_device(kn), to_device(vn), to_device(q), d_ptr, d_ids)
+                kn = normal(300 + 7 * step + layer, (B, Hkv, D), "bf16")
+                vn = normal(400 + 7 * step + layer, (B, Hkv, D), "bf16")
+                q = normal(500 + 7 * step + layer, (B, Hq, D), "bf16")
+                o = pool.decode_step(layer, plan, to_device(kn), to_device(vn), to_device(q), None, None)
                 assert orc.append(od, want, layer, kn, vn, new) == -1
-                sp, si, sc = _sub_batch(indptr, ids, ctx, sample)
-                ref = orc.decode_attention(od, want, layer, widen(q[sample]), sp, si, sc)
-                assert_attention_close(to_host(o)[sample], ref, "bf16")
-            plan.close()
+                if step % 8 == 7 or step == 0:
+                    sp, si, sc_ = _sub_batch(indptr, ids, ctx, sample)
+                    ref = orc.decode_attention(od, want, layer, widen(q[sample]), sp, si, sc_)
+                    assert_attention_close(to_host(o)[sample], ref, "bf16")
+        plan.close()
         pool.check()
         assert np.array_equal(bits(pool.read()), bits(want))
         # The shared-prefix step over the same tables: the prefix's 256 full
-        # pages (the partial one was copied on write) read once for all 256
-        # sequences, then each suffix; equal to the plain planned attention.
+        # pages read once for all 256 sequences, then each suffix.
         indptr, ids, ctx = bm.batch(seqs)
         pre, s_ptr, s_ids, s_len = bm.batch_shared_prefix(seqs)
-        assert pre.size == prefix_blocks - 1 and np.array_equal(pre, shared[:-1])
-        q = normal(550, (C4_SEQS, Hq, D), "bf16")
-        plan = pool.plan(ctx)
-        o_full = to_host(pool.decode_attention_planned(1, plan, to_device(q), _i32(indptr), _i32(ids)))
+        assert pre.size == sc.prefix_full_blocks and np.array_equal(pre, shared[:-1])
+        q = normal(550, (B, Hq, D), "bf16")
+        plan = pool.plan(ctx, block_indptr=_u32(indptr), block_ids=_u32(ids))
+        o_full = to_host(pool.decode_attention_planned(1, plan, to_device(q), None, None))
         plan.close()
-        splan = pool.plan_suffixes(s_len)
-        o_sp = to_host(pool.decode_step_shared_prefix(1, splan, None, None, to_device(q), _i32(pre), _i32(s_ptr),
-                                                      _i32(s_ids)))
+        splan = pool.plan_shared_prefix(_u32(pre), s_len, _u32(s_ptr), _u32(s_ids))
+        o_sp = to_host(pool.decode_step_shared_prefix(1, splan, None, None, to_device(q), None, None, None))
         splan.close()
         pool.check()
         assert_attention_close(o_sp, widen(o_full), "bf16")
-        sp_, si_, sc_ = _sub_batch(indptr, ids, ctx, sample)
-        assert_attention_close(o_sp[sample], orc.decode_attention(od, want, 1, widen(q[sample]), sp_, si_, sc_), "bf16")
-        # 20% of the sequences finish; compaction moves tail blocks into the holes.
-        done = seqs[::5]
-        live = [s for s in seqs if s not in done]
-        indptr, ids, ctx = bm.batch(live)
-        d_cptr = _i32(_ctx_indptr(ctx))
-        before = [to_host(t) for t in pool.gather(0, _i32(indptr), _i32(ids), d_cptr, int(ctx.max()))]
-        q = normal(600, (len(live), Hq, D), "bf16")
-        plan = pool.plan(ctx)
-        o_before = to_host(pool.decode_attention_planned(1, plan, to_device(q), _i32(indptr), _i32(ids)))
-        plan.close()
-        for s in done:
-            bm.release(s)
+        sp_, si_, sc2 = _sub_batch(indptr, ids, ctx, sample)
+        assert_attention_close(o_sp[sample], orc.decode_attention(od, want, 1, widen(q[sample]), sp_, si_, sc2),
+                               "bf16")
+        # 4. A third of the sequences finish; LRU eviction frees 20% of the blocks.
+        live_tabs = {s: bm.table(s).copy() for s in seqs}
+        done, freed, live_before = sc.finish_and_evict()
+        live = sc.live
+        assert freed >= 0.2 * live_before and bm.live_blocks() == live_before - freed
         bm.check_invariants()
-        src, dst = bm.plan_compaction()
+        indptr, ids, ctx = bm.batch(live)
+        assert all(np.array_equal(bm.table(s), live_tabs[s]) for s in live)
+        before = [to_host(t) for t in pool.gather_host(0, _u32(indptr), _u32(ids), ctx)]
+        q = normal(600, (len(live), Hq, D), "bf16")
+        plan = pool.plan(ctx, block_indptr=_u32(indptr), block_ids=_u32(ids))
+        o_before = to_host(pool.decode_attention_planned(1, plan, to_device(q), None, None))
+        plan.close()
+        # 5. Compaction: the moves pack the live blocks below the live count.
+        src, dst = sc.compaction()
         assert len(src) > 0 and set(src.tolist()).isdisjoint(dst.tolist())
-        pool.copy_blocks(_i32(src), _i32(dst))
+        pool.copy_blocks(_u32(src), _u32(dst))
         orc.copy_blocks(od, want, src, dst)
         bm.check_invariants()
         indptr2, ids2, ctx2 = bm.batch(live)
         assert np.array_equal(ctx2, ctx) and int(ids2.max()) < bm.live_blocks()
-        after = [to_host(t) for t in pool.gather(0, _i32(indptr2), _i32(ids2), d_cptr, int(ctx.max()))]
+        after = [to_host(t) for t in pool.gather_host(0, _u32(indptr2), _u32(ids2), ctx2)]
         assert all(np.array_equal(bits(a), bits(b)) for a, b in zip(after, before))
-        plan = pool.plan(ctx2)
-        o_after = to_host(pool.decode_attention_planned(1, plan, to_device(q), _i32(indptr2), _i32(ids2)))
+        plan = pool.plan(ctx2, block_indptr=_u32(indptr2), block_ids=_u32(ids2))
+        o_after = to_host(pool.decode_attention_planned(1, plan, to_device(q), None, None))
         plan.close()
         assert np.array_equal(bits(o_after), bits(o_before))  # same bytes, same order: same bits
         pool.check()
@@ -283,7 +277,7 @@ def test_c5_pool_pressure_chunked_append_and_decode():
             slots = np.concatenate([bm.append(s, C5_CHUNK)[0] for s in chunk]).astype(np.int32)
             kc = normal(700 + step, (slots.size, Hkv, D), "bf16")
             vc = normal(800 + step, (slots.size, Hkv, D), "bf16")
-            pool.append(0, to_device(kc), to_device(vc), _i32(slots))
+            pool.append(0, to_device(kc), to_device(vc), _u32(slots))
             blk = torch.from_numpy((slots // 16).astype(np.int64)).cuda()
             off = torch.from_numpy((slots % 16).astype(np.int64)).cuda()
             assert np.array_equal(to_host(view[0, 0, blk, off]), kc)
@@ -291,9 +285,8 @@ def test_c5_pool_pressure_chunked_append_and_decode():
             # The chunks' causal attention over their whole caches (extend).
             cptr, cids, cctx = bm.batch(chunk)
             qc = normal(850 + step, (len(chunk) * C5_CHUNK, Hq, D), "bf16")
-            q_indptr = np.arange(len(chunk) + 1, dtype=np.int32) * C5_CHUNK
-            oc = to_host(pool.extend_attention(0, to_device(qc), _i32(q_indptr), _i32(cptr), _i32(cids),
-                                               _i32(cctx), C5_CHUNK, int(cctx.max())))
+            oc = to_host(pool.extend_attention_host(0, to_device(qc), [C5_CHUNK] * len(chunk), cctx, _u32(cptr),
+                                                    _u32(cids)))
             for r in (0, len(chunk) - 1):  # two chunk sequences, first / middle / last queries
                 table = cids[cptr[r]:cptr[r + 1]]
                 mini = np.ascontiguousarray(blocks_of(table)[None])
@@ -309,12 +302,11 @@ def test_c5_pool_pressure_chunked_append_and_decode():
             dec = [s for s in seqs if s not in chunk]
             new = np.concatenate([bm.append(s, 1)[0] for s in dec]).astype(np.int32)
             indptr, ids, ctx = bm.batch(dec)
-            plan = pool.plan(ctx)
+            plan = pool.plan(ctx, block_indptr=_u32(indptr), block_ids=_u32(ids))
             kn = normal(900 + step, (len(dec), Hkv, D), "bf16")
             vn = normal(950 + step, (len(dec), Hkv, D), "bf16")
             q = normal(990 + step, (len(dec), Hq, D), "bf16")
-            o = to_host(pool.decode_step(0, plan, to_device(kn), to_device(vn), to_device(q),
-                                         _i32(indptr), _i32(ids)))
+            o = to_host(pool.decode_step(0, plan, to_device(kn), to_device(vn), to_device(q), None, None))
             plan.close()
             pool.check()
             blk = torch.from_numpy((new // 16).astype(np.int64)).cuda()
