@@ -227,8 +227,8 @@ int meta_acquire(Pool *p, size_t n, hipStream_t hs, MetaSlot **out) {
     sl->pending = false;
   }
   n = std::max<size_t>(n, 1);
-  if (sl->cap < n) {
-    const size_t cap = std::max<size_t>(n, 4096);
+  if (sl->cap < n) {  // grows by half again at least: a batch's tables grow step by step
+    const size_t cap = std::max<size_t>({n, 4096, sl->cap + sl->cap / 2});
     if (sl->h) MKV_CHECK_HIP(hipHostFree(sl->h));
     if (sl->d) MKV_CHECK_HIP(hipFree(sl->d));
     sl->h = nullptr;
