@@ -74,7 +74,8 @@ def parse():
                     help="time the steps without per-launch HIP events (roofline fields null)")
     ap.add_argument("--cpu-layers", type=int, default=5,
                     help="layers of the batch in the CPU baseline sample")
-    ap.add_argument("--op", choices=["decode", "prep", "wire", "gather", "copy", "extend", "shared", "pressure"],
+    ap.add_argument("--op", choices=["decode", "prep", "wire", "gather", "copy", "append", "extend", "shared",
+                                     "pressure"],
                     default="decode",
                     help="decode: the decode step (headline); prep: the fused q/k-norm + RoPE + "
                          "append kernel on a prefill chunk; wire: KV block export + import of a "
@@ -88,6 +89,8 @@ def parse():
     ap.add_argument("--tokens-per-chunk", type=int, default=512, help="--op extend: chunk length")
     ap.add_argument("--prefix", type=int, default=4096, help="--op extend: cached tokens before the chunk")
     ap.add_argument("--copy-pairs", type=int, default=4096, help="--op copy: block pairs")
+    ap.add_argument("--append-chunks", type=int, default=8,
+                    help="--op append: 512-token chunks appended per launch (the pool-pressure step's 8)")
     ap.add_argument("--handoff-blocks", type=int, default=2048,
                     help="--op wire: blocks handed off (all layers)")
     ap.add_argument("--tokens", type=int, default=16384, help="--op prep: tokens in the chunk")
@@ -429,7 +432,7 @@ def bench_move(args):
                             total_tokens=tokens, stream=stream)
             kernel, what = "mkv_gather", (f"{args.config} decode batch: {batch.num_seqs} sequences, "
                                           f"{tokens} context tokens, one layer per launch")
-        else:
+        elif args.op == "copy":
             rng = wl.SplitMix64(batch.seed + 5)
             perm = wl.permutation(batch.num_blocks, rng)
             npairs = args.copy_pairs
@@ -439,6 +442,30 @@ def bench_move(args):
             def launch(i):
                 pool.copy_blocks(src, dst, stream=stream)
             kernel, what = "mkv_copy_blocks", f"{args.config} pool: {npairs} block pairs, all {L} layers, K and V"
+        elif args.op == "append":
+            # The pool-pressure step's chunk appends: `--append-chunks` chunks
+            # of 512 consecutive positions, each in 32 whole blocks drawn from
+            # a seeded permutation of the pool; one layer per launch.
+            rng = wl.SplitMix64(batch.seed + 6)
+            perm = wl.permutation(batch.num_blocks, rng)
+            nch = args.append_chunks
+            blocks = perm[:nch * 32].astype(np.int64)
+            slots_h = (blocks[:, None] * 16 + np.arange(16)[None, :]).reshape(-1).astype(np.uint32)
+            n_tok = int(slots_h.size)
+            tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+            kk = torch.randn((n_tok, Hkv, D), generator=gen, device=dev, dtype=torch.float32).to(tdt)
+            vv = torch.randn((n_tok, Hkv, D), generator=gen, device=dev, dtype=torch.float32).to(tdt)
+            slots_d = i32(slots_h.astype(np.int32))
+            launch_bytes = 4 * n_tok * row + 4 * n_tok
+            host_slots = args.mode == "planned"  # reuse --mode planned to select the host-slot entry point
+
+            def launch(i):
+                if host_slots:
+                    pool.append(i % L, kk, vv, slots_h, stream=stream)
+                else:
+                    pool.append(i % L, kk, vv, slots_d, stream=stream)
+            kernel = "mkv_append_host" if host_slots else "mkv_append"
+            what = f"{args.config} pool: {nch} x 512-token chunk append ({n_tok} tokens), one layer per launch"
         for i in range(args.warmup):
             launch(i)
         torch.cuda.synchronize()
@@ -468,11 +495,16 @@ def bench_move(args):
                 orc.gather(od, host, 0, batch.block_indptr[:ns + 1], batch.block_ids[:hi], batch.ctx_lens[:ns])
                 cpu_bytes = 4 * int(batch.ctx_lens[:ns].sum()) * row
                 sample = f"oracle gather of {ns} sequences ({int(batch.ctx_lens[:ns].sum())} tokens)"
-            else:
+            elif args.op == "copy":
                 ps = min(64, npairs)
                 orc.copy_blocks(od, host, perm[:ps], perm[npairs:npairs + ps])
                 cpu_bytes = 2 * ps * L * 2 * desc.block_bytes
                 sample = f"oracle copy_blocks of {ps} pairs, all layers"
+            else:
+                hk = host[0, 0, :n_tok // 16].reshape(n_tok, Hkv, D).copy()
+                orc.append(od, host, 0, hk, hk, slots_h.astype(np.int32))
+                cpu_bytes = launch_bytes
+                sample = f"oracle append of the {n_tok} tokens, one layer"
             reps += 1
         cpu_s = (time.perf_counter() - c0) / reps
     launch_s = float(np.mean([a.elapsed_time(b) for a, b in evs])) / 1e3
@@ -1076,7 +1108,7 @@ def main():
     if args.op == "wire":
         bench_wire(args)
         return
-    if args.op in ("gather", "copy"):
+    if args.op in ("gather", "copy", "append"):
         bench_move(args)
         return
     if args.op == "extend":

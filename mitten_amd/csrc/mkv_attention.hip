@@ -55,6 +55,7 @@ constexpr int kQChunkValu = 8;
 constexpr int kRing = 3;       // MFMA loop: blocks loaded ahead + 1
 constexpr int kBlockWeight = 8;    // plan: weight of one block in a piece ...
 constexpr int kSwitchWeight = 12;  // ... and of a sequence start inside it (about 1.5 blocks)
+constexpr int kFirstRoundWeight = 116;  // plan: cap of the first-dispatched pieces, percent
 constexpr int kCoopRing = 3;   // register stages of the cooperative kernel (one less when
                                // its slots carry four Q loads per lane)
 
@@ -2093,15 +2094,23 @@ static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t 
   // block) adds kSwitchWeight, what its predecessor's partial stores and the
   // Q reload cost that piece (measured: about 1.5 blocks' time).
   std::vector<int32_t> f0s;
+  // With two resident workgroups per CU, the pieces dispatched first (the
+  // first `first` indices, one per CU) get kFirstRoundWeight percent of the
+  // cap: their waves are older and win issue arbitration over the second
+  // workgroup of their CU.
+  const int64_t first = (!pieces && resident > 0 && device_cus(pl->pool) > 0 &&
+                         resident == 2 * (int64_t)device_cus(pl->pool)) ? device_cus(pl->pool) : 0;
   auto cut = [&](int64_t cap) {
     f0s.clear();
     int64_t w = 0;
     int cnt = 0;
     int32_t b = 0;
+    const int64_t cap_first = cap * kFirstRoundWeight / 100;
     for (int64_t f = 0; f < total; f++) {
       while (blk0v[b + 1] <= f) b++;
       int64_t wi = kBlockWeight + ((f == blk0v[b] && cnt > 0) ? kSwitchWeight : 0);
-      if (cnt > 0 && (cnt == 64 || w + wi > cap)) {
+      const int64_t cq = (int64_t)f0s.size() - 1 < first ? cap_first : cap;
+      if (cnt > 0 && (cnt == 64 || w + wi > cq)) {
         cnt = 0;
         w = 0;
         wi = kBlockWeight;
@@ -2113,7 +2122,7 @@ static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t 
     f0s.push_back((int32_t)total);
   };
   {  // smallest cap giving at most P pieces (the count falls as the cap grows)
-    int64_t lo = (kBlockWeight * total + P - 1) / P, hi = 64 * (kBlockWeight + kSwitchWeight);
+    int64_t lo = kBlockWeight, hi = 64 * (kBlockWeight + kSwitchWeight);
     while (lo < hi) {
       const int64_t mid = (lo + hi) / 2;
       cut(mid);

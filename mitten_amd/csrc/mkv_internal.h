@@ -7,6 +7,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <string>
+#include <vector>
 
 #include "mitten_kv.h"
 
@@ -37,6 +38,7 @@ struct MetaSlot {
   size_t cap = 0;        // int32 elements of both
   hipEvent_t done = nullptr;
   bool pending = false;
+  uint64_t gen = 0;  // counts acquisitions (a staged array is current while gen is unchanged)
 };
 
 struct Pool {
@@ -53,6 +55,12 @@ struct Pool {
   int ext_per_cu[3][5][2] = {};  // resident extend workgroups per CU by (head_dim, waves, sub-tiles); 0: not yet queried
   MetaSlot meta[kMetaSlots];
   int meta_next = 0;
+  // The last host slot mapping staged by the append entry points: the slot
+  // that holds it, its generation and stream, and the values.
+  int app_slot = -1;
+  uint64_t app_gen = 0;
+  hipStream_t app_stream = nullptr;
+  std::vector<uint32_t> app_vals;
 };
 
 // Next staging slot with room for n int32 values (waits for its previous

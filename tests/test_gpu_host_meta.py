@@ -390,3 +390,38 @@ def test_wire_host_equals_device_form_and_rejects_repeated_destinations():
     want = host.copy()
     want[:, :, dst.astype(np.int64)] = host[:, :, ids]
     assert np.array_equal(bits(after), bits(want))
+
+
+def test_append_host_reuses_an_equal_mapping_and_follows_a_changed_one():
+    """Every layer of a step appends the same tokens: the library uploads an
+    equal mapping once. A mapping changed in place under the same array, a
+    staging slot claimed by other host calls in between, and another stream
+    all get a fresh upload; every append is bit-exact."""
+    import torch
+
+    desc, pool, host = _pool("qwen7b-bf16", 64, 70)
+    want = host.copy()
+    rng = np.random.default_rng(71)
+    slots = rng.choice(desc.num_blocks * 16, size=40, replace=False).astype(np.uint32)
+    side = torch.cuda.Stream()
+
+    def app(layer, seed, stream=None):
+        k = normal(seed, (slots.size, desc.num_kv_heads, desc.head_dim), desc.dtype)
+        v = normal(seed + 1, (slots.size, desc.num_kv_heads, desc.head_dim), desc.dtype)
+        pool.append(layer, to_device(k), to_device(v), slots, stream=stream)
+        orc.append(odesc(desc), want, layer, k, v, slots.astype(np.int32))
+
+    app(0, 72)
+    app(1, 74)                      # same mapping: launched from the staged copy
+    slots[:] = rng.choice(desc.num_blocks * 16, size=40, replace=False)
+    app(0, 76)                      # changed in place: uploaded again
+    for i in range(9):              # other host calls claim every staging slot
+        pool.copy_blocks(np.array([60], np.uint32), np.array([61 + i % 3], np.uint32))
+        orc.copy_blocks(odesc(desc), want, np.array([60], np.int32), np.array([61 + i % 3], np.int32))
+    app(1, 78)                      # equal values, but its slot was reused: uploaded again
+    torch.cuda.synchronize()
+    app(0, 80, stream=side)         # another stream: uploaded on it
+    side.synchronize()
+    pool.check()
+    assert np.array_equal(bits(pool.read()), bits(want))
+    pool.close()
