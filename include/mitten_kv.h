@@ -338,7 +338,15 @@ MKV_API int mkv_decode_step(mkv_pool *pool, const mkv_decode_plan *plan, int32_t
  * d_k_new / d_v_new (both or neither) go at suffix position suffix_len_b - 1.
  * Three launches: the prefix over all queries (f32 partials per key range in
  * the pool-owned workspace, grown on demand as for mkv_extend_attention),
- * the suffixes through the plan, and their merge. bf16 pools, head_dim
+ * the suffixes through the plan, and their merge. Where a workgroup of the
+ * prefix fits beside one of the suffixes on every compute unit (the pool's
+ * geometry decides; Qwen2.5-7B heads do), a plan built with pieces = 0 cuts
+ * one suffix piece per compute unit and the step runs the prefix on a
+ * second HIP stream that the pool creates on first use: forked from
+ * `stream` at entry and joined back into it before the merge, so work
+ * enqueued on `stream` after the call still follows the whole step. Calls
+ * on one pool must not overlap on different streams (they share the
+ * workspace and that second stream). bf16 pools, head_dim
  * 64/128/256, at most 16 query heads per KV head. Same result as
  * mkv_decode_step over tables prefix + suffix, within the attention
  * tolerance (the partials merge in another order). Flags: MKV_ATTN_ZERO_SINK. */

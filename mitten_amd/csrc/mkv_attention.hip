@@ -1770,6 +1770,7 @@ struct Plan {
   bool has_tables = false;    // flat_id holds the block ids given at build time
   int32_t n_prefix = 0;       // shared-prefix ids given at build time (0: none)
   bool all_partial = false;   // every sequence stores partials (built for a shared prefix's suffixes)
+  bool beside = false;        // suffix pieces sized to run beside the prefix tiles (one per CU)
 };
 
 static PlanDev plan_dev(const Plan *pl) {
@@ -1983,10 +1984,6 @@ extern "C" int mkv_decode_plan_destroy(mkv_decode_plan *plan) {
   return MKV_OK;
 }
 
-// Workgroups of the cooperative decode kernel the device holds at once
-// (CUs x resident workgroups per CU for the instantiation the pool's
-// geometry selects), or 0 when that kernel does not apply. Pieces beyond it
-// run in a second round; fewer leave CUs idle. Queried once per pool.
 // Compute units of the pool's device, queried once (-1 when unknown).
 static int device_cus(Pool *p) {
   if (p->cus == 0) {
@@ -2000,6 +1997,10 @@ static int device_cus(Pool *p) {
   return p->cus;
 }
 
+// Workgroups of the cooperative decode kernel the device holds at once
+// (CUs x resident workgroups per CU for the instantiation the pool's
+// geometry selects), or 0 when that kernel does not apply. Pieces beyond it
+// run in a second round; fewer leave CUs idle. Queried once per pool.
 static int64_t coop_resident(Pool *p) {
   if (p->coop_slots >= 0) return p->coop_slots;
   const Geom &g = p->g;
@@ -2035,6 +2036,32 @@ static int64_t coop_resident(Pool *p) {
   }
   p->coop_slots = per_cu > 0 && cus > 0 ? (int64_t)per_cu * cus : 0;
   return p->coop_slots;
+}
+
+static const void *ext_kernel(int D, int W, int TP);
+static int ext_resident_per_cu(Pool *p, const void *fn, int W, int TP);
+
+// Whether the shared-prefix step runs its prefix tiles beside the suffix
+// pieces, on a second stream. The suffixes are HBM-bound and the prefix is
+// bound by issue and the matrix cores, so a CU that holds one workgroup of
+// each keeps both busy. That pairing fits when the decode kernel and the
+// one-sub-tile prefix instantiation each hold two workgroups per CU: each
+// then takes at most half of every CU resource. The plan then cuts one
+// suffix piece per CU, and the prefix is split to about one workgroup per
+// CU (Qwen2.5-7B heads, 256 sequences over a 4,100-token prefix: 2.86 ->
+// 2.42 ms per 28-layer step). Queried once per pool.
+static bool prefix_beside(Pool *p) {
+  if (p->beside == 0) {
+    p->beside = -1;
+    const Geom &g = p->g;
+    const int G = g.Hq / g.Hkv;
+    const int cus = device_cus(p);
+    if (cus > 0 && g.D <= 128 && G <= 8 && coop_resident(p) == 2 * (int64_t)cus) {
+      const int WG = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8;
+      if (ext_resident_per_cu(p, ext_kernel(g.D, WG, 1), WG, 1) >= 2) p->beside = 1;
+    }
+  }
+  return p->beside > 0;
 }
 
 // Host tables given to a plan build (the engine's form; all NULL when the
@@ -2075,7 +2102,9 @@ static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t 
   // chunk); a piece is one workgroup of the grid.
   const int G = g.Hq / g.Hkv;
   const int nqc = (G + kQChunkMfma - 1) / kQChunkMfma;
-  const int64_t resident = pieces ? 0 : coop_resident(pl->pool);
+  // A shared prefix's suffixes run beside the prefix tiles: one piece per CU.
+  const bool beside = !pieces && all_partial && prefix_beside(pl->pool);
+  const int64_t resident = pieces ? 0 : beside ? device_cus(pl->pool) : coop_resident(pl->pool);
   int64_t P = pieces ? pieces : resident ? resident : std::max<int64_t>(1, 2048 / std::max(1, g.Hkv * nqc));
   P = std::max<int64_t>(P, (total + 63) / 64);  // a piece is at most 64 blocks (one per lane)
   P = std::min<int64_t>(P, total);
@@ -2236,6 +2265,7 @@ static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t 
   pl->total = (int32_t)total;
   pl->n_merge = n_merge;
   pl->all_partial = all_partial;
+  pl->beside = beside;
   return MKV_OK;
 }
 
@@ -2404,7 +2434,7 @@ extern "C" int mkv_decode_step(mkv_pool *pool, const mkv_decode_plan *plan, int3
                         d_k_new, d_v_new, d_q, d_o, d_block_indptr, d_block_ids, scale, flags, stream);
 }
 
-static int launch_ext_tiles(Pool *p, KArgs &a, ExtArgs &e, int split_cap, hipStream_t hs);
+static int launch_ext_tiles(Pool *p, KArgs &a, ExtArgs &e, int split_cap, hipStream_t hs, bool beside = false);
 
 extern "C" int mkv_decode_step_shared_prefix(mkv_pool *pool, const mkv_decode_plan *plan, int32_t layer,
                                              const void *d_k_new, const void *d_v_new, const void *d_q,
@@ -2446,7 +2476,17 @@ extern "C" int mkv_decode_step_shared_prefix(mkv_pool *pool, const mkv_decode_pl
   DeviceGuard guard(p->device);
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
   // 1. The prefix: the B decode queries as one chunk over the prefix's keys,
-  //    no causal mask, f32 partials per key range (pool workspace).
+  //    no causal mask, f32 partials per key range (pool workspace). When the
+  //    plan's suffix pieces leave room for it (one per CU), it runs on the
+  //    pool's second stream, forked from the caller's stream here and joined
+  //    back before the merge, beside the suffixes. The events order device
+  //    work only, so they skip the system-scope fence.
+  const bool beside = pl->beside;
+  if (beside && !p->aux) {
+    MKV_CHECK_HIP(hipStreamCreateWithFlags(&p->aux, hipStreamNonBlocking));
+    MKV_CHECK_HIP(hipEventCreateWithFlags(&p->aux_fork, hipEventDisableTiming | hipEventDisableSystemFence));
+    MKV_CHECK_HIP(hipEventCreateWithFlags(&p->aux_join, hipEventDisableTiming | hipEventDisableSystemFence));
+  }
   KArgs ap = make_kargs(p, layer, d_q, d_o, nullptr, d_prefix_ids, scale, flags, true);
   ExtArgs e{};
   e.B = 1;
@@ -2454,12 +2494,22 @@ extern "C" int mkv_decode_step_shared_prefix(mkv_pool *pool, const mkv_decode_pl
   e.max_q = e.v_nq = pl->B;
   e.causal = 0;
   e.partial = 1;
-  rc = launch_ext_tiles(p, ap, e, 16, hs);
-  if (rc) return rc;
+  if (beside) {
+    MKV_CHECK_HIP(hipEventRecord(p->aux_fork, hs));
+    MKV_CHECK_HIP(hipStreamWaitEvent(p->aux, p->aux_fork, 0));
+    rc = launch_ext_tiles(p, ap, e, 16, p->aux, true);
+    MKV_CHECK_HIP(hipEventRecord(p->aux_join, p->aux));
+  } else {
+    rc = launch_ext_tiles(p, ap, e, 16, hs);
+  }
   // 2. The suffixes (and the fused append): every sequence's partials, one
   //    per piece, in the plan's workspace.
-  rc = launch_planned(p, pl, layer, d_k_new, d_v_new, d_q, d_o, d_block_indptr, d_block_ids, scale, flags, stream,
-                      false);
+  if (!rc)
+    rc = launch_planned(p, pl, layer, d_k_new, d_v_new, d_q, d_o, d_block_indptr, d_block_ids, scale, flags,
+                        stream, false);
+  // The join comes before any return: nothing the caller enqueues after this
+  // call (nor the merge) may overtake the prefix tiles.
+  if (beside) MKV_CHECK_HIP(hipStreamWaitEvent(hs, p->aux_join, 0));
   if (rc) return rc;
   // 3. Both runs of partials merged into o.
   KArgs am = make_kargs(p, layer, d_q, d_o, d_block_indptr, d_block_ids, scale, flags, true);
@@ -2570,12 +2620,61 @@ extern "C" int mkv_extend_attention_host(mkv_pool *pool, int32_t layer, const vo
   return rc ? rc : rr;
 }
 
+// The extend kernel's instantiation for head_dim D, W waves and TP
+// sub-tiles of 16 positions per workgroup.
+static const void *ext_kernel(int D, int W, int TP) {
+  const void *fn = nullptr;
+#define MKV_EXT_FN(DD, TT)                                                                                  \
+  do {                                                                                                      \
+    switch (W / TT) {                                                                                       \
+      case 1: fn = reinterpret_cast<const void *>(&attn_extend_kernel<DD, 1 * TT, kExtKB, kExtR, TT>); break; \
+      case 2: fn = reinterpret_cast<const void *>(&attn_extend_kernel<DD, 2 * TT, kExtKB, kExtR, TT>); break; \
+      case 4: fn = reinterpret_cast<const void *>(&attn_extend_kernel<DD, 4 * TT, kExtKB, kExtR, TT>); break; \
+      case 8: fn = reinterpret_cast<const void *>(&attn_extend_kernel<DD, 8 * TT, kExtKB, kExtR, TT>); break; \
+      default: fn = reinterpret_cast<const void *>(&attn_extend_kernel<DD, 16, kExtKB, kExtR, 1>); break;     \
+    }                                                                                                       \
+  } while (0)
+  switch (D) {
+    case 64: if (TP == 2) MKV_EXT_FN(64, 2); else MKV_EXT_FN(64, 1); break;
+    case 128: if (TP == 2) MKV_EXT_FN(128, 2); else MKV_EXT_FN(128, 1); break;
+    default:
+      switch (W) {
+        case 4: fn = reinterpret_cast<const void *>(&attn_extend_kernel<256, 4, kExtKB, kExtR, 1>); break;
+        case 8: fn = reinterpret_cast<const void *>(&attn_extend_kernel<256, 8, kExtKB, kExtR, 1>); break;
+        default: fn = reinterpret_cast<const void *>(&attn_extend_kernel<256, 16, kExtKB, kExtR, 1>); break;
+      }
+      break;
+  }
+#undef MKV_EXT_FN
+  return fn;
+}
+
+// Resident workgroups per CU of an extend instantiation (occupancy query,
+// once per pool and instantiation); -1 when unknown.
+static int ext_resident_per_cu(Pool *p, const void *fn, int W, int TP) {
+  const Geom &g = p->g;
+  int &per_cu = p->ext_per_cu[g.D == 64 ? 0 : g.D == 128 ? 1 : 2][W == 1 ? 0 : W == 2 ? 1 : W == 4 ? 2 : W == 8 ? 3 : 4][TP - 1];
+  if (per_cu == 0) {
+    int n_cu = 0;
+    DeviceGuard guard(p->device);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n_cu, fn, 64 * W, 0) != hipSuccess) {
+      (void)hipGetLastError();  // leave no sticky error: no splitting
+      n_cu = 0;
+    }
+    per_cu = n_cu > 0 ? n_cu : -1;
+  }
+  return per_cu;
+}
+
 // MFMA query tiles of the extend kernel for e (B, max_q, max_ctx, causal,
 // partial and the sequence arguments set): picks the instantiation and the
 // key-range split (at most split_cap), grows the pool workspace when
 // partials are stored, launches, and merges the splits unless e.partial
-// (then a.ws_ml / a.ws_o and e.splits describe the partials left).
-static int launch_ext_tiles(Pool *p, KArgs &a, ExtArgs &e, int split_cap, hipStream_t hs) {
+// (then a.ws_ml / a.ws_o and e.splits describe the partials left). With
+// beside, the tiles share the device with a decode launch that holds one
+// workgroup per CU: one sub-tile per workgroup, and the split aims at one
+// workgroup per CU.
+static int launch_ext_tiles(Pool *p, KArgs &a, ExtArgs &e, int split_cap, hipStream_t hs, bool beside) {
   const Geom &g = p->g;
   const int G = g.Hq / g.Hkv;
   const int64_t num_seqs = e.B, max_q_len = e.max_q, max_ctx_len = e.max_ctx;
@@ -2592,50 +2691,20 @@ static int launch_ext_tiles(Pool *p, KArgs &a, ExtArgs &e, int split_cap, hipStr
   // share the loads, and one or two waves would each carry 16-32 loads per
   // ring stage (register spills).
   const int WG = G <= 1 && g.D < 256 ? 1 : G <= 2 && g.D < 256 ? 2 : G <= 4 ? 4 : G <= 8 ? 8 : 16;
-  const int TP = (WG <= 8 && g.D <= 128 && max_q_len > 16) ? 2 : 1;
+  const int TP = (!beside && WG <= 8 && g.D <= 128 && max_q_len > 16) ? 2 : 1;
   const int W = WG * TP;
   const int64_t tiles = ((int64_t)max_q_len + 16 * TP - 1) / (16 * TP);
   const int64_t per_split = tiles * g.Hkv * num_seqs;  // (tile, KV head, sequence) workgroups
-  const void *fn = nullptr;
-#define MKV_EXT_FN(DD, TT)                                                                                  \
-  do {                                                                                                      \
-    switch (W / TT) {                                                                                       \
-      case 1: fn = reinterpret_cast<const void *>(&attn_extend_kernel<DD, 1 * TT, kExtKB, kExtR, TT>); break; \
-      case 2: fn = reinterpret_cast<const void *>(&attn_extend_kernel<DD, 2 * TT, kExtKB, kExtR, TT>); break; \
-      case 4: fn = reinterpret_cast<const void *>(&attn_extend_kernel<DD, 4 * TT, kExtKB, kExtR, TT>); break; \
-      case 8: fn = reinterpret_cast<const void *>(&attn_extend_kernel<DD, 8 * TT, kExtKB, kExtR, TT>); break; \
-      default: fn = reinterpret_cast<const void *>(&attn_extend_kernel<DD, 16, kExtKB, kExtR, 1>); break;     \
-    }                                                                                                       \
-  } while (0)
-  switch (g.D) {
-    case 64: if (TP == 2) MKV_EXT_FN(64, 2); else MKV_EXT_FN(64, 1); break;
-    case 128: if (TP == 2) MKV_EXT_FN(128, 2); else MKV_EXT_FN(128, 1); break;
-    default:
-      switch (W) {
-        case 4: fn = reinterpret_cast<const void *>(&attn_extend_kernel<256, 4, kExtKB, kExtR, 1>); break;
-        case 8: fn = reinterpret_cast<const void *>(&attn_extend_kernel<256, 8, kExtKB, kExtR, 1>); break;
-        default: fn = reinterpret_cast<const void *>(&attn_extend_kernel<256, 16, kExtKB, kExtR, 1>); break;
-      }
-      break;
-  }
-#undef MKV_EXT_FN
+  const void *fn = ext_kernel(g.D, W, TP);
   // When the launch leaves resident workgroup slots empty (short chunks over
   // long contexts: one workgroup per (sequence, KV head) streams a whole
   // context), each key range splits in up to 4, at least 8 steps apiece;
   // the f32 partials go to the pool-owned workspace and a second launch
   // merges them. Slots = resident workgroups per CU of this instantiation
-  // (occupancy query, once per pool) x CUs.
-  int &per_cu = p->ext_per_cu[g.D == 64 ? 0 : g.D == 128 ? 1 : 2][W == 1 ? 0 : W == 2 ? 1 : W == 4 ? 2 : W == 8 ? 3 : 4][TP - 1];
-  if (per_cu == 0) {
-    int n_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n_cu, fn, 64 * W, 0) != hipSuccess) {
-      (void)hipGetLastError();  // leave no sticky error: no splitting
-      n_cu = 0;
-    }
-    per_cu = n_cu > 0 ? n_cu : -1;
-  }
+  // (occupancy query, once per pool) x CUs; one per CU beside a decode launch.
+  const int per_cu = ext_resident_per_cu(p, fn, W, TP);
   const int cus = device_cus(p);
-  const int64_t slots = per_cu > 0 && cus > 0 ? (int64_t)per_cu * cus : 0;
+  const int64_t slots = per_cu > 0 && cus > 0 ? (beside ? 1 : (int64_t)per_cu) * cus : 0;
   const int64_t steps_max = ((int64_t)(max_ctx_len + kPageSize - 1) / kPageSize + kExtKB - 1) / kExtKB;
   if (per_split < slots)
     e.splits = (int32_t)std::min<int64_t>({(int64_t)split_cap, (slots + per_split - 1) / per_split,

@@ -53,6 +53,13 @@ struct Pool {
   int64_t coop_slots = -1;   // resident workgroups of the decode kernel (-1: not yet queried)
   int cus = 0;               // compute units of the device (0: not yet queried)
   int ext_per_cu[3][5][2] = {};  // resident extend workgroups per CU by (head_dim, waves, sub-tiles); 0: not yet queried
+  // The shared-prefix step's second stream, which runs the prefix tiles
+  // beside the suffix pieces, and its fork / join events (created on first
+  // use). beside: 1 when one prefix workgroup fits beside one decode-kernel
+  // workgroup on every CU, -1 when not, 0 before the first query.
+  hipStream_t aux = nullptr;
+  hipEvent_t aux_fork = nullptr, aux_join = nullptr;
+  int beside = 0;
   MetaSlot meta[kMetaSlots];
   int meta_next = 0;
   // The last host slot mapping staged by the append entry points: the slot

@@ -365,6 +365,9 @@ extern "C" int mkv_pool_destroy(mkv_pool *pool) {
   DeviceGuard guard(p->device);
   (void)hipDeviceSynchronize();
   if (p->ws) (void)hipFree(p->ws);
+  if (p->aux_fork) (void)hipEventDestroy(p->aux_fork);
+  if (p->aux_join) (void)hipEventDestroy(p->aux_join);
+  if (p->aux) (void)hipStreamDestroy(p->aux);
   meta_free(p);
   (void)hipFree(p->d_err);
   (void)hipFree(p->data);
