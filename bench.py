@@ -39,6 +39,7 @@ step of 8 chunk appends and 504 decodes over a 217,982-block (200 GB) pool.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import platform
@@ -53,6 +54,60 @@ if ROOT not in sys.path:
 
 PEAK_HBM_GBS = 8000.0
 METRIC = "paged KV append+decode-attn achieved HBM GB/s (% peak); decode tokens/s"
+
+_HIP = None  # the HIP runtime torch loaded (ctypes), once a timing event is made
+
+
+class _HipEvent:
+    """HIP timing event created with hipEventDisableSystemFence: its record
+    skips the system-scope release that a default event performs (an L2
+    write-back and invalidate), which would slow the launches it brackets.
+    Same calls as torch.cuda.Event: record(stream), elapsed_time(end) in ms
+    after a synchronize."""
+
+    def __init__(self, lib, handle):
+        self._lib, self.handle = lib, handle
+
+    def record(self, stream):
+        rc = self._lib.hipEventRecord(self.handle, ctypes.c_void_p(stream.cuda_stream))
+        if rc:
+            raise RuntimeError(f"hipEventRecord failed ({rc})")
+
+    def elapsed_time(self, end) -> float:
+        ms = ctypes.c_float()
+        rc = self._lib.hipEventElapsedTime(ctypes.byref(ms), self.handle, end.handle)
+        if rc:
+            raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
+        return ms.value
+
+    def __del__(self):
+        try:
+            self._lib.hipEventDestroy(self.handle)
+        except Exception:
+            pass
+
+
+def _event():
+    """A timing event for the timed regions: _HipEvent, or torch's event where
+    the runtime refuses the flag."""
+    global _HIP
+    import torch
+
+    if _HIP is None:
+        try:  # torch has loaded the runtime: this finds the same copy by its soname
+            lib = ctypes.CDLL("libamdhip64.so.7")
+            lib.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+            lib.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+            lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+            lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+            _HIP = lib
+        except OSError:
+            _HIP = False
+    if _HIP:
+        h = ctypes.c_void_p()
+        if _HIP.hipEventCreateWithFlags(ctypes.byref(h), 0x20000000) == 0:  # hipEventDisableSystemFence
+            return _HipEvent(_HIP, h)
+    return torch.cuda.Event(enable_timing=True)
 
 
 def parse():
@@ -246,7 +301,7 @@ def bench_prep(args):
             step()
         torch.cuda.synchronize()
         pool.check()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0, e1 = _event(), _event()
         t0 = time.perf_counter()
         e0.record(stream)
         for _ in range(args.steps):
@@ -343,7 +398,7 @@ def bench_wire(args):
             step()
         torch.cuda.synchronize()
         pool.check()
-        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+        evs = [[_event() for _ in range(3)] for _ in range(args.steps)]
         t0 = time.perf_counter()
         for s_ in range(args.steps):
             step(evs[s_])
@@ -470,7 +525,7 @@ def bench_move(args):
             launch(i)
         torch.cuda.synchronize()
         pool.check()
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        evs = [(_event(), _event())
                for _ in range(args.steps)]
         t0 = time.perf_counter()
         for i, (a, b) in enumerate(evs):
@@ -567,7 +622,7 @@ def bench_extend(args):
             launch()
         torch.cuda.synchronize()
         pool.check()
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        evs = [(_event(), _event())
                for _ in range(args.steps)]
         t0 = time.perf_counter()
         for a_, b_ in evs:
@@ -660,8 +715,8 @@ def _time_steps(step, steps, warmup, stream, L=None, every=4):
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    lay = {i: [torch.cuda.Event(enable_timing=True) for _ in range(L + 1)]
+    evs = [(_event(), _event()) for _ in range(steps)]
+    lay = {i: [_event() for _ in range(L + 1)]
            for i in range(0, steps, every)} if L else {}
     t0 = time.perf_counter()
     for i, (a_, b_) in enumerate(evs):
@@ -688,7 +743,7 @@ def _time_copies(pool, src, dst, reps, stream):
     s_, d_ = np.ascontiguousarray(src, np.uint32), np.ascontiguousarray(dst, np.uint32)
     pool.copy_blocks(s_, d_, stream=stream)
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    evs = [(_event(), _event()) for _ in range(reps)]
     for a_, b_ in evs:
         a_.record(stream)
         pool.copy_blocks(s_, d_, stream=stream)
@@ -1027,7 +1082,7 @@ def decode_config(name: str, steps: int, warmup: int, mode: str = "step", pieces
     # timed steps close to unperturbed).
     EVENT_EVERY = 4
     timed = [s_ for s_ in range(steps) if s_ % EVENT_EVERY == 0 and launch_events]
-    ev = {s_: [torch.cuda.Event(enable_timing=True) for _ in range(L + 1)] for s_ in timed}
+    ev = {s_: [_event() for _ in range(L + 1)] for s_ in timed}
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for s_ in range(steps):
