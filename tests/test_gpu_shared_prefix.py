@@ -149,3 +149,39 @@ def test_shared_prefix_errors():
             with pytest.raises(BackendError):  # f32 pools / head_dim 32 have no MFMA tiles
                 pool.decode_step_shared_prefix(0, sp, None, None, q, _i32([0]), _i32([0, 1, 2]), _i32([2, 3]))
             sp.close()
+
+
+def test_shared_prefix_beside_and_in_order_agree():
+    """A suffix plan built with pieces = 0 runs the prefix tiles beside the
+    suffixes on the pool's second stream where the geometry allows it (one
+    piece per CU); an explicit piece count runs the three launches in
+    order. Back-to-back steps with different queries on one stream, no
+    synchronisation between them, both forms against the oracle."""
+    import torch
+
+    L, Hq, Hkv, D = SHAPES["qwen7b"]
+    seqs, prefix = 96, 4100
+    batch = wl.shared_prefix_batch(seqs, prefix, 64, 700, wl.SplitMix64(127))
+    full = prefix // 16
+    sptr, sids, slen = _split_tables(batch, full)
+    desc = PoolDesc(L, Hkv, Hq, D, batch.num_blocks, "bf16")
+    host = normal(128, desc.shape, "bf16")
+    qs = [normal(129 + i, (seqs, Hq, D), "bf16") for i in range(3)]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    got = {}
+    with DeviceKvPool(desc) as pool:
+        pool.write(host)
+        pre, sp_, si_ = _i32(batch.meta["shared_blocks"]), _i32(sptr), _i32(sids)
+        for name, pieces in (("beside", 0), ("in_order", 2 * cus)):
+            plan = pool.plan_suffixes(slen, pieces=pieces)
+            if pieces == 0:
+                assert plan.info()["pieces"] <= cus
+            outs = [pool.decode_step_shared_prefix(L - 1, plan, None, None, to_device(q), pre, sp_, si_) for q in qs]
+            pool.check()
+            got[name] = [to_host(o) for o in outs]
+            plan.close()
+    for i, q in enumerate(qs):
+        ref = orc.decode_attention(odesc(desc), host, L - 1, widen(q), batch.block_indptr, batch.block_ids,
+                                   batch.ctx_lens)
+        assert_attention_close(got["beside"][i], ref, "bf16")
+        assert_attention_close(got["in_order"][i], ref, "bf16")
