@@ -564,6 +564,24 @@ def bench_move(args):
         cpu_s = (time.perf_counter() - c0) / reps
     launch_s = float(np.mean([a.elapsed_time(b) for a, b in evs])) / 1e3
     gbs = launch_bytes / launch_s / 1e9
+    ref_copy = None
+    if args.op == "append":  # a device copy of the same rows, as a floor for a launch of this size
+        src = torch.cat([kk.reshape(-1), vv.reshape(-1)])
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        cevs = [(_event(), _event()) for _ in range(args.steps)]
+        for a, b in cevs:
+            a.record(stream)
+            dst.copy_(src)
+            b.record(stream)
+        torch.cuda.synchronize()
+        copy_s = float(np.mean([a.elapsed_time(b) for a, b in cevs])) / 1e3
+        copy_bytes = 2 * src.numel() * src.element_size()
+        ref_copy = {"what": "torch device copy of the same K/V rows (read + write)", "bytes": copy_bytes,
+                    "avg_launch_us": round(copy_s * 1e6, 2), "GB_s": round(copy_bytes / copy_s / 1e9, 2)}
+        del src, dst
     print(json.dumps({
         "metric": f"{kernel} achieved HBM GB/s",
         "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -576,6 +594,7 @@ def bench_move(args):
                      "bytes_per_launch": launch_bytes, "avg_launch_us": round(launch_s * 1e6, 2)},
         "cpu_baseline": {"value": round(cpu_bytes / cpu_s / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
                          "sample": f"{sample}, {reps} repetitions"},
+        **({"reference_copy": ref_copy} if ref_copy else {}),
     }), flush=True)
 
 
