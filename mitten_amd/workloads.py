@@ -189,7 +189,7 @@ def pool_pressure_step(num_blocks: int, num_seqs: int, chunk: int, chunk_seqs: i
     return batch, np.concatenate(chunk_slots).astype(np.int32), lengths.astype(np.int32)
 
 
-# Benchmark configurations (shapes of the BASELINE configurations).
+# Benchmark configurations: the model shapes and batches the benchmarks are quoted on.
 CONFIGS = {
     "qwen2.5-0.5b": dict(num_layers=24, num_q_heads=14, num_kv_heads=2, head_dim=64, dtype="f32",
                          batch=8, ctx_lo=32, ctx_hi=512, index=0),
