@@ -37,6 +37,7 @@
 #include <cstring>
 #include <mutex>
 #include <new>
+#include <type_traits>
 #include <vector>
 
 #include "mkv_internal.h"
@@ -1292,6 +1293,9 @@ attn_coop_kernel(KArgs a, PlanDev pd) {
 // step raise the register count past two workgroups per CU.
 constexpr int kExtKB = 2;  // blocks per softmax step of the extend kernel
 constexpr int kExtR = 2;   // ring depth (steps) of the extend kernel
+// Block ids a workgroup stages in LDS for its unmasked steps (16k keys);
+// a longer key range takes the scalar table reads throughout.
+constexpr int kExtIdCap = 1024;
 
 struct ExtArgs {
   const int32_t *q_indptr;  // [B+1] query tokens of each sequence in q / o; null: one sequence of
@@ -1430,6 +1434,59 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
     }
   };
 
+  // Unmasked steps take a lean path. The ids of the workgroup's blocks
+  // [kfirst, kend) are staged in LDS and range-checked once (any rejected id:
+  // the generic path throughout, which masks it and records the error).
+  // Chunk c = 64 * (wave + W * i) + lane of a step lies in one (block, K/V)
+  // plane per wave, so a load is a wave-uniform base (block id, plane) plus a
+  // lane offset (row, chunk, head) fixed for the whole launch.
+  __shared__ int32_t ids_s[kExtIdCap];
+  const int kfirst = st0 * KB, kend = min(st1 * KB, n);
+  // (More than four loads per lane and step would hold more registers than the
+  // lean path saves: those launches keep the generic path.)
+  int fast = LPL <= 4 && kend - kfirst <= kExtIdCap;
+  if (fast) {
+    int badl = 0;
+    const int32_t *tg = a.ids + tab0 + kfirst;
+    for (int i = (int)threadIdx.x; i < kend - kfirst; i += 64 * W) {
+      const int32_t id = tg[i];
+      badl |= (id < 0) | (id >= a.nblocks);
+      ids_s[i] = id;
+    }
+    fast = !__syncthreads_or(badl);
+  }
+  fast = __builtin_amdgcn_readfirstlane(fast);
+  // A wave past the step's chunks (head_dim 64 with 16 waves) loads the
+  // step's last chunks again and does not store them: one load form, so the
+  // compiler's in-order load counting stays exact.
+  constexpr bool kAllVal = NCH % (64 * W) == 0;
+  uint32_t flo[LPL], fwr[LPL];  // lane offset in the block; LDS offset in one ring buffer
+  int fkb[LPL];                 // wave-uniform block of the step
+  const uint8_t *fpl[LPL];      // wave-uniform plane (K or V)
+  bool fval[LPL];               // wave-uniform: the wave's chunk is stored
+#pragma unroll
+  for (int i = 0; i < LPL; i++) {
+    const int cw = 64 * (wave + W * i);
+    fval[i] = kAllVal || cw < NCH;
+    const int cu = min(cw, NCH - 64);
+    const int pl = cu / (16 * CPR), kv = pl & 1;
+    fkb[i] = pl >> 1;
+    fpl[i] = kv ? a.v_plane : a.k_plane;
+    const int rem2 = cu % (16 * CPR) + lane, row = rem2 / CPR, cc = rem2 % CPR;
+    flo[i] = (uint32_t)(row * (int)a.row_bytes + h * RB + 16 * cc);
+    fwr[i] = (uint32_t)((2 * fkb[i] + kv) * TILE + row * RB + ((cc ^ (kv ? ext_v_swz(row, CPR) : ext_k_swz(row, CPR))) << 4));
+  }
+  // A step whose KB blocks all lie in [kfirst, kend).
+  auto issue_fast = [&](u32x4 (&d)[LPL], uint32_t &bad, int step) {
+    bad = 0;
+#pragma unroll
+    for (int i = 0; i < LPL; i++) {
+      const int32_t bk = __builtin_amdgcn_readfirstlane(ids_s[step * KB + fkb[i] - kfirst]);
+      d[i] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4 *>(fpl[i] + (int64_t)bk * a.block_bytes + flo[i]));
+    }
+  };
+
   MStateT<D> st;
 #pragma unroll
   for (int nn = 0; nn < NT; nn++) st.O[nn] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1445,12 +1502,21 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
   for (int nn = 0; nn < NT; nn++)
     v_rd[nn] = vrow * RB + (((2 * nn + (rq >> 1)) ^ ext_v_swz(vrow, CPR)) << 4) + 8 * (rq & 1);
 
-  auto stage = [&](int s, int step) {
-    issue(ring[(s + R - 1) % R], badr[(s + R - 1) % R], step + R - 1);
+  // FAST: every block of the step is in range and fully visible to every
+  // query of the workgroup (no mask), and the step issued R - 1 ahead lies
+  // in the staged ids.
+  auto stage = [&](auto fast_c, int s, int step) {
+    constexpr bool FAST = decltype(fast_c)::value;
+    if constexpr (FAST) issue_fast(ring[(s + R - 1) % R], badr[(s + R - 1) % R], step + R - 1);
+    else issue(ring[(s + R - 1) % R], badr[(s + R - 1) % R], step + R - 1);
     // step = (multiple of R) + s: buffer s & 1 alternates like step & 1 and
     // is a compile-time constant here (immediate LDS offsets).
 #pragma unroll
     for (int i = 0; i < LPL; i++) {
+      if constexpr (FAST) {
+        if (kAllVal || fval[i]) *reinterpret_cast<u32x4 *>(&tiles[s & 1][0][0][0] + fwr[i]) = ring[s][i];
+        continue;
+      }
       const int c = (int)threadIdx.x + 64 * W * i;
       if (c < NCH) {
         const int kb = c / BCH, rem = c % BCH;
@@ -1465,8 +1531,8 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
     }
     __syncthreads();
     if (!computes) return;
-    const uint32_t bad = badr[s];
-    if (bad && lane == 0) record_error(a.d_err, MKV_DEVERR_BLOCK);
+    const uint32_t bad = FAST ? 0u : badr[s];
+    if (!FAST && bad && lane == 0) record_error(a.d_err, MKV_DEVERR_BLOCK);
     // Raw scores of the step's blocks (masked ones -inf). Lane holds
     // sr[kb][i] = S[key 16k + 4*g4 + i][query position qlo + lane%16].
     float sr[KB][4];
@@ -1475,7 +1541,7 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
 #pragma unroll
     for (int kb = 0; kb < KB; kb++) {
       const int k = step * KB + kb;
-      if (k >= nw) {  // uniform: past this sub-tile's last position (or past n in the last step)
+      if (!FAST && k >= nw) {  // uniform: past this sub-tile's last position (or past n in the last step)
 #pragma unroll
         for (int i = 0; i < 4; i++) sr[kb][i] = -INFINITY;
         masked = true;
@@ -1500,7 +1566,7 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
         S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kq[r]), qop[r], S, 0, 0, 0);
       if constexpr (kPrio) __builtin_amdgcn_s_setprio(0);
       const bool kbad = (bad >> kb) & 1;
-      const bool full = !kbad && kPageSize * k + kPageSize - 1 <= qlo && kPageSize * k + kPageSize <= ctx;
+      const bool full = FAST || (!kbad && kPageSize * k + kPageSize - 1 <= qlo && kPageSize * k + kPageSize <= ctx);
 #pragma unroll
       for (int i = 0; i < 4; i++) sr[kb][i] = S[i];
       if (!full) {  // only the last blocks of a tile (and rejected ones)
@@ -1532,14 +1598,42 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
       st.m = mn;
       thr = (mn + kRescaleSlack) * inv_sl2;
     }
+    if constexpr (FAST && KB == 2) {
+      // Both blocks in one full-rate 16x16x32 product per 16 dims: lane
+      // group g4's k-slots 0-3 are keys 4*g4..+3 of the first block and 4-7
+      // the same keys of the second, in P^T (the score layout) and in V^T
+      // (one transposed read per block).
+      uint32_t pk[4];
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++) {
+        float pr[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) pr[i] = fast_exp2(fmaf(sr[kb][i], a.sl2, -st.m));
+        st.l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+        pk[2 * kb] = pack_bf16x2(pr[0], pr[1]);
+        pk[2 * kb + 1] = pack_bf16x2(pr[2], pr[3]);
+      }
+      const bf16x8 pb = __builtin_bit_cast(bf16x8, u32x4{pk[0], pk[1], pk[2], pk[3]});
+      const uint8_t *tv0 = tiles[s & 1][0][1], *tv1 = tiles[s & 1][1][1];
+#pragma unroll
+      for (int nn = 0; nn < NT; nn++) {
+        const i16x4s r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(tv0 + v_rd[nn]));
+        const i16x4s r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(tv1 + v_rd[nn]));
+        const uint64_t w0 = __builtin_bit_cast(uint64_t, r0), w1 = __builtin_bit_cast(uint64_t, r1);
+        const bf16x8 va = __builtin_bit_cast(bf16x8, u32x4{(uint32_t)w0, (uint32_t)(w0 >> 32), (uint32_t)w1,
+                                                            (uint32_t)(w1 >> 32)});
+        st.O[nn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, st.O[nn], 0, 0, 0);
+      }
+      return;
+    }
 #pragma unroll
     for (int kb = 0; kb < KB; kb++) {
       const int k = step * KB + kb;
-      if (k >= nw) continue;  // uniform
+      if (!FAST && k >= nw) continue;  // uniform
       float pr[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) pr[i] = fast_exp2(fmaf(sr[kb][i], a.sl2, -st.m));
-      if (masked) {  // a fully masked column has m = -inf: keep its p at 0, not NaN
+      if (!FAST && masked) {  // a fully masked column has m = -inf: keep its p at 0, not NaN
 #pragma unroll
         for (int i = 0; i < 4; i++)
           if (sr[kb][i] == -INFINITY) pr[i] = 0.0f;
@@ -1560,15 +1654,25 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
 
 #pragma unroll
   for (int s = 0; s < R - 1; s++) issue(ring[s], badr[s], st0 + s);
-  const int nfull = (st1 - st0) / R;
+  // Fast steps: [st0, fast_end), blocks below the workgroup's first query
+  // position and below ctx (all keys visible to all its queries), with the
+  // steps issued R - 1 ahead inside [kfirst, kend).
+  const int fb = e.causal ? min((ctx - nq + 16 * TP * t + 1) / kPageSize, ctx / kPageSize) : ctx / kPageSize;
+  const int fast_end = fast ? max(st0, min(min(st1, fb / KB), kend / KB - (R - 1))) : st0;
+  const std::integral_constant<bool, true> kFast;
+  const std::integral_constant<bool, false> kGeneric;
   int k0 = st0;
-  for (int it = 0; it < nfull; it++, k0 += R) {
+  for (int it = 0, nit = (fast_end - st0) / R; it < nit; it++, k0 += R) {
 #pragma unroll
-    for (int s = 0; s < R; s++) stage(s, k0 + s);
+    for (int s = 0; s < R; s++) stage(kFast, s, k0 + s);
+  }
+  for (int it = 0, nit = (st1 - k0) / R; it < nit; it++, k0 += R) {
+#pragma unroll
+    for (int s = 0; s < R; s++) stage(kGeneric, s, k0 + s);
   }
 #pragma unroll
   for (int s = 0; s < R - 1; s++)
-    if (k0 + s < st1) stage(s, k0 + s);
+    if (k0 + s < st1) stage(kGeneric, s, k0 + s);
 
   if (!computes) return;
   st.l += __shfl_xor(st.l, 16);
