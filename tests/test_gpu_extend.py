@@ -105,6 +105,19 @@ def test_extend_long_context_chunk():
     assert_attention_close(got, ref, "bf16")
 
 
+def test_extend_key_range_past_the_staged_ids():
+    """A workgroup whose key range holds more blocks than the kernel stages
+    in LDS for its unmasked steps (1,024 ids) takes the generic step
+    throughout: one 16-token chunk at the end of a 16,900-token context
+    (1,057 blocks), beside 255 short prompts so that the launch fills the
+    device and the long range is not split."""
+    ctx = [16900] + [16] * 255
+    nq = [16] * 256
+    got, ref, dec, q_indptr = _case("qwen7b", ctx, nq, 98)
+    assert_attention_close(got, ref, "bf16")
+    assert_attention_close(dec, ref[q_indptr[1:] - 1], "bf16")
+
+
 def test_extend_errors_are_reported():
     Hq, Hkv, D = SHAPES["qwen7b"]
     desc = PoolDesc(1, Hkv, Hq, D, 10, "bf16")
