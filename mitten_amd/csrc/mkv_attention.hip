@@ -1284,7 +1284,10 @@ attn_coop_kernel(KArgs a, PlanDev pd) {
 // bank-conflict-free swizzle), loaded cooperatively one step of two blocks
 // ahead; scores, online softmax and the V^T transpose reads follow the
 // decode kernel, with the causal mask applied on blocks that reach past a
-// sub-tile's first position.
+// sub-tile's first position. Steps whose keys every query of the workgroup
+// sees (all but the last one or two of a tile) run a lean form: block ids
+// staged in LDS and checked once, wave-uniform load bases, no masks, and the
+// PV product on one full-rate 16x16x32 MFMA per 16 dims over both blocks.
 // ===========================================================================
 
 // Extend kernel: two blocks (32 keys) per softmax step, steps loaded one
@@ -1440,11 +1443,12 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
   // Chunk c = 64 * (wave + W * i) + lane of a step lies in one (block, K/V)
   // plane per wave, so a load is a wave-uniform base (block id, plane) plus a
   // lane offset (row, chunk, head) fixed for the whole launch.
-  __shared__ int32_t ids_s[kExtIdCap];
-  const int kfirst = st0 * KB, kend = min(st1 * KB, n);
   // (More than four loads per lane and step would hold more registers than the
   // lean path saves: those launches keep the generic path.)
-  int fast = LPL <= 4 && kend - kfirst <= kExtIdCap;
+  constexpr bool kLean = LPL <= 4;
+  __shared__ int32_t ids_s[kLean ? kExtIdCap : 1];
+  const int kfirst = st0 * KB, kend = min(st1 * KB, n);
+  int fast = kLean && kend - kfirst <= kExtIdCap;
   if (fast) {
     int badl = 0;
     const int32_t *tg = a.ids + tab0 + kfirst;
