@@ -1311,6 +1311,7 @@ struct ExtArgs {
   int32_t causal;           // 0: every query sees all ctx keys (a shared prefix's decode queries)
   int32_t partial;          // 1: f32 partials whatever the split count, merged by the caller
   int32_t v_nq, v_ctx;      // the one sequence when q_indptr is null
+  int32_t hgroups;          // workgroups per (tile, KV head): each takes W / TP consecutive query heads
 };
 
 // Workgroups are dealt to the 8 XCDs round-robin by linear index. The
@@ -1318,20 +1319,22 @@ struct ExtArgs {
 // (L % 8) * per_xcd + L / 8, so each XCD receives a contiguous run of
 // logical indices: the query tiles of one (sequence, KV head) share that
 // XCD's L2 while they stream the same K/V. Logical index = (tiles - 1 -
-// tile) + tiles * (head + Hkv * (sequence + B * split)); false for the
-// padding past the last one. The last tile of a chunk attends the most keys,
+// tile) + tiles * (group + hgroups * (head + Hkv * (sequence + B * split)));
+// false for the padding past the last one. `h` returns head * hgroups +
+// group. The last tile of a chunk attends the most keys,
 // so a sequence's tiles start longest first (causal 2k-token prompts: 518 ->
 // 487 us), leaving the short ones for the tail.
 __device__ __forceinline__ bool ext_tile(const ExtArgs &e, int Hkv, int &t, int &h, int &b, int &sp) {
   const int L = blockIdx.x;
   const int logical = (L & 7) * e.per_xcd + (L >> 3);
-  const int per_split = e.tiles * Hkv * e.B;
+  const int heads = Hkv * e.hgroups;
+  const int per_split = e.tiles * heads * e.B;
   if (logical >= per_split * e.splits) return false;
   const int r = logical % per_split;
   sp = logical / per_split;
   t = e.tiles - 1 - r % e.tiles;
-  h = (r / e.tiles) % Hkv;
-  b = r / (e.tiles * Hkv);
+  h = (r / e.tiles) % heads;
+  b = r / (e.tiles * heads);
   return true;
 }
 
@@ -1351,8 +1354,9 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int m16 = lane & 15, g4 = lane >> 4, a4 = m16 >> 2, rq = m16 & 3;
-  int t, h, b, sp;
-  if (!ext_tile(e, a.Hkv, t, h, b, sp)) return;
+  int t, hx, b, sp;
+  if (!ext_tile(e, a.Hkv, t, hx, b, sp)) return;
+  const int h = hx / e.hgroups, hg = hx % e.hgroups;  // KV head; group of W / TP query heads
   const bool virt = e.q_indptr == nullptr;  // one sequence; the host checked its table length
   const int q0 = virt ? 0 : e.q_indptr[b], nq = virt ? e.v_nq : e.q_indptr[b + 1] - q0;
   if (nq <= 0 || 16 * TP * t >= nq) return;
@@ -1388,8 +1392,9 @@ __global__ void __launch_bounds__(64 * W) attn_extend_kernel(KArgs a, ExtArgs e)
   const int nsteps_all = (n + KB - 1) / KB;
   const int sps = (nsteps_all + e.splits - 1) / e.splits;
   const int st0 = min(sp * sps, nsteps_all), st1 = min(st0 + sps, nsteps_all);
-  const bool computes = hw < a.G;
-  const int hq = h * a.G + min(hw, a.G - 1);
+  const int hslot = hg * WG + hw;  // this wave's query head among the KV head's G
+  const bool computes = hslot < a.G;
+  const int hq = h * a.G + min(hslot, a.G - 1);
   const int qp = e.causal ? qlo + m16 : ctx - 1;  // this lane's query position (rows past nq: unused)
   const int64_t spare = dummy_offset(a);
 
@@ -2746,11 +2751,8 @@ static const void *ext_kernel(int D, int W, int TP) {
     case 64: if (TP == 2) MKV_EXT_FN(64, 2); else MKV_EXT_FN(64, 1); break;
     case 128: if (TP == 2) MKV_EXT_FN(128, 2); else MKV_EXT_FN(128, 1); break;
     default:
-      switch (W) {
-        case 4: fn = reinterpret_cast<const void *>(&attn_extend_kernel<256, 4, kExtKB, kExtR, 1>); break;
-        case 8: fn = reinterpret_cast<const void *>(&attn_extend_kernel<256, 8, kExtKB, kExtR, 1>); break;
-        default: fn = reinterpret_cast<const void *>(&attn_extend_kernel<256, 16, kExtKB, kExtR, 1>); break;
-      }
+      fn = W == 4 ? reinterpret_cast<const void *>(&attn_extend_kernel<256, 4, kExtKB, kExtR, 1>)
+                  : reinterpret_cast<const void *>(&attn_extend_kernel<256, 8, kExtKB, kExtR, 1>);
       break;
   }
 #undef MKV_EXT_FN
@@ -2786,7 +2788,7 @@ static int launch_ext_tiles(Pool *p, KArgs &a, ExtArgs &e, int split_cap, hipStr
   const Geom &g = p->g;
   const int G = g.Hq / g.Hkv;
   const int64_t num_seqs = e.B, max_q_len = e.max_q, max_ctx_len = e.max_ctx;
-  if (((max_q_len + 15) / 16 * g.Hkv * num_seqs) * split_cap + 8 > INT32_MAX)
+  if (((max_q_len + 15) / 16 * g.Hq * num_seqs) * split_cap + 8 > INT32_MAX)
     return set_error(MKV_ERR_INVALID_ARGUMENT, "grid too large");
   e.splits = 1;
   // Waves per 16-position sub-tile: the next power of two >= G. Two
@@ -2797,12 +2799,16 @@ static int launch_ext_tiles(Pool *p, KArgs &a, ExtArgs &e, int split_cap, hipStr
   // 534 us; 16-token chunks would leave half the waves idle (168 -> 220 us).
   // At head_dim 256 a workgroup has at least 4 waves: waves past G only
   // share the loads, and one or two waves would each carry 16-32 loads per
-  // ring stage (register spills).
-  const int WG = G <= 1 && g.D < 256 ? 1 : G <= 2 && g.D < 256 ? 2 : G <= 4 ? 4 : G <= 8 ? 8 : 16;
+  // ring stage (register spills). It has at most 8: more than 8 query heads
+  // per KV head go to groups of 8 in workgroups of their own (16 waves cap
+  // the registers at 128, and the head_dim-256 state then spills).
+  const int WG = G <= 1 && g.D < 256 ? 1 : G <= 2 && g.D < 256 ? 2 : G <= 4 ? 4 : G <= 8 || g.D == 256 ? 8 : 16;
+  e.hgroups = (G + WG - 1) / WG;
   const int TP = (!beside && WG <= 8 && g.D <= 128 && max_q_len > 16) ? 2 : 1;
   const int W = WG * TP;
   const int64_t tiles = ((int64_t)max_q_len + 16 * TP - 1) / (16 * TP);
-  const int64_t per_split = tiles * g.Hkv * num_seqs;  // (tile, KV head, sequence) workgroups
+  // (tile, KV head, head group, sequence) workgroups
+  const int64_t per_split = tiles * g.Hkv * e.hgroups * num_seqs;
   const void *fn = ext_kernel(g.D, W, TP);
   // When the launch leaves resident workgroup slots empty (short chunks over
   // long contexts: one workgroup per (sequence, KV head) streams a whole
@@ -2833,7 +2839,7 @@ static int launch_ext_tiles(Pool *p, KArgs &a, ExtArgs &e, int split_cap, hipStr
     a.ws_ml = reinterpret_cast<float *>(p->ws);
     a.ws_o = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(p->ws) + ml_bytes);
   }
-  const int64_t total = per_split * e.splits;  // linear index -> (tile, KV head, sequence, split), grouped by XCD
+  const int64_t total = per_split * e.splits;  // linear index -> (tile, KV head, group, sequence, split), by XCD
   e.tiles = (int32_t)tiles;
   e.per_xcd = (int32_t)((total + 7) / 8);
   const dim3 grid((unsigned)(8 * (int64_t)e.per_xcd)), block(64 * W);
