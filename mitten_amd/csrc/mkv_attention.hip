@@ -2596,9 +2596,15 @@ extern "C" int mkv_decode_step_shared_prefix(mkv_pool *pool, const mkv_decode_pl
   //    work only, so they skip the system-scope fence.
   const bool beside = pl->beside;
   if (beside && !p->aux) {
-    MKV_CHECK_HIP(hipStreamCreateWithFlags(&p->aux, hipStreamNonBlocking));
-    MKV_CHECK_HIP(hipEventCreateWithFlags(&p->aux_fork, hipEventDisableTiming | hipEventDisableSystemFence));
-    MKV_CHECK_HIP(hipEventCreateWithFlags(&p->aux_join, hipEventDisableTiming | hipEventDisableSystemFence));
+    // The stream is published last, so a failed creation leaves none of the
+    // three half made for the next call.
+    if (!p->aux_fork)
+      MKV_CHECK_HIP(hipEventCreateWithFlags(&p->aux_fork, hipEventDisableTiming | hipEventDisableSystemFence));
+    if (!p->aux_join)
+      MKV_CHECK_HIP(hipEventCreateWithFlags(&p->aux_join, hipEventDisableTiming | hipEventDisableSystemFence));
+    hipStream_t aux = nullptr;
+    MKV_CHECK_HIP(hipStreamCreateWithFlags(&aux, hipStreamNonBlocking));
+    p->aux = aux;
   }
   KArgs ap = make_kargs(p, layer, d_q, d_o, nullptr, d_prefix_ids, scale, flags, true);
   ExtArgs e{};
