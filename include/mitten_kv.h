@@ -223,7 +223,9 @@ MKV_API int mkv_decode_attention_static(mkv_pool *pool, int32_t layer, const voi
 /* ---- host metadata (the engine's u32 form) ------------------------------- */
 
 /* mkv_append with a host slot mapping (slot = page * page_size + offset, as
- * the engine derives it from kv_pages: prefill.rs:72-81, scheduler.rs:42-57). */
+ * the engine derives it from kv_pages: prefill.rs:72-81, scheduler.rs:42-57).
+ * A mapping equal to the previous call's (same stream) is not uploaded
+ * again. */
 MKV_API int mkv_append_host(mkv_pool *pool, int32_t layer, const void *d_k, const void *d_v,
                             const uint32_t *h_slot_mapping, int32_t num_tokens, void *stream);
 /* mkv_append_all_layers with a host slot mapping. */
@@ -231,7 +233,8 @@ MKV_API int mkv_append_all_layers_host(mkv_pool *pool, const void *d_k, const vo
                                        const uint32_t *h_slot_mapping, int32_t num_tokens, void *stream);
 /* mkv_gather with host tables: sequence b's first h_ctx_lens[b] tokens
  * through table h_block_ids[h_block_indptr[b] ..), written at element offset
- * (sum of the earlier h_ctx_lens) * Hkv * D of the outputs. */
+ * (sum of the earlier h_ctx_lens) * Hkv * D of the outputs. Tables equal to
+ * the previous call's (same stream) are not uploaded again. */
 MKV_API int mkv_gather_host(mkv_pool *pool, int32_t layer, const uint32_t *h_block_indptr,
                             const uint32_t *h_block_ids, const int32_t *h_ctx_lens, int32_t num_seqs,
                             void *d_out_k, void *d_out_v, int64_t out_capacity_tokens, void *stream);
@@ -243,7 +246,8 @@ MKV_API int mkv_copy_blocks_host(mkv_pool *pool, const uint32_t *h_src_blocks, c
 /* mkv_extend_attention with host metadata: sequence b has h_q_lens[b] new
  * tokens (its extend_len, request.rs:46-54; 0 <= q_len <= ctx) whose query
  * rows follow those of sequence b-1 in d_q / d_o, and h_ctx_lens[b] tokens
- * in its table (the chunk included). */
+ * in its table (the chunk included). Metadata equal to the previous call's
+ * (same stream) is not uploaded again. */
 MKV_API int mkv_extend_attention_host(mkv_pool *pool, int32_t layer, const void *d_q, void *d_o,
                                       const int32_t *h_q_lens, const int32_t *h_ctx_lens,
                                       const uint32_t *h_block_indptr, const uint32_t *h_block_ids,

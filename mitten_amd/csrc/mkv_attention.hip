@@ -2723,15 +2723,18 @@ extern "C" int mkv_extend_attention_host(mkv_pool *pool, int32_t layer, const vo
   const size_t n = 3 * (size_t)num_seqs + 2 + nids;  // q_indptr | indptr | ctx | ids
   DeviceGuard guard(p->device);
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
-  MetaSlot *sl = nullptr;
-  if ((rc = meta_acquire(p, n, hs, &sl))) return rc;
-  int32_t *qp = sl->h, *ip = qp + num_seqs + 1, *cl = ip + num_seqs + 1, *ix = cl + num_seqs;
+  // Every layer of a step passes the same chunks and tables: uploaded once
+  // per step.
+  std::vector<int32_t> &stg = p->stage_tmp;
+  stg.resize(n);
+  int32_t *qp = stg.data(), *ip = qp + num_seqs + 1, *cl = ip + num_seqs + 1, *ix = cl + num_seqs;
   qp[0] = 0;
   for (int32_t b = 0; b < num_seqs; b++) qp[b + 1] = qp[b] + h_q_lens[b];
   for (int32_t b = 0; b <= num_seqs; b++) ip[b] = (int32_t)h_block_indptr[b];
   std::memcpy(cl, h_ctx_lens, (size_t)num_seqs * 4);
   if (nids) std::memcpy(ix, h_block_ids, nids * 4);
-  if ((rc = meta_upload(sl, n, hs))) return rc;
+  MetaSlot *sl = nullptr;
+  if ((rc = stage_cached(p, p->extend_cache, stg.data(), n, hs, &sl))) return rc;
   const int32_t *d = sl->d;
   rc = mkv_extend_attention(pool, layer, d_q, d_o, d, d + num_seqs + 1, d + 3 * num_seqs + 2, d + 2 * num_seqs + 2,
                             num_seqs, max_q, max_ctx, scale, flags, stream);

@@ -41,6 +41,15 @@ struct MetaSlot {
   uint64_t gen = 0;  // counts acquisitions (a staged array is current while gen is unchanged)
 };
 
+// The last array one entry point staged: the slot that holds it, that
+// slot's generation then, the stream it was uploaded on, and the values.
+struct StagedCache {
+  int slot = -1;
+  uint64_t gen = 0;
+  hipStream_t stream = nullptr;
+  std::vector<int32_t> vals;
+};
+
 struct Pool {
   mkv_pool_desc desc;
   Geom g;
@@ -62,12 +71,11 @@ struct Pool {
   int beside = 0;
   MetaSlot meta[kMetaSlots];
   int meta_next = 0;
-  // The last host slot mapping staged by the append entry points: the slot
-  // that holds it, its generation and stream, and the values.
-  int app_slot = -1;
-  uint64_t app_gen = 0;
-  hipStream_t app_stream = nullptr;
-  std::vector<uint32_t> app_vals;
+  // The last host arrays staged by the append, gather and extend entry
+  // points (an engine step passes the same ones to every layer), and a
+  // scratch array to assemble a staged array in.
+  StagedCache app_cache, gather_cache, extend_cache;
+  std::vector<int32_t> stage_tmp;
 };
 
 // Next staging slot with room for n int32 values (waits for its previous
@@ -77,6 +85,11 @@ int meta_acquire(Pool *p, size_t n, hipStream_t hs, MetaSlot **out);
 int meta_upload(MetaSlot *s, size_t n, hipStream_t hs);
 int meta_release(MetaSlot *s, hipStream_t hs);
 void meta_free(Pool *p);
+// meta_acquire + fill + meta_upload of h[0..n), unless the cache's last
+// array equals it, was uploaded on the same stream, and its slot has not
+// been claimed since: then that device copy is handed out again. Either
+// way the caller launches from (*out)->d and calls meta_release.
+int stage_cached(Pool *p, StagedCache &c, const int32_t *h, size_t n, hipStream_t hs, MetaSlot **out);
 
 // Looks up this device's address of the static scratch of
 // mkv_decode_attention_static (once per device; called by mkv_pool_create).

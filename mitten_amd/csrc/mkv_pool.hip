@@ -515,30 +515,34 @@ extern "C" int mkv_copy_blocks(mkv_pool *pool, const int32_t *d_src_blocks,
 
 // ---- C ABI: host metadata (the engine's u32 form) --------------------------------------
 
-// Stages a host slot mapping for the append entry points. Every layer of an
-// engine step appends the same tokens, so a mapping equal to the previous
-// one, staged on the same stream into a slot not claimed since, is launched
-// from that device copy without another upload.
-static int stage_append_slots(Pool *p, const uint32_t *h, int32_t n, hipStream_t hs, MetaSlot **out) {
-  if (p->app_slot >= 0 && p->app_stream == hs && p->app_vals.size() == (size_t)n) {
-    MetaSlot *sl = &p->meta[p->app_slot];
-    if (sl->gen == p->app_gen && std::memcmp(p->app_vals.data(), h, (size_t)n * 4) == 0) {
+int mkv::stage_cached(Pool *p, StagedCache &c, const int32_t *h, size_t n, hipStream_t hs, MetaSlot **out) {
+  if (c.slot >= 0 && c.stream == hs && c.vals.size() == n) {
+    MetaSlot *sl = &p->meta[c.slot];
+    if (sl->gen == c.gen && std::memcmp(c.vals.data(), h, n * 4) == 0) {
       *out = sl;
       return MKV_OK;
     }
   }
+  c.slot = -1;
   const int idx = p->meta_next;  // the slot meta_acquire hands out
   MetaSlot *sl = nullptr;
   int rc = meta_acquire(p, n, hs, &sl);
   if (rc) return rc;
-  std::memcpy(sl->h, h, (size_t)n * 4);
+  std::memcpy(sl->h, h, n * 4);
   if ((rc = meta_upload(sl, n, hs))) return rc;
-  p->app_slot = idx;
-  p->app_gen = sl->gen;
-  p->app_stream = hs;
-  p->app_vals.assign(h, h + n);
+  c.slot = idx;
+  c.gen = sl->gen;
+  c.stream = hs;
+  c.vals.assign(h, h + n);
   *out = sl;
   return MKV_OK;
+}
+
+// Stages a host slot mapping for the append entry points. Every layer of an
+// engine step appends the same tokens, so the mapping is uploaded once per
+// step (stage_cached).
+static int stage_append_slots(Pool *p, const uint32_t *h, int32_t n, hipStream_t hs, MetaSlot **out) {
+  return stage_cached(p, p->app_cache, reinterpret_cast<const int32_t *>(h), (size_t)n, hs, out);
 }
 
 extern "C" int mkv_append_host(mkv_pool *pool, int32_t layer, const void *d_k, const void *d_v,
@@ -599,14 +603,16 @@ extern "C" int mkv_gather_host(mkv_pool *pool, int32_t layer, const uint32_t *h_
   const size_t n = 2 * ((size_t)num_seqs + 1) + nids;  // indptr | ctx_indptr | ids
   DeviceGuard guard(p->device);
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
-  MetaSlot *sl = nullptr;
-  if ((rc = meta_acquire(p, n, hs, &sl))) return rc;
-  int32_t *ip = sl->h, *cp = ip + num_seqs + 1, *ix = cp + num_seqs + 1;
+  // Every layer of a step gathers the same tables: uploaded once per step.
+  std::vector<int32_t> &st = p->stage_tmp;
+  st.resize(n);
+  int32_t *ip = st.data(), *cp = ip + num_seqs + 1, *ix = cp + num_seqs + 1;
   cp[0] = 0;
   for (int32_t b = 0; b <= num_seqs; b++) ip[b] = (int32_t)h_block_indptr[b];
   for (int32_t b = 0; b < num_seqs; b++) cp[b + 1] = cp[b] + h_ctx_lens[b];
   if (nids) std::memcpy(ix, h_block_ids, nids * 4);
-  if ((rc = meta_upload(sl, n, hs))) return rc;
+  MetaSlot *sl = nullptr;
+  if ((rc = stage_cached(p, p->gather_cache, st.data(), n, hs, &sl))) return rc;
   rc = mkv_gather(pool, layer, sl->d, sl->d + 2 * (num_seqs + 1), sl->d + num_seqs + 1, num_seqs, max_ctx,
                   d_out_k, d_out_v, out_capacity_tokens, stream);
   const int rr = meta_release(sl, hs);

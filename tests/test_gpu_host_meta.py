@@ -425,3 +425,80 @@ def test_append_host_reuses_an_equal_mapping_and_follows_a_changed_one():
     pool.check()
     assert np.array_equal(bits(pool.read()), bits(want))
     pool.close()
+
+
+def test_gather_host_reuses_equal_tables_and_follows_changed_ones():
+    """Every layer of a step gathers the same tables: the library uploads
+    equal tables once. Tables changed in place under the same arrays, new
+    context lengths, staging slots claimed by other host calls in between,
+    and another stream all get a fresh upload; every gather is bit-exact."""
+    import torch
+
+    rng = wl.SplitMix64(90)
+    batch = wl.decode_batch_from_contexts([40, 300, 16, 7], rng, extra_blocks=12)
+    desc, pool, host = _pool("qwen7b-bf16", batch.num_blocks, 91)
+    ip = batch.block_indptr.astype(np.uint32)
+    ids = batch.block_ids.astype(np.uint32)
+    ctx = batch.ctx_lens.copy()
+    side = torch.cuda.Stream()
+
+    def check(layer, stream=None):
+        kh, vh = pool.gather_host(layer, ip, ids, ctx, stream=stream)
+        if stream is not None:
+            stream.synchronize()
+        wk, wv = orc.gather(odesc(desc), host, layer, ip.astype(np.int32), ids.astype(np.int32), ctx)
+        assert np.array_equal(bits(to_host(kh)), bits(wk))
+        assert np.array_equal(bits(to_host(vh)), bits(wv))
+
+    check(0)
+    check(1)                                  # equal tables: gathered from the staged copy
+    free = np.setdiff1d(np.arange(desc.num_blocks), ids)
+    ids[:3] = free[:3]                        # changed in place: uploaded again
+    check(1)
+    ctx[1] -= 17                              # shorter context, same tables
+    check(0)
+    for i in range(9):                        # other host calls claim every staging slot
+        src, dst = np.array([free[5]], np.uint32), np.array([free[6 + i % 3]], np.uint32)
+        pool.copy_blocks(src, dst)
+        orc.copy_blocks(odesc(desc), host, src.astype(np.int32), dst.astype(np.int32))
+    check(1)                                  # equal values, slot reused: uploaded again
+    torch.cuda.synchronize()
+    check(0, stream=side)                     # another stream: uploaded on it
+    pool.check()
+    pool.close()
+
+
+def test_extend_host_reuses_equal_tables_and_follows_changed_ones():
+    """Every layer of a chunked-prefill step passes the same chunks and
+    tables: uploaded once, and re-uploaded when they change in place."""
+    L, Hq, Hkv, D, dt = SHAPES["qwen7b-bf16"]
+    rng = wl.SplitMix64(92)
+    ctx = np.array([70, 300, 33], np.int32)
+    ql = np.array([20, 64, 33], np.int32)
+    batch = wl.decode_batch_from_contexts(list(ctx - 1), rng, extra_blocks=8)
+    desc = PoolDesc(L, Hkv, Hq, D, batch.num_blocks, dt)
+    host = normal(93, desc.shape, dt)
+    q = normal(94, (int(ql.sum()), Hq, D), dt)
+    qip = np.zeros(ctx.size + 1, np.int32)
+    np.cumsum(ql, out=qip[1:])
+    ip = batch.block_indptr.astype(np.uint32)
+    ids = batch.block_ids.astype(np.uint32)
+    with DeviceKvPool(desc) as pool:
+        pool.write(host)
+        qd = to_device(q)
+
+        def check(layer):
+            got = to_host(pool.extend_attention_host(layer, qd, ql, ctx, ip, ids))
+            ref = orc.extend_attention(odesc(desc), host, layer, widen(q), qip, ip.astype(np.int32),
+                                       ids.astype(np.int32), ctx)
+            assert_attention_close(got, ref, dt)
+            return got
+
+        a = check(0)
+        b = check(0)                          # equal tables: launched from the staged copy
+        assert np.array_equal(bits(a), bits(b))
+        check(1)
+        free = np.setdiff1d(np.arange(desc.num_blocks), ids)
+        ids[-4:] = free[:4]                   # changed in place: uploaded again
+        check(1)
+        pool.check()
