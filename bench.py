@@ -9,7 +9,9 @@ slot, then run paged GQA decode attention over context + 1 tokens.
 Prints one JSON line: whole-step HBM throughput in algorithmic bytes (K/V
 read once, Q read, O written, appends read+written, block tables and slot
 ids), tokens/s, the attention kernel's roofline fraction measured with HIP
-events on its stream over the timed region, and the CPU baseline (the
+events that the library records on its stream right before and after that
+kernel (its split-K merge excluded; the whole layer's figure is nested
+beside it) over the timed region, and the CPU baseline (the
 oracle's reference-faithful restatement of the reference's CPU attention,
 timed on a bounded sample on this host).
 
@@ -171,15 +173,17 @@ def copy_calibration():
     print(json.dumps({"copy_bytes": n}), flush=True)
 
 
-def profiled_traffic(key: str):
+def profiled_traffic(key: str, field: str = "traffic_bytes_per_launch"):
     """HBM bytes per launch from the committed rocprofv3 PMC summary of a
     workload (profiles/<key>_hbm_traffic.md: FETCH_SIZE and WRITE_SIZE,
-    scaled by a 1 GiB copy kernel), or (None, None) when there is none."""
+    scaled by a 1 GiB copy kernel), or (None, None) when there is none.
+    field: traffic_bytes_per_launch (the timed launch group) or
+    traffic_bytes_per_kernel_launch (its dominant kernel alone)."""
     path = os.path.join(ROOT, "profiles", f"{key}_hbm_traffic.md")
     try:
         with open(path) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
+                if line.startswith(field + ":"):
                     return int(line.split(":", 1)[1]), os.path.relpath(path, ROOT)
     except OSError:
         pass
@@ -1066,8 +1070,10 @@ def decode_config(name: str, steps: int, warmup: int, mode: str = "step", pieces
 
     run_layer = pool.bind_decode_step(plan, k_new, v_new, q, None, None, out, kernel=kernel, stream=stream)
 
-    def step(events=None):
-        """events: None, or L+1 timing events recorded between layers."""
+    def step(events=None, kevents=None):
+        """events: None, or L+1 timing events recorded between layers;
+        kevents: None, or per layer a (start, end) pair that the library
+        records around the layer's attention kernel alone."""
         if mode != "split":
             # The engine's one call per step: host lengths and host page
             # tables (u32 CSR), validated, copied and uploaded with the plan.
@@ -1077,6 +1083,8 @@ def decode_config(name: str, steps: int, warmup: int, mode: str = "step", pieces
                 pool.append(layer, k_new[layer], v_new[layer], slots, stream=stream)
             if events is not None:
                 events[layer].record(stream)
+            if kevents is not None and kevents[layer] is not None:
+                pool.set_launch_events(*kevents[layer])
             if mode == "step":
                 run_layer(layer)
             elif mode == "planned":
@@ -1099,13 +1107,26 @@ def decode_config(name: str, steps: int, warmup: int, mode: str = "step", pieces
     # Launch timing: an event chain around every layer's launch on every
     # EVENT_EVERY-th timed step (events cost GPU time; sampling keeps the
     # timed steps close to unperturbed).
+    # The planned modes also time the attention kernel alone (the library
+    # records a pair of events around it, before its merge) on every fourth
+    # layer of the steps in between, a different quarter of the layers each
+    # time. (A pair on every layer of those steps, on top of the layer
+    # events, made the runtime stall the host for about 30 ms once per run.)
     EVENT_EVERY = 4
     timed = [s_ for s_ in range(steps) if s_ % EVENT_EVERY == 0 and launch_events]
     ev = {s_: [_event() for _ in range(L + 1)] for s_ in timed}
+    ktimed = [s_ for s_ in range(steps) if s_ % EVENT_EVERY == 2 and launch_events and mode != "split"]
+    kev = {s_: [(_event(), _event()) if layer % 4 == (s_ // EVENT_EVERY) % 4 else None for layer in range(L)]
+           for s_ in ktimed}
+    for pairs in kev.values():
+        for pair in pairs:
+            if pair is not None and not isinstance(pair[0], _HipEvent):  # torch creates its event at the first record
+                pair[0].record(stream)
+                pair[1].record(stream)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for s_ in range(steps):
-        step(ev.get(s_))
+        step(ev.get(s_), kev.get(s_))
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     pool.check()
@@ -1115,12 +1136,35 @@ def decode_config(name: str, steps: int, warmup: int, mode: str = "step", pieces
     attn_avg_s = float(np.mean(attn_ms)) / 1e3
     gbs = step_bytes / (elapsed / steps) / 1e9
     attn_gbs = launch_bytes / attn_avg_s / 1e9
+    # The dominant kernel alone: attention (with the fused append in step
+    # mode), its merge and the gather excluded.
+    kern_bytes = attn_bytes + (app_bytes if mode == "step" else 0)
+    kern_ms = [k[i][0].elapsed_time(k[i][1]) for k in kev.values() for i in range(L) if k[i] is not None]
+    kern_avg_s = float(np.mean(kern_ms)) / 1e3 if kern_ms else float("nan")
+    kern_gbs = kern_bytes / kern_avg_s / 1e9 if kern_ms else float("nan")
     traffic, traffic_src = profiled_traffic(f"decode_{mode}_{name}")
     kernel_name = {"step": "mkv_decode_step (append + attention + merge, per layer)",
                    "planned": "mkv_decode_attention_planned (attention + merge, per layer)",
                    "split": "mkv_decode_attention (attention + merge, per layer)"}[mode]
     if with_gather:
         kernel_name += " + mkv_gather_host"
+    layer = {"what": kernel_name, "bytes": launch_bytes, "avg_us": round(attn_avg_s * 1e6, 2),
+             "GB_s": round(attn_gbs, 2), "frac": round(attn_gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
+             "launches_timed": len(attn_ms) if ev else 0}
+    if kern_ms:
+        # The roofline of the dominant kernel: the attention kernel alone.
+        ktraffic, _ = profiled_traffic(f"decode_{mode}_{name}", "traffic_bytes_per_kernel_launch")
+        roof = {"bound": "hbm", "achieved": round(kern_gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(kern_gbs / PEAK_HBM_GBS, 4), "traffic": ktraffic, "traffic_source": traffic_src,
+                "kernel": "the decode attention kernel alone" + (" (with the fused append)" if mode == "step" else "")
+                          + ", timed by events the library records around it",
+                "bytes_per_launch": kern_bytes, "avg_launch_us": round(kern_avg_s * 1e6, 2),
+                "launches_timed": len(kern_ms), "layer": layer}
+    else:
+        roof = {"bound": "hbm", "achieved": round(attn_gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(attn_gbs / PEAK_HBM_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
+                "kernel": kernel_name, "bytes_per_launch": launch_bytes, "avg_launch_us": round(attn_avg_s * 1e6, 2),
+                "launches_timed": len(attn_ms) if ev else 0}
     result = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -1145,11 +1189,7 @@ def decode_config(name: str, steps: int, warmup: int, mode: str = "step", pieces
         "pct_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "tokens_per_s": round(B / (elapsed / steps), 1),
         "step_bytes": step_bytes,
-        "roofline": {"bound": "hbm", "achieved": round(attn_gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(attn_gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
-                     "traffic_source": traffic_src, "kernel": kernel_name,
-                     "bytes_per_launch": launch_bytes, "avg_launch_us": round(attn_avg_s * 1e6, 2),
-                     "launches_timed": len(attn_ms) if ev else 0},
+        "roofline": roof,
         "cpu_baseline": None,
     }
     plan.close()

@@ -141,6 +141,15 @@ MKV_API int mkv_pool_buffer(const mkv_pool *pool, void **out_dev_ptr, uint64_t *
  * Returns MKV_ERR_DEVICE_INDEX if any bit was set (bits in *out_bits). */
 MKV_API int mkv_pool_check(mkv_pool *pool, void *stream, uint32_t *out_bits);
 
+/* Measurement hook (no counterpart in the reference: it lets a caller time
+ * the decode step's dominant kernel alone with events). The next
+ * mkv_decode_step, mkv_decode_attention_planned or (its suffix kernel)
+ * mkv_decode_step_shared_prefix call on this pool records ev_start (a
+ * hipEvent_t) on its stream right before its attention kernel and ev_end
+ * right after it, before the split-K merge, then forgets both. NULL, NULL
+ * forgets them now. */
+MKV_API int mkv_pool_set_launch_events(mkv_pool *pool, void *ev_start, void *ev_end);
+
 /* ---- data-plane operations ----------------------------------------------- */
 
 /* Append num_tokens K/V rows into `layer`:

@@ -61,6 +61,7 @@ DEVICE_SIGNATURES = {
     "mkv_pool_get_desc": (c_int, [P, DESC_P]),
     "mkv_pool_buffer": (c_int, [P, ctypes.POINTER(P), ctypes.POINTER(u64)]),
     "mkv_pool_check": (c_int, [P, P, ctypes.POINTER(u32)]),
+    "mkv_pool_set_launch_events": (c_int, [P, P, P]),
     "mkv_append": (c_int, [P, i32, P, P, P, i32, P]),
     "mkv_append_all_layers": (c_int, [P, P, P, P, i32, P]),
     "mkv_gather": (c_int, [P, i32, P, P, P, i32, i32, P, P, i64, P]),

@@ -2469,6 +2469,10 @@ static int launch_planned(Pool *p, const Plan *pl, int32_t layer, const void *d_
   const int hcs = g.Hkv * a.nqc;
   const int wpw = std::min(4, hcs);
   const dim3 grid((unsigned)pl->P, (unsigned)((hcs + wpw - 1) / wpw)), block(64 * wpw);
+  // A caller's measurement events bracket the attention kernel alone (one shot).
+  hipEvent_t ev_start = p->ev_start, ev_end = p->ev_end;
+  p->ev_start = p->ev_end = nullptr;
+  if (ev_start) MKV_CHECK_HIP(hipEventRecord(ev_start, hs));
   if (use_mfma) {
     // Cooperative kernel: Q rows of one sequence (Hq * D * 2 bytes) must fit
     // the QL loads per lane its ring slots carry.
@@ -2520,6 +2524,7 @@ static int launch_planned(Pool *p, const Plan *pl, int32_t layer, const void *d_
     MKV_DISPATCH(attn_planned_kernel, grid, block, hs, a, pd);
     MKV_CHECK_LAUNCH("attn_planned_kernel");
   }
+  if (ev_end) MKV_CHECK_HIP(hipEventRecord(ev_end, hs));
   if (pl->n_merge && merge) {
     const int64_t mwgs = ((int64_t)pl->n_merge * g.Hq + 3) / 4;
     MKV_DISPATCH_MERGE(merge_planned_kernel, dim3((unsigned)mwgs), dim3(256), hs, a, pd);

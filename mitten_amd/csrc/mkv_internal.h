@@ -69,6 +69,9 @@ struct Pool {
   hipStream_t aux = nullptr;
   hipEvent_t aux_fork = nullptr, aux_join = nullptr;
   int beside = 0;
+  // Caller events recorded around the next decode attention kernel (one
+  // shot; mkv_pool_set_launch_events).
+  hipEvent_t ev_start = nullptr, ev_end = nullptr;
   MetaSlot meta[kMetaSlots];
   int meta_next = 0;
   // The last host arrays staged by the append, gather and extend entry

@@ -404,6 +404,15 @@ extern "C" int mkv_pool_check(mkv_pool *pool, void *stream, uint32_t *out_bits) 
   return MKV_OK;
 }
 
+extern "C" int mkv_pool_set_launch_events(mkv_pool *pool, void *ev_start, void *ev_end) {
+  if (!pool) return set_error(MKV_ERR_INVALID_ARGUMENT, "pool is NULL");
+  if (!ev_start != !ev_end) return set_error(MKV_ERR_INVALID_ARGUMENT, "give both events, or neither");
+  Pool *p = reinterpret_cast<Pool *>(pool);
+  p->ev_start = reinterpret_cast<hipEvent_t>(ev_start);
+  p->ev_end = reinterpret_cast<hipEvent_t>(ev_end);
+  return MKV_OK;
+}
+
 // ---- C ABI: data movement -----------------------------------------------------------
 
 static int check_layer(const Pool *p, int32_t layer) {

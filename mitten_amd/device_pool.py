@@ -263,6 +263,24 @@ class DeviceKvPool:
             raise DeviceIndexError(st, self._lib.mkv_last_error().decode(), bits.value)
         _raise(st)
 
+    def set_launch_events(self, start, end) -> None:
+        """Measurement: record `start` and `end` (HIP events: an object with a
+        `handle`, a torch.cuda.Event already recorded once, or a raw handle)
+        right before and after the attention kernel of the next decode call on
+        this pool, before its merge (mkv_pool_set_launch_events). None, None
+        forgets them."""
+
+        def raw(ev):
+            if ev is None:
+                return None
+            if hasattr(ev, "handle"):
+                return ev.handle
+            if hasattr(ev, "cuda_event"):
+                return ctypes.c_void_p(ev.cuda_event)
+            return ctypes.c_void_p(int(ev))
+
+        _raise(self._lib.mkv_pool_set_launch_events(self._h, raw(start), raw(end)))
+
     # -- operations -----------------------------------------------------------------------
     def append(self, layer: int, k, v, slot_mapping, stream=None) -> None:
         """slot_mapping: device int32 tensor, or host u32 slots (numpy/list:

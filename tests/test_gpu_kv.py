@@ -6,7 +6,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from mitten_amd import DeviceIndexError, DeviceKvPool, PoolDesc
+from mitten_amd import BackendError, DeviceIndexError, DeviceKvPool, PoolDesc
 from mitten_amd import device_pool as dp
 from mitten_amd import workloads as wl
 from oracle import oracle as orc
@@ -437,3 +437,38 @@ def test_bound_decode_step_matches_per_call():
             plan.close()
     assert np.array_equal(bits(results[0][0]), bits(results[1][0]))
     assert np.array_equal(bits(results[0][1]), bits(results[1][1]))
+
+
+@pytest.mark.parametrize("kernel", ["mfma", "valu"])
+def test_launch_events_bracket_the_next_attention_kernel_once(kernel):
+    """The measurement hook records its two events around the next decode
+    call's attention kernel only (one shot); the results are unchanged."""
+    import torch
+
+    desc = PoolDesc(1, 4, 28, 128, 40, "bf16") if kernel == "mfma" else PoolDesc(1, 2, 14, 64, 40, "f32")
+    dt = desc.dtype
+    host = normal(84, desc.shape, dt)
+    q = normal(85, (3, desc.num_q_heads, desc.head_dim), dt)
+    kn, vn = (normal(s, (3, desc.num_kv_heads, desc.head_dim), dt) for s in (86, 87))
+    ip, ids = _i32([0, 3, 5, 12]), _i32(np.arange(12) + 20)
+    with DeviceKvPool(desc) as pool:
+        pool.write(host)
+        plan = pool.plan([40, 20, 100])
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        b.record()  # torch creates its events at their first record
+        torch.cuda.synchronize()
+        pool.set_launch_events(a, b)
+        o1 = to_host(pool.decode_step(0, plan, to_device(kn), to_device(vn), to_device(q), ip, ids, kernel=kernel))
+        torch.cuda.synchronize()
+        first = a.elapsed_time(b)
+        assert first > 0.0
+        o2 = to_host(pool.decode_step(0, plan, to_device(kn), to_device(vn), to_device(q), ip, ids, kernel=kernel))
+        torch.cuda.synchronize()
+        assert a.elapsed_time(b) == first  # not recorded again
+        with pytest.raises(BackendError):
+            pool.set_launch_events(a, None)
+        pool.set_launch_events(None, None)
+        pool.check()
+        plan.close()
+    assert np.array_equal(bits(o1), bits(o2))
