@@ -1058,7 +1058,11 @@ def decode_config(name: str, steps: int, warmup: int, mode: str = "step", pieces
 
     attn_bytes = wl.algorithmic_bytes_attention(batch, Hq, Hkv, D, es)
     app_bytes = wl.algorithmic_bytes_append(B, Hkv, D, es)
-    gather_bytes = (4 * batch.total_tokens * Hkv * D * es + 4 * int(batch.block_ids.size)) if with_gather else 0
+    # The gather reads every row and writes it back contiguous; fused into the
+    # step (f32 step mode) it reads nothing the attention does not already.
+    fused_gather = with_gather and mode == "step"
+    gather_bytes = (0 if not with_gather else 2 * batch.total_tokens * Hkv * D * es if fused_gather
+                    else 4 * batch.total_tokens * Hkv * D * es + 4 * int(batch.block_ids.size))
     step_bytes = L * (attn_bytes + app_bytes + gather_bytes)
     # Bytes of the work the HIP events bracket per layer: the fused step moves
     # the append's bytes too, and the gather follows it in the same bracket.
@@ -1068,7 +1072,10 @@ def decode_config(name: str, steps: int, warmup: int, mode: str = "step", pieces
     ip_h, ids_h = batch.block_indptr.astype(np.uint32), batch.block_ids.astype(np.uint32)
     plan = pool.plan(ctx_host, pieces=pieces, stream=stream, block_indptr=ip_h, block_ids=ids_h)
 
-    run_layer = pool.bind_decode_step(plan, k_new, v_new, q, None, None, out, kernel=kernel, stream=stream)
+    # The f32 configuration's gather goes with each layer's step: the
+    # per-head kernel stores the rows as it reads them (mkv_decode_step_gather).
+    run_layer = pool.bind_decode_step(plan, k_new, v_new, q, None, None, out, kernel=kernel, stream=stream,
+                                      gather_out=(gk, gv) if fused_gather else None)
 
     def step(events=None, kevents=None):
         """events: None, or L+1 timing events recorded between layers;
@@ -1094,7 +1101,7 @@ def decode_config(name: str, steps: int, warmup: int, mode: str = "step", pieces
                 pool.decode_attention(layer, q[layer], indptr, ids, ctx, max_ctx, out=out[layer],
                                       split_tokens=split_tokens, workspace=ws, kernel=kernel,
                                       stream=stream)
-            if with_gather:
+            if with_gather and not fused_gather:
                 pool.gather_host(layer, ip_h, ids_h, ctx_host, out_k=gk, out_v=gv, stream=stream)
         if events is not None:
             events[L].record(stream)
@@ -1138,7 +1145,7 @@ def decode_config(name: str, steps: int, warmup: int, mode: str = "step", pieces
     attn_gbs = launch_bytes / attn_avg_s / 1e9
     # The dominant kernel alone: attention (with the fused append in step
     # mode), its merge and the gather excluded.
-    kern_bytes = attn_bytes + (app_bytes if mode == "step" else 0)
+    kern_bytes = attn_bytes + (app_bytes if mode == "step" else 0) + (gather_bytes if fused_gather else 0)
     kern_ms = [k[i][0].elapsed_time(k[i][1]) for k in kev.values() for i in range(L) if k[i] is not None]
     kern_avg_s = float(np.mean(kern_ms)) / 1e3 if kern_ms else float("nan")
     kern_gbs = kern_bytes / kern_avg_s / 1e9 if kern_ms else float("nan")
@@ -1146,7 +1153,9 @@ def decode_config(name: str, steps: int, warmup: int, mode: str = "step", pieces
     kernel_name = {"step": "mkv_decode_step (append + attention + merge, per layer)",
                    "planned": "mkv_decode_attention_planned (attention + merge, per layer)",
                    "split": "mkv_decode_attention (attention + merge, per layer)"}[mode]
-    if with_gather:
+    if fused_gather:
+        kernel_name = "mkv_decode_step_gather (append + attention + gather + merge, per layer)"
+    elif with_gather:
         kernel_name += " + mkv_gather_host"
     layer = {"what": kernel_name, "bytes": launch_bytes, "avg_us": round(attn_avg_s * 1e6, 2),
              "GB_s": round(attn_gbs, 2), "frac": round(attn_gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
@@ -1157,6 +1166,7 @@ def decode_config(name: str, steps: int, warmup: int, mode: str = "step", pieces
         roof = {"bound": "hbm", "achieved": round(kern_gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(kern_gbs / PEAK_HBM_GBS, 4), "traffic": ktraffic, "traffic_source": traffic_src,
                 "kernel": "the decode attention kernel alone" + (" (with the fused append)" if mode == "step" else "")
+                          + (" and gather" if fused_gather else "")
                           + ", timed by events the library records around it",
                 "bytes_per_launch": kern_bytes, "avg_launch_us": round(kern_avg_s * 1e6, 2),
                 "launches_timed": len(kern_ms), "layer": layer}

@@ -325,6 +325,20 @@ MKV_API int mkv_decode_step(mkv_pool *pool, const mkv_decode_plan *plan, int32_t
                             const void *d_k_new, const void *d_v_new, const void *d_q, void *d_o,
                             const int32_t *d_block_indptr, const int32_t *d_block_ids,
                             float scale, uint32_t flags, void *stream);
+/* mkv_decode_step that also writes the layer's block-table gather, the
+ * grown KVCacheState of model.rs:390-392 (the step's new row included):
+ * what mkv_gather writes for the plan's sequences and contexts, sequence b's
+ * [num_kv_heads][ctx_b][head_dim] at element offset (ctx_0 + ... +
+ * ctx_{b-1}) * num_kv_heads * head_dim of d_out_k / d_out_v (capacity
+ * out_capacity_tokens tokens, 16-byte aligned). On the per-head kernel (f32
+ * pools, and bf16 ones the MFMA kernels do not take) the attention kernel
+ * stores the rows as it reads them; after the MFMA kernels the gather
+ * kernel follows on the same stream. Not for suffix plans. */
+MKV_API int mkv_decode_step_gather(mkv_pool *pool, const mkv_decode_plan *plan, int32_t layer,
+                                   const void *d_k_new, const void *d_v_new, const void *d_q, void *d_o,
+                                   const int32_t *d_block_indptr, const int32_t *d_block_ids,
+                                   void *d_out_k, void *d_out_v, int64_t out_capacity_tokens,
+                                   float scale, uint32_t flags, void *stream);
 
 /* ---- decode over a shared prefix ------------------------------------------ */
 

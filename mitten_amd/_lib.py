@@ -75,6 +75,7 @@ DEVICE_SIGNATURES = {
     "mkv_decode_plan_info": (c_int, [P, I32P, I32P, I32P]),
     "mkv_decode_attention_planned": (c_int, [P, P, i32, P, P, P, P, f32, u32, P]),
     "mkv_decode_step": (c_int, [P, P, i32, P, P, P, P, P, P, f32, u32, P]),
+    "mkv_decode_step_gather": (c_int, [P, P, i32, P, P, P, P, P, P, P, P, i64, f32, u32, P]),
     "mkv_decode_plan_build_suffixes": (c_int, [P, I32P, i32, i32, P]),
     "mkv_decode_step_shared_prefix": (c_int, [P, P, i32, P, P, P, P, P, i32, P, P, f32, u32, P]),
     "mkv_extend_attention": (c_int, [P, i32, P, P, P, P, P, P, i32, i32, i32, f32, u32, P]),

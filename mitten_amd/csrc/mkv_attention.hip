@@ -81,6 +81,11 @@ struct KArgs {
   int32_t Hq, Hkv, G, nqc;
   float sl2;  // scale * log2(e)
   int32_t zero_sink;
+  // Fused block-table gather (the per-head kernel of the planned path):
+  // every row the attention reads is also stored at gather row
+  // gtok0[b] * Hkv + h * ctx_b + t of gk / gv ([Hkv][ctx][D] per sequence).
+  uint8_t *gk, *gv;
+  const int32_t *gtok0;
 };
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -126,6 +131,7 @@ struct Seg {
   const int32_t *table;  // ids + tab0
   const uint8_t *nk;     // fused append: new K row (this head) or nullptr
   const uint8_t *nv;
+  int64_t gtok = 0;      // fused gather: the sequence's first token in the outputs
 };
 
 // ===========================================================================
@@ -430,6 +436,11 @@ __device__ __forceinline__ void valu_segment(const KArgs &a, const Seg &sg, int 
     for (int u = 0; u < U; u++) {
       const int t = tb + u * TPI + lt;
       const bool valid = okb && t < t_end;
+      if (a.gk && sg.qc == 0 && valid) {  // fused gather: the row as read (the new row from its input)
+        const int64_t go = ((sg.gtok * a.Hkv + (int64_t)sg.h * sg.ctx + t) * D) * ES + ld * 16;
+        *reinterpret_cast<u32x4 *>(a.gk + go) = kd[u];
+        *reinterpret_cast<u32x4 *>(a.gv + go) = vd[u];
+      }
       float kf[VEC], vf[VEC];
       if constexpr (BF16) {
 #pragma unroll
@@ -737,6 +748,7 @@ struct PlanDev {
   const int32_t *seq_piece0;  // [B] first piece of each sequence
   const int32_t *seq_npiece;  // [B] pieces a sequence spans
   const int32_t *merge_seqs;  // [n_merge] sequences cut by a piece boundary
+  const int32_t *tok0;        // [B+1] first token of each sequence (sum of the earlier contexts)
   const int32_t *flat_seq;    // [total] sequence of each flattened block
   const int32_t *flat_meta;   // [total] kMetaValid | kMetaLast | kMetaSingle bits
   int32_t *flat_id;           // [total] block id (written per step from the tables)
@@ -949,6 +961,7 @@ __global__ void __launch_bounds__(256) attn_planned_kernel(KArgs a, PlanDev pd) 
       }
     }
     const bool single = pd.flat_meta[sb] & kMetaSingle;
+    if (a.gk) sg.gtok = a.gtok0[b];
     run_segment<D, BF16, MFMA>(a, sg, lane, single, (int64_t)(p + b) * a.Hq, 1);
   }
 }
@@ -1803,6 +1816,8 @@ static KArgs make_kargs(Pool *p, int32_t layer, const void *d_q, void *d_o, cons
   a.nqc = (a.G + qcw - 1) / qcw;
   a.sl2 = scale * kLog2e;
   a.zero_sink = (flags & MKV_ATTN_ZERO_SINK) ? 1 : 0;
+  a.gk = a.gv = nullptr;
+  a.gtok0 = nullptr;
   return a;
 }
 
@@ -1869,8 +1884,8 @@ struct Plan {
   int32_t B = 0, P = 0, BP = 0, total = 0, n_merge = 0;
   int32_t *d_meta = nullptr;  // ctx[B] | seq_blk0[B+1] | piece_f0[P+1] | piece_seq[P] |
                               // seq_piece0[B] | seq_npiece[B] | merge_seqs[n_merge] |
-                              // flat_seq[total] | flat_meta[total] | flat_id[total] |
-                              // prefix_ids[n_prefix]
+                              // tok0[B+1] | flat_seq[total] | flat_meta[total] |
+                              // flat_id[total] | prefix_ids[n_prefix]
   size_t meta_cap = 0;        // ints
   int32_t *h_meta = nullptr;  // pinned staging
   size_t h_cap = 0;
@@ -1884,6 +1899,8 @@ struct Plan {
   int32_t n_prefix = 0;       // shared-prefix ids given at build time (0: none)
   bool all_partial = false;   // every sequence stores partials (built for a shared prefix's suffixes)
   bool beside = false;        // suffix pieces sized to run beside the prefix tiles (one per CU)
+  int64_t tokens = 0;         // sum of the context lengths
+  int32_t max_ctx = 0;        // the longest context
 };
 
 static PlanDev plan_dev(const Plan *pl) {
@@ -1895,7 +1912,8 @@ static PlanDev plan_dev(const Plan *pl) {
   d.seq_piece0 = d.piece_seq + pl->P;
   d.seq_npiece = d.seq_piece0 + pl->B;
   d.merge_seqs = d.seq_npiece + pl->B;
-  d.flat_seq = d.merge_seqs + pl->n_merge;
+  d.tok0 = d.merge_seqs + pl->n_merge;
+  d.flat_seq = d.tok0 + pl->B + 1;
   d.flat_meta = d.flat_seq + pl->total;
   d.flat_id = pl->d_meta + pl->flat_off;
   d.B = pl->B;
@@ -2280,7 +2298,7 @@ static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t 
   DeviceGuard guard(pl->pool->device);
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
   const size_t n_ints = (size_t)num_seqs + (num_seqs + 1) + (P + 1) + P + 3 * (size_t)num_seqs +
-                        3 * (size_t)total + ht.n_prefix;
+                        (num_seqs + 1) + 3 * (size_t)total + ht.n_prefix;
   // Staging: wait for the previous upload to leave the pinned buffer.
   if (pl->pending) {
     MKV_CHECK_HIP(hipEventSynchronize(pl->uploaded));
@@ -2319,7 +2337,17 @@ static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t 
   int n_merge = 0;
   for (int32_t b = 0; b < num_seqs; b++)
     if (snpiece[b] > 1 || all_partial) mseq[n_merge++] = b;
-  int32_t *fseq = mseq + n_merge, *fmeta = fseq + total;
+  int32_t *tok0 = mseq + n_merge, *fseq = tok0 + num_seqs + 1, *fmeta = fseq + total;
+  // Gather rows: sequence b's tokens start after the earlier contexts
+  // (clamped where they pass 2^31 - 1: the fused gather then refuses the plan).
+  int64_t tokens = 0;
+  int32_t max_ctx = 0;
+  for (int32_t b = 0; b < num_seqs; b++) {
+    tok0[b] = (int32_t)std::min<int64_t>(tokens, INT32_MAX);
+    tokens += ctx[b];
+    max_ctx = std::max(max_ctx, ctx[b]);
+  }
+  tok0[num_seqs] = (int32_t)std::min<int64_t>(tokens, INT32_MAX);
   for (int32_t b = 0; b < num_seqs; b++) {
     const int nb = blk0[b + 1] - blk0[b];
     const int single = snpiece[b] == 1 && !all_partial ? kMetaSingle : 0;
@@ -2332,7 +2360,7 @@ static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t 
   // Block ids in piece order (flattened order: sequence b's first
   // ceil(ctx_b / 16) table entries at seq_blk0[b]), then the prefix ids.
   const size_t flat_off = (size_t)num_seqs + (num_seqs + 1) + (P + 1) + P + 2 * (size_t)num_seqs + n_merge +
-                          2 * (size_t)total;
+                          (num_seqs + 1) + 2 * (size_t)total;
   const bool tables = ht.indptr != nullptr;
   if (tables) {
     int32_t *fid = pl->h_meta + flat_off;
@@ -2379,6 +2407,8 @@ static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t 
   pl->n_merge = n_merge;
   pl->all_partial = all_partial;
   pl->beside = beside;
+  pl->tokens = tokens;
+  pl->max_ctx = max_ctx;
   return MKV_OK;
 }
 
@@ -2429,10 +2459,20 @@ extern "C" int mkv_decode_plan_info(const mkv_decode_plan *plan, int32_t *out_pi
 static int launch_planned(Pool *p, const Plan *pl, int32_t layer, const void *d_k_new, const void *d_v_new,
                           const void *d_q, void *d_o, const int32_t *d_block_indptr,
                           const int32_t *d_block_ids, float scale, uint32_t flags, void *stream,
-                          bool merge = true) {
+                          bool merge = true, void *d_gk = nullptr, void *d_gv = nullptr, int64_t gcap = 0) {
   const Geom &g = p->g;
   if (pl->pool != p) return set_error(MKV_ERR_INVALID_ARGUMENT, "plan belongs to another pool");
   if (pl->B < 1) return set_error(MKV_ERR_INVALID_ARGUMENT, "plan was never built");
+  const bool gather = d_gk || d_gv;
+  if (gather) {
+    if (!d_gk || !d_gv) return set_error(MKV_ERR_INVALID_ARGUMENT, "give both gather outputs");
+    if (!aligned16(d_gk) || !aligned16(d_gv))
+      return set_error(MKV_ERR_INVALID_ARGUMENT, "gather outputs must be 16-byte aligned");
+    if (pl->tokens > INT32_MAX) return set_error(MKV_ERR_INVALID_ARGUMENT, "more than 2^31 - 1 tokens to gather");
+    if (pl->tokens > gcap)
+      return set_error(MKV_ERR_INVALID_ARGUMENT, "gather outputs hold %lld tokens, the plan's contexts %lld",
+                       (long long)gcap, (long long)pl->tokens);
+  }
   bool use_mfma = false;
   int rc = check_common(p, layer, flags, scale, use_mfma);
   if (rc) return rc;
@@ -2466,6 +2506,14 @@ static int launch_planned(Pool *p, const Plan *pl, int32_t layer, const void *d_
   a.new_v = reinterpret_cast<const uint8_t *>(d_v_new);
   a.ws_ml = reinterpret_cast<float *>(pl->d_ws);
   a.ws_o = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(pl->d_ws) + pl->ws_ml_bytes);
+  // The per-head kernel stores the gather's rows as it reads them; after the
+  // MFMA kernels the gather kernel runs on the same stream.
+  const bool fused_gather = gather && !use_mfma;
+  if (fused_gather) {
+    a.gk = reinterpret_cast<uint8_t *>(d_gk);
+    a.gv = reinterpret_cast<uint8_t *>(d_gv);
+    a.gtok0 = pd.tok0;
+  }
   const int hcs = g.Hkv * a.nqc;
   const int wpw = std::min(4, hcs);
   const dim3 grid((unsigned)pl->P, (unsigned)((hcs + wpw - 1) / wpw)), block(64 * wpw);
@@ -2530,6 +2578,9 @@ static int launch_planned(Pool *p, const Plan *pl, int32_t layer, const void *d_
     MKV_DISPATCH_MERGE(merge_planned_kernel, dim3((unsigned)mwgs), dim3(256), hs, a, pd);
     MKV_CHECK_LAUNCH("merge_planned_kernel");
   }
+  if (gather && !fused_gather)
+    return mkv_gather(reinterpret_cast<mkv_pool *>(p), layer, d_block_indptr, d_block_ids, pd.tok0, pl->B,
+                      pl->max_ctx, d_gk, d_gv, gcap, stream);
   return MKV_OK;
 }
 
@@ -2550,6 +2601,21 @@ extern "C" int mkv_decode_step(mkv_pool *pool, const mkv_decode_plan *plan, int3
   if (!d_k_new || !d_v_new) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL new K/V rows");
   return launch_planned(reinterpret_cast<Pool *>(pool), reinterpret_cast<const Plan *>(plan), layer,
                         d_k_new, d_v_new, d_q, d_o, d_block_indptr, d_block_ids, scale, flags, stream);
+}
+
+extern "C" int mkv_decode_step_gather(mkv_pool *pool, const mkv_decode_plan *plan, int32_t layer,
+                                      const void *d_k_new, const void *d_v_new, const void *d_q, void *d_o,
+                                      const int32_t *d_block_indptr, const int32_t *d_block_ids, void *d_out_k,
+                                      void *d_out_v, int64_t out_capacity_tokens, float scale, uint32_t flags,
+                                      void *stream) {
+  if (!pool || !plan) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL pool or plan");
+  if (!d_k_new || !d_v_new) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL new K/V rows");
+  if (!d_out_k || !d_out_v) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL gather outputs");
+  if (reinterpret_cast<const Plan *>(plan)->all_partial)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "a suffix plan's contexts are not whole sequences");
+  return launch_planned(reinterpret_cast<Pool *>(pool), reinterpret_cast<const Plan *>(plan), layer, d_k_new,
+                        d_v_new, d_q, d_o, d_block_indptr, d_block_ids, scale, flags, stream, true, d_out_k,
+                        d_out_v, out_capacity_tokens);
 }
 
 static int launch_ext_tiles(Pool *p, KArgs &a, ExtArgs &e, int split_cap, hipStream_t hs, bool beside = false);

@@ -711,27 +711,47 @@ class DeviceKvPool:
 
     def decode_step(self, layer: int, plan, k_new, v_new, q, block_indptr, block_ids, out=None,
                     scale: float | None = None, zero_sink: bool = False, kernel: str | None = None,
-                    stream=None, cached_loads: bool = False):
+                    stream=None, cached_loads: bool = False, gather_out=None):
         """Append k_new/v_new ([B, Hkv, D]) at position ctx-1 of every sequence,
-        then attend over ctx tokens, in one launch (plus the split-K merge)."""
+        then attend over ctx tokens, in one launch (plus the split-K merge).
+        gather_out: (k, v) flat device tensors that also receive the layer's
+        block-table gather (mkv_decode_step_gather)."""
         d = self.desc
         out, scale, flags = self._planned_args(plan, q, block_indptr, block_ids, out, scale, zero_sink, kernel,
                                                cached_loads)
         B = plan.num_seqs
         self._check_tensor(k_new, (B, d.num_kv_heads, d.head_dim), "k_new")
         self._check_tensor(v_new, (B, d.num_kv_heads, d.head_dim), "v_new")
-        _raise(self._lib.mkv_decode_step(
-            self._h, plan._h, layer, _dptr(k_new), _dptr(v_new), _dptr(q), _dptr(out),
-            _tptr(block_indptr), _tptr(block_ids), scale, flags, _stream_handle(stream)))
+        if gather_out is None:
+            _raise(self._lib.mkv_decode_step(
+                self._h, plan._h, layer, _dptr(k_new), _dptr(v_new), _dptr(q), _dptr(out),
+                _tptr(block_indptr), _tptr(block_ids), scale, flags, _stream_handle(stream)))
+        else:
+            gk, gv, cap = self._gather_outputs(gather_out)
+            _raise(self._lib.mkv_decode_step_gather(
+                self._h, plan._h, layer, _dptr(k_new), _dptr(v_new), _dptr(q), _dptr(out),
+                _tptr(block_indptr), _tptr(block_ids), gk, gv, cap, scale, flags, _stream_handle(stream)))
         return out
+
+    def _gather_outputs(self, gather_out):
+        """(k, v) flat device tensors of the pool dtype -> (k ptr, v ptr, capacity in tokens)."""
+        d = self.desc
+        gk, gv = gather_out
+        self._check_tensor(gk, None, "gather k")
+        self._check_tensor(gv, None, "gather v")
+        cap = min(gk.numel(), gv.numel()) // (d.num_kv_heads * d.head_dim)
+        return _dptr(gk), _dptr(gv), cap
 
     def bind_decode_step(self, plan, k_new, v_new, q, block_indptr, block_ids, out,
                          scale: float | None = None, zero_sink: bool = False,
-                         kernel: str | None = None, stream=None, cached_loads: bool = False):
+                         kernel: str | None = None, stream=None, cached_loads: bool = False,
+                         gather_out=None):
         """Validates, once, the buffers of every layer of one decode step
         (k_new, v_new: [L, B, Hkv, D]; q, out: [L, B, Hq, D]) and returns
         `run(layer)`, which enqueues mkv_decode_step for that layer with no
-        per-call Python checks (the engine's per-layer hot loop)."""
+        per-call Python checks (the engine's per-layer hot loop).
+        gather_out: (k, v) flat device tensors that every layer's call also
+        writes its block-table gather into (mkv_decode_step_gather)."""
         d = self.desc
         L, B = d.num_layers, plan.num_seqs
         self._check_tensor(k_new, (L, B, d.num_kv_heads, d.head_dim), "k_new")
@@ -740,7 +760,8 @@ class DeviceKvPool:
         self._check_tensor(out, (L, B, d.num_q_heads, d.head_dim), "out")
         _, scale, flags = self._planned_args(plan, q[0], block_indptr, block_ids, out[0], scale, zero_sink,
                                              kernel, cached_loads)
-        fn = self._lib.mkv_decode_step
+        fn = self._lib.mkv_decode_step if gather_out is None else self._lib.mkv_decode_step_gather
+        gx = () if gather_out is None else self._gather_outputs(gather_out)
         h, ph = self._h, plan._h
         sh = _stream_handle(stream)
         kv_stride = B * d.num_kv_heads * d.head_dim * d.elem_bytes
@@ -748,9 +769,9 @@ class DeviceKvPool:
         kb, vb, qb, ob = k_new.data_ptr(), v_new.data_ptr(), q.data_ptr(), out.data_ptr()
         ip, ix = _tptr(block_indptr), _tptr(block_ids)
         args = [(h, ph, layer, ctypes.c_void_p(kb + layer * kv_stride), ctypes.c_void_p(vb + layer * kv_stride),
-                 ctypes.c_void_p(qb + layer * qo_stride), ctypes.c_void_p(ob + layer * qo_stride), ip, ix,
-                 scale, flags, sh) for layer in range(L)]
-        keep = (k_new, v_new, q, out, block_indptr, block_ids)
+                 ctypes.c_void_p(qb + layer * qo_stride), ctypes.c_void_p(ob + layer * qo_stride), ip, ix)
+                + gx + (scale, flags, sh) for layer in range(L)]
+        keep = (k_new, v_new, q, out, block_indptr, block_ids, gather_out)
 
         def run(layer: int) -> None:
             st = fn(*args[layer])

@@ -472,3 +472,66 @@ def test_launch_events_bracket_the_next_attention_kernel_once(kernel):
         pool.check()
         plan.close()
     assert np.array_equal(bits(o1), bits(o2))
+
+
+@pytest.mark.parametrize("pieces", [0, 1, 7, 300])
+@pytest.mark.parametrize("shape,kernel", [("qwen0.5b-f32", None), ("qwen7b-bf16", "valu"),
+                                          ("qwen7b-bf16", "mfma"), ("gemma2b-bf16", "mfma-per-head")])
+def test_decode_step_gather_equals_step_then_gather(shape, kernel, pieces):
+    """The step with its gather (stored by the per-head kernel as it reads
+    the rows, or the gather kernel after the MFMA kernels) is bit-identical
+    to mkv_decode_step followed by mkv_gather: output, pool and both gathered
+    caches, which equal the oracle's gather of the appended pool."""
+    import torch
+
+    L, Hq, Hkv, D, dt = SHAPES[shape]
+    ctx = [1, 2, 15, 16, 17, 33, 100, 257, 500, 64]
+    rng = wl.SplitMix64(63)
+    batch = wl.decode_batch_from_contexts([c - 1 for c in ctx], rng, extra_blocks=3)
+    desc = PoolDesc(L, Hkv, Hq, D, batch.num_blocks, dt)
+    layer = L - 1
+    B = len(ctx)
+    host = normal(64, desc.shape, dt)
+    q = normal(65, (B, Hq, D), dt)
+    kn, vn = normal(66, (B, Hkv, D), dt), normal(67, (B, Hkv, D), dt)
+    ntok = int(sum(ctx)) * Hkv * D
+    res = []
+    for with_gather in (True, False):
+        with DeviceKvPool(desc) as pool:
+            pool.write(host)
+            plan = pool.plan(batch.ctx_lens, pieces=pieces)
+            args = (_i32(batch.block_indptr), _i32(batch.block_ids))
+            if with_gather:
+                gk = torch.full((ntok + 8,), 7.0, dtype=pool.torch_dtype, device="cuda")
+                gv = torch.full_like(gk, 7.0)
+                o = pool.decode_step(layer, plan, to_device(kn), to_device(vn), to_device(q), *args, kernel=kernel,
+                                     gather_out=(gk, gv))
+                gk, gv = to_host(gk[:ntok]), to_host(gv[:ntok])
+            else:
+                o = pool.decode_step(layer, plan, to_device(kn), to_device(vn), to_device(q), *args, kernel=kernel)
+                gk, gv = (to_host(t) for t in pool.gather(layer, *args, _i32(batch.ctx_indptr), batch.max_ctx))
+            pool.check()
+            res.append((to_host(o), pool.read(), gk, gv))
+            plan.close()
+    (o1, p1, k1, v1), (o2, p2, k2, v2) = res
+    assert np.array_equal(bits(o1), bits(o2))
+    assert np.array_equal(bits(p1), bits(p2))
+    assert np.array_equal(bits(k1), bits(k2)) and np.array_equal(bits(v1), bits(v2))
+    want = host.copy()
+    assert orc.append(odesc(desc), want, layer, kn, vn, batch.slot_mapping) == -1
+    wk, wv = orc.gather(odesc(desc), want, layer, batch.block_indptr, batch.block_ids, batch.ctx_lens)
+    assert np.array_equal(bits(k1), bits(wk)) and np.array_equal(bits(v1), bits(wv))
+
+
+def test_decode_step_gather_rejects_small_outputs():
+    import torch
+
+    desc = PoolDesc(1, 2, 14, 64, 8, "f32")
+    with DeviceKvPool(desc) as pool:
+        plan = pool.plan([20, 30])
+        z = torch.zeros((2, 2, 64), dtype=torch.float32, device="cuda")
+        q = torch.zeros((2, 14, 64), dtype=torch.float32, device="cuda")
+        small = torch.zeros(49 * 2 * 64, dtype=torch.float32, device="cuda")  # 49 < 50 tokens
+        with pytest.raises(BackendError):
+            pool.decode_step(0, plan, z, z, q, _i32([0, 2, 4]), _i32([0, 1, 2, 3]), gather_out=(small, small))
+        plan.close()
