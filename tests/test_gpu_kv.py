@@ -474,14 +474,16 @@ def test_launch_events_bracket_the_next_attention_kernel_once(kernel):
     assert np.array_equal(bits(o1), bits(o2))
 
 
+@pytest.mark.parametrize("held", [False, True])
 @pytest.mark.parametrize("pieces", [0, 1, 7, 300])
 @pytest.mark.parametrize("shape,kernel", [("qwen0.5b-f32", None), ("qwen7b-bf16", "valu"),
                                           ("qwen7b-bf16", "mfma"), ("gemma2b-bf16", "mfma-per-head")])
-def test_decode_step_gather_equals_step_then_gather(shape, kernel, pieces):
+def test_decode_step_gather_equals_step_then_gather(shape, kernel, pieces, held):
     """The step with its gather (stored by the per-head kernel as it reads
     the rows, or the gather kernel after the MFMA kernels) is bit-identical
     to mkv_decode_step followed by mkv_gather: output, pool and both gathered
-    caches, which equal the oracle's gather of the appended pool."""
+    caches, which equal the oracle's gather of the appended pool. held: the
+    plan holds the host tables and the calls pass none."""
     import torch
 
     L, Hq, Hkv, D, dt = SHAPES[shape]
@@ -499,8 +501,14 @@ def test_decode_step_gather_equals_step_then_gather(shape, kernel, pieces):
     for with_gather in (True, False):
         with DeviceKvPool(desc) as pool:
             pool.write(host)
-            plan = pool.plan(batch.ctx_lens, pieces=pieces)
-            args = (_i32(batch.block_indptr), _i32(batch.block_ids))
+            dev_tables = (_i32(batch.block_indptr), _i32(batch.block_ids))
+            if held:
+                plan = pool.plan(batch.ctx_lens, pieces=pieces, block_indptr=batch.block_indptr.astype(np.uint32),
+                                 block_ids=batch.block_ids.astype(np.uint32))
+                args = (None, None)
+            else:
+                plan = pool.plan(batch.ctx_lens, pieces=pieces)
+                args = dev_tables
             if with_gather:
                 gk = torch.full((ntok + 8,), 7.0, dtype=pool.torch_dtype, device="cuda")
                 gv = torch.full_like(gk, 7.0)
@@ -509,7 +517,7 @@ def test_decode_step_gather_equals_step_then_gather(shape, kernel, pieces):
                 gk, gv = to_host(gk[:ntok]), to_host(gv[:ntok])
             else:
                 o = pool.decode_step(layer, plan, to_device(kn), to_device(vn), to_device(q), *args, kernel=kernel)
-                gk, gv = (to_host(t) for t in pool.gather(layer, *args, _i32(batch.ctx_indptr), batch.max_ctx))
+                gk, gv = (to_host(t) for t in pool.gather(layer, *dev_tables, _i32(batch.ctx_indptr), batch.max_ctx))
             pool.check()
             res.append((to_host(o), pool.read(), gk, gv))
             plan.close()
