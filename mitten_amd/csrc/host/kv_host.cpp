@@ -615,9 +615,10 @@ int mkvh_bm_append(mkvh_block_manager *bm, uint64_t seq, int32_t n_new, int32_t 
   if ((int64_t)m->pool.free_stack.size() < need)
     return fail(MKVH_ERR_EXHAUSTED, "append needs %lld blocks, %zu free", (long long)need, m->pool.free_stack.size());
   *out_n_cow = 0;
+  // The allocations below cannot fail: `need` free blocks were checked above.
   for (int64_t j : shared) {
-    uint32_t fresh;
-    m->pool.allocate(seq, &fresh);
+    uint32_t fresh = 0;
+    if (m->pool.allocate(seq, &fresh) != MKVH_OK) return MKVH_ERR_EXHAUSTED;
     const uint32_t old = s.blocks[j];
     bool freed = false;
     m->pool.release(old, &freed);
@@ -630,8 +631,8 @@ int mkvh_bm_append(mkvh_block_manager *bm, uint64_t seq, int32_t n_new, int32_t 
   }
   for (int64_t p = s.len; p < end; p++) {
     if (p / ps == (int64_t)s.blocks.size()) {
-      uint32_t b;
-      m->pool.allocate(seq, &b);
+      uint32_t b = 0;
+      if (m->pool.allocate(seq, &b) != MKVH_OK) return MKVH_ERR_EXHAUSTED;
       s.blocks.push_back(b);
     }
     out_slots[p - s.len] = (int32_t)(s.blocks[p / ps] * ps + p % ps);
