@@ -53,7 +53,7 @@ struct KvPool {
     for (int64_t i = n - 1; i >= 0; i--) free_stack.push_back((uint32_t)i);
   }
   bool valid(uint32_t p) const { return (int64_t)p < num_pages; }
-  int allocate(uint64_t who, uint32_t *out) {
+  [[nodiscard]] int allocate(uint64_t who, uint32_t *out) {
     if (free_stack.empty()) return fail(MKVH_ERR_EXHAUSTED, "KV pool exhausted (%lld pages)", (long long)num_pages);
     const uint32_t p = free_stack.back();
     free_stack.pop_back();
@@ -71,12 +71,12 @@ struct KvPool {
     free_stack.push_back(p);
     return MKVH_OK;
   }
-  int retain(uint32_t p) {
+  [[nodiscard]] int retain(uint32_t p) {
     if (!valid(p) || !in_use[p]) return fail(MKVH_ERR_NOT_IN_USE, "retain of page %u that is not in use", p);
     refcnt[p]++;
     return MKVH_OK;
   }
-  int release(uint32_t p, bool *freed) {
+  [[nodiscard]] int release(uint32_t p, bool *freed) {
     if (!valid(p) || !in_use[p]) return fail(MKVH_ERR_NOT_IN_USE, "release of page %u that is not in use", p);
     *freed = --refcnt[p] == 0;
     if (*freed) return free(p);
@@ -305,6 +305,27 @@ struct Seq {
   int64_t len = 0;
   std::vector<size_t> locked;
 };
+
+// Reference counts of blocks the manager's books say are in use. Every
+// block is processed; a failure (the books disagree with the pool) is
+// returned after the loop, with the pool's message.
+static int retain_all(KvPool &pool, const std::vector<uint32_t> &blocks) {
+  int rc = MKVH_OK;
+  for (uint32_t b : blocks) {
+    const int r = pool.retain(b);
+    if (r != MKVH_OK && rc == MKVH_OK) rc = r;
+  }
+  return rc;
+}
+static int release_all(KvPool &pool, const std::vector<uint32_t> &blocks) {
+  int rc = MKVH_OK;
+  for (uint32_t b : blocks) {
+    bool freed = false;
+    const int r = pool.release(b, &freed);
+    if (r != MKVH_OK && rc == MKVH_OK) rc = r;
+  }
+  return rc;
+}
 
 struct BlockMgr {
   KvPool pool;
@@ -553,16 +574,13 @@ int mkvh_bm_admit(mkvh_block_manager *bm, uint64_t seq, const uint32_t *tokens, 
   Seq s;
   size_t matched = 0;
   m->radix.match_prefix(tokens, (size_t)n_tokens, &matched, s.blocks, s.locked);
-  for (uint32_t b : s.blocks) m->pool.retain(b);
+  const int held = retain_all(m->pool, s.blocks);
   while ((int64_t)s.blocks.size() < need) {
     uint32_t b;
     if (m->pool.allocate(seq, &b) != MKVH_OK) {  // not reachable after the check above
       std::vector<uint64_t> ids(s.locked.begin(), s.locked.end());
       m->radix.unlock_nodes(ids.data(), ids.size());
-      for (uint32_t x : s.blocks) {
-        bool f = false;
-        m->pool.release(x, &f);
-      }
+      (void)release_all(m->pool, s.blocks);
       return MKVH_ERR_EXHAUSTED;
     }
     s.blocks.push_back(b);
@@ -570,7 +588,7 @@ int mkvh_bm_admit(mkvh_block_manager *bm, uint64_t seq, const uint32_t *tokens, 
   s.len = (int64_t)matched;
   m->seqs.emplace(seq, std::move(s));
   if (out_cached_len) *out_cached_len = (int64_t)matched;
-  return MKVH_OK;
+  return held;
 }
 
 int mkvh_bm_fork(mkvh_block_manager *bm, uint64_t parent, uint64_t child) {
@@ -580,10 +598,10 @@ int mkvh_bm_fork(mkvh_block_manager *bm, uint64_t parent, uint64_t child) {
   if (it == m->seqs.end()) return fail(MKVH_ERR_NOT_FOUND, "unknown sequence %llu", (unsigned long long)parent);
   if (m->seqs.count(child)) return fail(MKVH_ERR_INVALID_ARGUMENT, "sequence %llu exists", (unsigned long long)child);
   Seq c = it->second;
-  for (uint32_t b : c.blocks) m->pool.retain(b);
+  const int held = retain_all(m->pool, c.blocks);
   m->radix.lock_nodes(c.locked);
   m->seqs.emplace(child, std::move(c));
-  return MKVH_OK;
+  return held;
 }
 
 int mkvh_bm_append(mkvh_block_manager *bm, uint64_t seq, int32_t n_new, int32_t *out_slots, int32_t *out_cow_src,
@@ -621,7 +639,7 @@ int mkvh_bm_append(mkvh_block_manager *bm, uint64_t seq, int32_t n_new, int32_t 
     if (m->pool.allocate(seq, &fresh) != MKVH_OK) return MKVH_ERR_EXHAUSTED;
     const uint32_t old = s.blocks[j];
     bool freed = false;
-    m->pool.release(old, &freed);
+    if (m->pool.release(old, &freed) != MKVH_OK) return MKVH_ERR_NOT_IN_USE;
     s.blocks[j] = fresh;
     if (j * ps < s.len) {  // rows [j*ps, len) of this block are written: copy them
       out_cow_src[0] = (int32_t)old;
@@ -652,9 +670,9 @@ int mkvh_bm_promote(mkvh_block_manager *bm, uint64_t seq, const uint32_t *tokens
   if (!tokens) return fail(MKVH_ERR_INVALID_ARGUMENT, "NULL tokens");
   std::vector<uint32_t> evicted, adopted;
   m->radix.insert_prefix(tokens, s.blocks.data(), (size_t)full, evicted, adopted);
-  for (uint32_t p : adopted) m->pool.retain(p);
+  const int held = retain_all(m->pool, adopted);
   m->drop_tree_pages(evicted);
-  return MKVH_OK;
+  return held;
 }
 
 int mkvh_bm_release(mkvh_block_manager *bm, uint64_t seq) {
@@ -664,12 +682,9 @@ int mkvh_bm_release(mkvh_block_manager *bm, uint64_t seq) {
   if (it == m->seqs.end()) return fail(MKVH_ERR_NOT_FOUND, "unknown sequence %llu", (unsigned long long)seq);
   std::vector<uint64_t> ids(it->second.locked.begin(), it->second.locked.end());
   m->radix.unlock_nodes(ids.data(), ids.size());
-  for (uint32_t b : it->second.blocks) {
-    bool f = false;
-    m->pool.release(b, &f);
-  }
+  const int rc = release_all(m->pool, it->second.blocks);
   m->seqs.erase(it);
-  return MKVH_OK;
+  return rc;
 }
 
 int mkvh_bm_evict(mkvh_block_manager *bm, int64_t target_pages, int64_t *out_freed_blocks) {
