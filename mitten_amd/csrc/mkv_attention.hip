@@ -58,7 +58,9 @@ constexpr int kBlockWeight = 8;    // plan: weight of one block in a piece ...
 constexpr int kSwitchWeight = 12;  // ... and of a sequence start inside it (about 1.5 blocks)
 constexpr int kFirstRoundWeight = 116;  // plan: cap of the first-dispatched pieces, percent
 constexpr int kCoopRing = 3;   // register stages of the cooperative kernel (one less when
-                               // its slots carry four Q loads per lane)
+                               // its slots carry four Q loads per lane, or at head_dim 256,
+                               // where three stages spilled registers)
+constexpr int coop_ring(int D, int QL) { return D >= 256 || QL >= 4 ? kCoopRing - 1 : kCoopRing; }
 
 // Kernel-side geometry and per-call arguments shared by every variant.
 struct KArgs {
@@ -805,6 +807,7 @@ template <int D>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1)))
 attn_stream_kernel(KArgs a, PlanDev pd) {
   constexpr int NR = D / 32;
+  constexpr int RG = D >= 256 ? 2 : kRing;  // register stages (three spilled at head_dim 256)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hc = (int)blockIdx.y * (int)(blockDim.x >> 6) + wave;
@@ -834,7 +837,7 @@ attn_stream_kernel(KArgs a, PlanDev pd) {
   const int64_t head_off = (int64_t)h * D * 2;
   const int64_t k_lane = (int64_t)m16 * a.row_bytes + head_off + 16 * g4;
   const int64_t v_lane = (int64_t)(4 * g4 + rq) * a.row_bytes + head_off + 16 * a4;
-  u32x4 kb[kRing][NR], vb[kRing][NR];
+  u32x4 kb[RG][NR], vb[RG][NR];
   // Items k >= n (past the piece) load the first 128 bytes of a block picked
   // by the workgroup index instead: every iteration then issues the same loads
   // with no branch around them, so the compiler's static wait counts cover
@@ -867,7 +870,7 @@ attn_stream_kernel(KArgs a, PlanDev pd) {
   int nxt = next_start(0);
   if (nxt < n) mfma_load_q<D>(a, lane, seq_at(nxt), h, qc, qnext);
 #pragma unroll
-  for (int s = 0; s < kRing - 1; s++) issue(kb[s], vb[s], s);
+  for (int s = 0; s < RG - 1; s++) issue(kb[s], vb[s], s);
 
   MState<D> st;
   auto reset = [&]() {
@@ -889,7 +892,7 @@ attn_stream_kernel(KArgs a, PlanDev pd) {
   reset();
   int seg_first = 0;
   auto stage = [&](int s, int k) {
-    issue(kb[(s + kRing - 1) % kRing], vb[(s + kRing - 1) % kRing], k + kRing - 1);
+    issue(kb[(s + RG - 1) % RG], vb[(s + RG - 1) % RG], k + RG - 1);
     if (k > 0 && ((startmask >> k) & 1)) {  // a new sequence starts at item k
       finish(seg, seg_first);
       reset();
@@ -905,15 +908,15 @@ attn_stream_kernel(KArgs a, PlanDev pd) {
   };
   // No branch around any stage of the main loop (a path that skipped one
   // would make the compiler's wait counts drain the ring); the last
-  // n mod kRing items run after it.
-  const int nfull = n / kRing;
+  // n mod RG items run after it.
+  const int nfull = n / RG;
   int k0 = 0;
-  for (int it = 0; it < nfull; it++, k0 += kRing) {
+  for (int it = 0; it < nfull; it++, k0 += RG) {
 #pragma unroll
-    for (int s = 0; s < kRing; s++) stage(s, k0 + s);
+    for (int s = 0; s < RG; s++) stage(s, k0 + s);
   }
 #pragma unroll
-  for (int s = 0; s < kRing - 1; s++)
+  for (int s = 0; s < RG - 1; s++)
     if (k0 + s < n) stage(s, k0 + s);
   finish(seg, seg_first);
   if (a.new_k && qc == 0) store_new_rows<D>(a, lane, h, idv, seqv, metav, n, badv);
@@ -2142,9 +2145,9 @@ static int64_t coop_resident(Pool *p) {
   if (ql > 4) return 0;
   const void *fn = nullptr;
 #define MKV_COOP_FN(DD, WW)                                                                        \
-  fn = ql == 1   ? reinterpret_cast<const void *>(&attn_coop_kernel<DD, WW, 1, kCoopRing, true>)  \
-       : ql == 2 ? reinterpret_cast<const void *>(&attn_coop_kernel<DD, WW, 2, kCoopRing, true>)  \
-                 : reinterpret_cast<const void *>(&attn_coop_kernel<DD, WW, 4, kCoopRing - 1, true>)
+  fn = ql == 1   ? reinterpret_cast<const void *>(&attn_coop_kernel<DD, WW, 1, coop_ring(DD, 1), true>)  \
+       : ql == 2 ? reinterpret_cast<const void *>(&attn_coop_kernel<DD, WW, 2, coop_ring(DD, 2), true>)  \
+                 : reinterpret_cast<const void *>(&attn_coop_kernel<DD, WW, 4, coop_ring(DD, 4), true>)
 #define MKV_COOP_FN_W(DD)              \
   do {                                 \
     if (g.Hkv == 1) MKV_COOP_FN(DD, 1); \
@@ -2536,9 +2539,9 @@ static int launch_planned(Pool *p, const Plan *pl, int32_t layer, const void *d_
       const dim3 cgrid((unsigned)pl->P), cblock(64 * g.Hkv);
 #define MKV_COOP_NT(DD, WW, NT)                                                                          \
   do {                                                                                                   \
-    if (ql == 1) hipLaunchKernelGGL((attn_coop_kernel<DD, WW, 1, kCoopRing, NT>), cgrid, cblock, 0, hs, a, pd); \
-    else if (ql == 2) hipLaunchKernelGGL((attn_coop_kernel<DD, WW, 2, kCoopRing, NT>), cgrid, cblock, 0, hs, a, pd); \
-    else hipLaunchKernelGGL((attn_coop_kernel<DD, WW, 4, kCoopRing - 1, NT>), cgrid, cblock, 0, hs, a, pd);    \
+    if (ql == 1) hipLaunchKernelGGL((attn_coop_kernel<DD, WW, 1, coop_ring(DD, 1), NT>), cgrid, cblock, 0, hs, a, pd); \
+    else if (ql == 2) hipLaunchKernelGGL((attn_coop_kernel<DD, WW, 2, coop_ring(DD, 2), NT>), cgrid, cblock, 0, hs, a, pd); \
+    else hipLaunchKernelGGL((attn_coop_kernel<DD, WW, 4, coop_ring(DD, 4), NT>), cgrid, cblock, 0, hs, a, pd);    \
   } while (0)
 #define MKV_COOP_QL(DD, WW)                     \
   do {                                          \

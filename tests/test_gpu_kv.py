@@ -22,6 +22,8 @@ SHAPES = {
     "qwen0.5b-bf16": (2, 14, 2, 64, "bf16"),
     "llama8b-bf16": (1, 32, 8, 128, "bf16"),
     "g16-bf16": (1, 64, 4, 128, "bf16"),
+    "d256-g4-bf16": (1, 16, 4, 256, "bf16"),  # head_dim 256, 2 Q loads per lane in the cooperative kernel
+    "d256-g2-bf16": (1, 4, 2, 256, "bf16"),   # head_dim 256, 1 Q load per lane
 }
 
 
@@ -294,7 +296,8 @@ PLAN_CTX = [1, 2, 15, 16, 17, 33, 100, 129, 257, 500, 1000, 3, 64, 65, 700]
 # stream kernel otherwise (llama8b: Hkv = 8); "mfma-per-head" forces the latter.
 PLANNED_KERNELS = [("qwen0.5b-f32", None), ("qwen7b-bf16", "mfma"), ("qwen7b-bf16", "mfma-per-head"),
                    ("qwen7b-bf16", "valu"), ("gemma2b-bf16", "mfma"), ("gemma2b-bf16", "mfma-per-head"),
-                   ("qwen0.5b-bf16", "mfma"), ("llama8b-bf16", "mfma"), ("g16-bf16", "mfma")]
+                   ("qwen0.5b-bf16", "mfma"), ("llama8b-bf16", "mfma"), ("g16-bf16", "mfma"),
+                   ("d256-g4-bf16", "mfma"), ("d256-g2-bf16", "mfma"), ("d256-g4-bf16", "mfma-per-head")]
 
 
 @pytest.mark.parametrize("pieces", [0, 1, 7, 40, 300])
