@@ -936,7 +936,7 @@ def bench_pressure(steps, warmup, cpu=True):
     heads), 512 sequences with log-normal lengths (median 2,048, sigma 1,
     capped at 32,768) in blocks from a seeded permutation of the pool. Per
     step and layer, 8 sequences append a 512-token chunk (mkv_append_host:
-    the slots are host u32 values, uploaded per call) and the other 504 run
+    host u32 slots, the same for every layer, so uploaded once per step) and the other 504 run
     the fused append + decode attention from a plan holding the step's host
     tables; the chunks' prefill attention is left out, as the configuration
     states."""
@@ -1019,8 +1019,10 @@ def decode_config(name: str, steps: int, warmup: int, mode: str = "step", pieces
     plan holding the step's host page tables; planned: mkv_append +
     mkv_decode_attention_planned; split: mkv_append + mkv_decode_attention).
     The f32 Qwen2.5-0.5B configuration also gathers every layer's block
-    tables into contiguous per-sequence caches (mkv_gather_host), as its
-    step states. Returns (result dict, batch, step_bytes); the pool is freed."""
+    tables into contiguous per-sequence caches, as its step states: in step
+    mode inside the step (mkv_decode_step_gather), otherwise by
+    mkv_gather_host after it. Returns (result dict, batch, step_bytes); the
+    pool is freed."""
     import torch
 
     from mitten_amd import DeviceKvPool, PoolDesc
