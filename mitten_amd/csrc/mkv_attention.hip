@@ -1888,7 +1888,7 @@ struct Plan {
   int32_t *d_meta = nullptr;  // ctx[B] | seq_blk0[B+1] | piece_f0[P+1] | piece_seq[P] |
                               // seq_piece0[B] | seq_npiece[B] | merge_seqs[n_merge] |
                               // tok0[B+1] | flat_seq[total] | flat_meta[total] |
-                              // flat_id[total] | prefix_ids[n_prefix]
+                              // flat_id[total] | prefix_ids[n_prefix] | dev_flat_id[total]
   size_t meta_cap = 0;        // ints
   int32_t *h_meta = nullptr;  // pinned staging
   size_t h_cap = 0;
@@ -1898,6 +1898,7 @@ struct Plan {
   uint64_t ws_cap = 0;
   uint64_t ws_ml_bytes = 0;   // offset of the o rows inside d_ws
   size_t flat_off = 0;        // offset (ints) of flat_id inside d_meta
+  size_t dev_flat_off = 0;    // offset (ints) of the ids flattened from a call's device tables
   bool has_tables = false;    // flat_id holds the block ids given at build time
   int32_t n_prefix = 0;       // shared-prefix ids given at build time (0: none)
   bool all_partial = false;   // every sequence stores partials (built for a shared prefix's suffixes)
@@ -2374,8 +2375,12 @@ static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t 
     for (int32_t i = 0; i < ht.n_prefix; i++) fid[total + i] = (int32_t)ht.prefix[i];
   }
   const size_t used = flat_off + (tables ? (size_t)total + ht.n_prefix : 0);
-  if (pl->meta_cap < flat_off + total + ht.n_prefix) {
-    const size_t cap = grown(n_ints, pl->meta_cap);
+  // A call that brings device tables flattens their ids into a region of its
+  // own after the held ids, so the ids given at build time stay intact for
+  // later calls without tables.
+  const size_t dev_flat_off = flat_off + (size_t)total + ht.n_prefix;
+  if (pl->meta_cap < dev_flat_off + total) {
+    const size_t cap = grown(dev_flat_off + total, pl->meta_cap);
     MKV_CHECK_HIP(hipStreamSynchronize(hs));  // earlier launches may read the old buffer
     if (pl->d_meta) MKV_CHECK_HIP(hipFree(pl->d_meta));
     pl->d_meta = nullptr;
@@ -2398,6 +2403,7 @@ static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t 
   }
   pl->ws_ml_bytes = ml;
   pl->flat_off = flat_off;
+  pl->dev_flat_off = dev_flat_off;
   pl->has_tables = tables;
   pl->n_prefix = ht.n_prefix;
   MKV_CHECK_HIP(hipMemcpyAsync(pl->d_meta, pl->h_meta, used * 4, hipMemcpyHostToDevice, hs));
@@ -2490,11 +2496,13 @@ static int launch_planned(Pool *p, const Plan *pl, int32_t layer, const void *d_
     return set_error(MKV_ERR_INVALID_ARGUMENT, "q, o and new K/V rows must be 16-byte aligned");
   DeviceGuard guard(p->device);
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
-  const PlanDev pd = plan_dev(pl);
+  PlanDev pd = plan_dev(pl);
   if (dev_tables) {
     // Device tables are read on every call: the MFMA kernels' piece-order
     // ids are gathered from them here, so a table rewritten in place between
-    // calls is seen by the next call.
+    // calls is seen by the next call. They land in their own region, never
+    // over the ids the plan holds from its build.
+    pd.flat_id = pl->d_meta + pl->dev_flat_off;
     if (use_mfma) hipLaunchKernelGGL(flatten_ids_kernel, dim3((unsigned)((pl->total + 255) / 256)), dim3(256), 0, hs, pd,
                        d_block_indptr, d_block_ids, g.nblocks, p->d_err);
     MKV_CHECK_LAUNCH("flatten_ids_kernel");

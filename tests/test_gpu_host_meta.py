@@ -266,6 +266,44 @@ def test_device_tables_rewritten_in_place_are_followed(shape, kernel):
     assert np.max(np.abs(r1 - r2)) > 0.05  # the two tables really give different results
 
 
+@pytest.mark.parametrize("shape,kernel", [("qwen7b-bf16", "mfma"), ("qwen7b-bf16", "mfma-per-head"),
+                                          ("qwen0.5b-f32", None), ("gemma2b-bf16", "mfma")])
+def test_held_tables_survive_a_call_with_device_tables(shape, kernel):
+    """A plan holding its build-time tables, called first without tables, then
+    with device tables that point elsewhere, then without tables again: the
+    third call attends over the build-time tables, bit-identical to the
+    first, and the second over the device tables."""
+    L, Hq, Hkv, D, dt = SHAPES[shape]
+    rng = wl.SplitMix64(29)
+    ctx = [40, 300, 17, 129, 1000]
+    batch = wl.decode_batch_from_contexts([c - 1 for c in ctx], rng, extra_blocks=120)
+    desc = PoolDesc(L, Hkv, Hq, D, batch.num_blocks, dt)
+    B = batch.num_seqs
+    host = normal(35, desc.shape, dt)
+    q = normal(36, (B, Hq, D), dt)
+    used = set(batch.block_ids.tolist())
+    free = np.array([i for i in range(batch.num_blocks) if i not in used], np.int32)
+    ids2 = batch.block_ids.copy()
+    ids2[::2] = free[:ids2[::2].size]
+    with DeviceKvPool(desc) as pool:
+        pool.write(host)
+        plan = pool.plan(batch.ctx_lens, pieces=6, block_indptr=batch.block_indptr.astype(np.uint32),
+                         block_ids=batch.block_ids.astype(np.uint32))
+        qd = to_device(q)
+        o_held = to_host(pool.decode_attention_planned(0, plan, qd, None, None, kernel=kernel))
+        o_dev = to_host(pool.decode_attention_planned(0, plan, qd, _i32(batch.block_indptr), _i32(ids2),
+                                                      kernel=kernel))
+        o_again = to_host(pool.decode_attention_planned(0, plan, qd, None, None, kernel=kernel))
+        pool.check()
+        plan.close()
+    assert np.array_equal(bits(o_again), bits(o_held))
+    r1 = orc.decode_attention(odesc(desc), host, 0, widen(q), batch.block_indptr, batch.block_ids, batch.ctx_lens)
+    r2 = orc.decode_attention(odesc(desc), host, 0, widen(q), batch.block_indptr, ids2, batch.ctx_lens)
+    assert_attention_close(o_held, r1, dt)
+    assert_attention_close(o_dev, r2, dt)
+    assert np.max(np.abs(r1 - r2)) > 0.05  # the two tables really give different results
+
+
 @pytest.mark.parametrize("shape", ["qwen7b-bf16", "gemma2b-bf16"])
 def test_shared_prefix_plan_with_host_tables(shape):
     """plan_shared_prefix (prefix ids and suffix tables held by the plan)
@@ -365,6 +403,68 @@ def test_prep_host_equals_device_form():
             res.append((to_host(o), pool.read()))
     assert np.array_equal(bits(res[0][0]), bits(res[1][0]))
     assert np.array_equal(bits(res[0][1]), bits(res[1][1]))
+
+
+def test_prep_host_reuses_equal_metadata_and_follows_changed_ones():
+    """Every layer of a step passes the same positions and slots to the fused
+    prep: the library uploads them once. Positions changed in place, slots
+    changed in place and staging slots claimed by other host calls in
+    between all get a fresh upload. Every call's output and the pool after
+    all of them are bit-identical to the device-array form of the same
+    calls."""
+    import torch
+
+    L, Hq, Hkv, D, dt = 3, 28, 4, 128, "bf16"
+    n = 21
+    desc = PoolDesc(L, Hkv, Hq, D, 16, dt)
+    host = normal(90, desc.shape, dt)
+    rng = np.random.default_rng(91)
+    pos = rng.integers(0, 9000, n).astype(np.int32)
+    slots = rng.choice(12 * 16, n, replace=False).astype(np.uint32)
+    wq = torch.from_numpy(rng.standard_normal(D).astype(np.float32)).cuda()
+    wk = torch.from_numpy(rng.standard_normal(D).astype(np.float32)).cuda()
+    inv = torch.from_numpy(dp.rope_inv_freq(D, 1e6)).cuda()
+    calls = []  # (layer, seed, positions, slots) as each call saw them
+
+    def run(pool, hostform, layer, seed, p_, s_):
+        qg = normal(seed, (n, Hq, 2, D), dt)
+        k, v = normal(seed + 1, (n, Hkv, D), dt), normal(seed + 2, (n, Hkv, D), dt)
+        a, b = (p_, s_) if hostform else (_i32(p_), _i32(s_))
+        return to_host(pool.qk_norm_rope_append(layer, to_device(qg), to_device(k), to_device(v), a, b, wq, wk,
+                                                inv))
+
+    res = {}
+    for hostform in (True, False):
+        outs = []
+        with DeviceKvPool(desc) as pool:
+            pool.write(host)
+            if hostform:
+                p_, s_ = pos.copy(), slots.copy()
+                outs.append(run(pool, True, 0, 92, p_, s_))
+                calls.append((0, 92, p_.copy(), s_.copy()))
+                outs.append(run(pool, True, 1, 95, p_, s_))       # equal arrays: the staged copy
+                calls.append((1, 95, p_.copy(), s_.copy()))
+                p_ += 7                                           # positions changed in place
+                outs.append(run(pool, True, 2, 98, p_, s_))
+                calls.append((2, 98, p_.copy(), s_.copy()))
+                s_[:] = rng.choice(np.setdiff1d(np.arange(12 * 16, 16 * 16), s_), n, replace=False)
+                outs.append(run(pool, True, 0, 101, p_, s_))      # slots changed in place
+                calls.append((0, 101, p_.copy(), s_.copy()))
+                for i in range(9):                                # other host calls claim every staging slot
+                    pool.copy_blocks(np.array([15], np.uint32), np.array([14 - i % 2], np.uint32))
+                outs.append(run(pool, True, 1, 104, p_, s_))      # equal values, slot reused: uploaded again
+                calls.append((1, 104, p_.copy(), s_.copy()))
+            else:
+                for i, (layer, seed, p_, s_) in enumerate(calls):
+                    outs.append(run(pool, False, layer, seed, p_, s_))
+                    if i == 3:
+                        for j in range(9):
+                            pool.copy_blocks(_i32([15]), _i32([14 - j % 2]))
+            pool.check()
+            res[hostform] = (outs, pool.read())
+    for a, b in zip(res[True][0], res[False][0]):
+        assert np.array_equal(bits(a), bits(b))
+    assert np.array_equal(bits(res[True][1]), bits(res[False][1]))
 
 
 def test_wire_host_equals_device_form_and_rejects_repeated_destinations():
