@@ -74,10 +74,10 @@ struct Pool {
   hipEvent_t ev_start = nullptr, ev_end = nullptr;
   MetaSlot meta[kMetaSlots];
   int meta_next = 0;
-  // The last host arrays staged by the append, gather and extend entry
-  // points (an engine step passes the same ones to every layer), and a
+  // The last host arrays staged by the append, gather, extend and fused prep
+  // entry points (an engine step passes the same ones to every layer), and a
   // scratch array to assemble a staged array in.
-  StagedCache app_cache, gather_cache, extend_cache;
+  StagedCache app_cache, gather_cache, extend_cache, prep_cache;
   std::vector<int32_t> stage_tmp;
 };
 

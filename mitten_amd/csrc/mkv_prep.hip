@@ -469,11 +469,15 @@ extern "C" int mkv_qk_norm_rope_append_host(mkv_pool *pool, int32_t layer, const
     if (h_positions[t] < 0) return set_error(MKV_ERR_INVALID_ARGUMENT, "position[%d] = %d < 0", t, h_positions[t]);
   DeviceGuard guard(p->device);
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  // Every layer of a step passes the same positions and slots: staged once
+  // per step, so a step of many layers does not cycle the staging ring (and
+  // wait on the launch from a full ring earlier) at every layer.
+  std::vector<int32_t> &st = p->stage_tmp;
+  st.resize(2 * (size_t)num_tokens);
+  std::memcpy(st.data(), h_positions, (size_t)num_tokens * 4);
+  std::memcpy(st.data() + num_tokens, h_slot_mapping, (size_t)num_tokens * 4);
   MetaSlot *sl = nullptr;
-  if ((rc = meta_acquire(p, 2 * (size_t)num_tokens, hs, &sl))) return rc;
-  std::memcpy(sl->h, h_positions, (size_t)num_tokens * 4);
-  std::memcpy(sl->h + num_tokens, h_slot_mapping, (size_t)num_tokens * 4);
-  if ((rc = meta_upload(sl, 2 * (size_t)num_tokens, hs))) return rc;
+  if ((rc = stage_cached(p, p->prep_cache, st.data(), st.size(), hs, &sl))) return rc;
   rc = mkv_qk_norm_rope_append(pool, layer, d_q, d_k, d_v, d_q_norm_w, d_k_norm_w, d_inv_freq, rotary_dim, eps,
                                sl->d, sl->d + num_tokens, num_tokens, d_q_out, flags, stream);
   const int rr = meta_release(sl, hs);

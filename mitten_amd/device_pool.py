@@ -144,10 +144,17 @@ def _is_host(x) -> bool:
 
 
 def _host_u32(x, name: str) -> np.ndarray:
-    """Engine page ids / slots (u32). Negative values cannot be u32 ids."""
+    """Engine page ids / slots (u32). Values outside [0, 2^32) cannot be u32
+    ids; they are refused here rather than wrapped by the cast (2^32 + 5
+    would otherwise become id 5, a valid block of another sequence)."""
     a = np.asarray(x.numpy() if hasattr(x, "numpy") else x)
-    if a.size and a.dtype.kind == "i" and int(a.min()) < 0:
-        raise BackendError(MKV_ERR_INVALID_ARGUMENT, f"{name} holds a negative id")
+    if a.size:
+        if a.dtype.kind not in "iu":
+            raise BackendError(MKV_ERR_INVALID_ARGUMENT, f"{name} must hold integers, not {a.dtype}")
+        if a.dtype.kind == "i" and int(a.min()) < 0:
+            raise BackendError(MKV_ERR_INVALID_ARGUMENT, f"{name} holds a negative id")
+        if int(a.max()) > 0xFFFFFFFF:
+            raise BackendError(MKV_ERR_INVALID_ARGUMENT, f"{name} holds an id of 2^32 or more")
     return np.ascontiguousarray(a, np.uint32).reshape(-1)
 
 
