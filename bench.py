@@ -129,8 +129,8 @@ def parse():
                     help="headline only: skip the other configurations' nested lines")
     ap.add_argument("--no-launch-events", action="store_true",
                     help="time the steps without per-launch HIP events (roofline fields null)")
-    ap.add_argument("--cpu-layers", type=int, default=5,
-                    help="layers of the batch in the CPU baseline sample")
+    ap.add_argument("--cpu-seconds", type=float, default=8.0,
+                    help="about how long the CPU baseline's one-thread sample runs, per configuration")
     ap.add_argument("--op", choices=["decode", "prep", "wire", "gather", "copy", "append", "extend", "shared",
                                      "pressure"],
                     default="decode",
@@ -203,36 +203,73 @@ def cpu_info():
     return model
 
 
-def cpu_baseline(cfg, batch, step_bytes, layers, paged=True):
+def _prefix_count(ctx, tokens: float) -> int:
+    """Sequences taken from the front of the batch until their contexts hold
+    about `tokens` tokens (at least one, at most all)."""
+    c = np.cumsum(np.asarray(ctx, np.int64))
+    return int(min(len(c), max(1, np.searchsorted(c, tokens, side="right"))))
+
+
+def cpu_baseline(cfg, batch, step_bytes, budget_s: float = 8.0, paged=True):
     """Reference-faithful CPU decode (contiguous f32 cache grown by a copy per
-    token, repeat_kv materialised, mask, softmax, matmuls) for `layers` layers
-    of every sequence of the batch, scaled to a full step. The primary figure
-    is one thread, sequences one after another, as the reference executes
-    requests serially (inference-backend/src/burn_backend.rs:44-71); one layer
-    of the same sample threaded over sequences is reported beside it."""
+    token, repeat_kv materialised, mask, softmax, matmuls) on a bounded sample
+    of the step, scaled to a full step by its share of the step's tokens.
+
+    The sample: a short calibration run gives the cost per token; then either
+    every sequence for as many layer passes as about `budget_s` seconds allow,
+    or, when one layer of the whole batch would take longer, the sequences at
+    the front of the batch that fill about `budget_s` seconds of one layer.
+    The primary figure is one thread, sequences one after another, as the
+    reference executes requests serially
+    (inference-backend/src/burn_backend.rs:44-71); the same kind of sample
+    threaded over sequences on every host thread is reported beside it."""
     from oracle import oracle as orc
 
-    ctx = batch.ctx_lens
-    layers = max(1, min(layers, cfg["num_layers"]))
+    ctx = np.asarray(batch.ctx_lens, np.int64)
+    L, Hkv, Hq, D = cfg["num_layers"], cfg["num_kv_heads"], cfg["num_q_heads"], cfg["head_dim"]
+    total_tok = int(ctx.sum())
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    orc.set_num_threads(1)
-    t1 = sum(orc.ref_faithful_batch(ctx, cfg["num_kv_heads"], cfg["num_q_heads"], cfg["head_dim"],
-                                    seed=1 + layer) for layer in range(layers))
+
+    def run(nseq: int, passes: int, nthreads: int, seed: int) -> float:
+        orc.set_num_threads(nthreads)
+        return sum(orc.ref_faithful_batch(ctx[:nseq], Hkv, Hq, D, seed=seed + 7919 * i) for i in range(passes))
+
+    def sample(budget: float, nthreads: int, seed: int):
+        """(sequences, layer passes, seconds, tokens) of one bounded sample."""
+        ncal = _prefix_count(ctx, min(total_tok, 65536))
+        per_tok = run(ncal, 1, nthreads, seed) / float(ctx[:ncal].sum())
+        layer_s = per_tok * total_tok
+        if layer_s <= budget:
+            nseq, passes = len(ctx), int(max(1, min(4 * L, budget // max(layer_s, 1e-9))))
+        else:
+            nseq, passes = _prefix_count(ctx, budget / per_tok), 1
+        t = run(nseq, passes, nthreads, seed + 1)
+        return nseq, passes, t, int(ctx[:nseq].sum()) * passes
+
+    orc.set_setup_threads(threads)  # the caches' seeded fill is set-up, outside the timed region
+    n1, p1, t1, tok1 = sample(budget_s, 1, 1)
+    step_1t = t1 * (total_tok * L) / tok1
+    nn, pn, tn, tokn = sample(budget_s / 4, threads, 100)
+    step_nt = tn * (total_tok * L) / tokn
     orc.set_num_threads(threads)
-    tn = orc.ref_faithful_batch(ctx, cfg["num_kv_heads"], cfg["num_q_heads"], cfg["head_dim"], seed=100)
-    step_1t, step_nt = t1 / layers * cfg["num_layers"], tn * cfg["num_layers"]
+    orc.set_setup_threads(0)
+
+    def what(nseq, passes, nthreads, t):
+        seqs = f"all {len(ctx)} sequences" if nseq == len(ctx) else f"the first {nseq} of {len(ctx)} sequences"
+        return (f"{passes} layer pass{'es' if passes > 1 else ''} of {seqs} ({nthreads} thread"
+                f"{'s' if nthreads > 1 else ''}, {t:.1f} s), scaled by tokens to all {L} layers of the step")
+
     out = {
         "value": round(step_bytes / step_1t / 1e9, 3),
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
-        "sample": (f"{layers} of {cfg['num_layers']} layers x all {batch.num_seqs} sequences, 1 thread, "
-                   f"{t1:.1f} s; scaled to a full step"),
+        "sample": what(n1, p1, 1, t1),
         "tokens_per_s": round(batch.num_seqs / step_1t, 2),
         "ms_per_step": round(step_1t * 1e3, 1),
         "threaded": {"value": round(step_bytes / step_nt / 1e9, 3), "unit": "GB/s", "cores": threads,
-                     "tokens_per_s": round(batch.num_seqs / step_nt, 2),
-                     "sample": f"1 layer of the sample, {threads} threads over sequences, {tn:.1f} s"},
+                     "tokens_per_s": round(batch.num_seqs / step_nt, 2), "ms_per_step": round(step_nt * 1e3, 1),
+                     "sample": what(nn, pn, threads, tn)},
         "cpu_model": cpu_info(),
         "host_cpus": os.cpu_count(),
     }
@@ -242,17 +279,16 @@ def cpu_baseline(cfg, batch, step_bytes, layers, paged=True):
     # f32 pool, threaded over sequences and heads) on one layer of the same
     # batch, K/V from a seeded host pool of the same blocks; scaled to a step.
     es = 2 if cfg["dtype"] == "bf16" else 4
-    od = orc.desc(1, cfg["num_kv_heads"], cfg["head_dim"], batch.num_blocks, es)
+    od = orc.desc(1, Hkv, D, batch.num_blocks, es)
     raw = np.random.default_rng(7).standard_normal(orc.pool_bytes(od) // es, dtype=np.float32)
     host = orc.f32_to_bf16(raw) if es == 2 else raw
     del raw
-    q = np.random.default_rng(8).standard_normal((batch.num_seqs, cfg["num_q_heads"], cfg["head_dim"]),
-                                                 dtype=np.float32)
+    q = np.random.default_rng(8).standard_normal((batch.num_seqs, Hq, D), dtype=np.float32)
     c0 = time.perf_counter()
-    orc.decode_attention(od, host, 0, q, batch.block_indptr, batch.block_ids, ctx)
+    orc.decode_attention(od, host, 0, q, batch.block_indptr, batch.block_ids, batch.ctx_lens)
     tp = time.perf_counter() - c0
     del host
-    step_p = tp * cfg["num_layers"]
+    step_p = tp * L
     out["paged_oracle"] = {"value": round(step_bytes / step_p / 1e9, 3), "unit": "GB/s", "cores": threads,
                            "tokens_per_s": round(batch.num_seqs / step_p, 2),
                            "sample": f"oracle paged decode attention, 1 layer of all {batch.num_seqs} sequences, "
@@ -729,19 +765,30 @@ def _decode_step_run(pool, plan, batch, L, Hq, Hkv, D, seed, dev, stream, pre_la
     return step
 
 
-def _time_steps(step, steps, warmup, stream, L=None, every=4):
-    """Wall-clock seconds per step over `steps` steps after `warmup`, the
-    HIP-event average of one step on `stream`, and (with L) the average of
-    one layer's bracket from per-layer events on every `every`-th step."""
+def _time_steps(step, steps, warmup, stream, L=None, every=4, before_pass=None):
+    """Wall-clock seconds per step over `steps` steps after `warmup`, with no
+    event recorded inside them; then a second pass of `steps` steps with an
+    event pair around each step gives the HIP-event average of one step on
+    `stream`, and (with L) per-layer events on every `every`-th step of that
+    pass the average of one layer's bracket. before_pass(): called before
+    each pass (a workload that cycles through its steps' metadata restarts)."""
     import torch
 
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    if before_pass:
+        before_pass()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
     evs = [(_event(), _event()) for _ in range(steps)]
     lay = {i: [_event() for _ in range(L + 1)]
            for i in range(0, steps, every)} if L else {}
-    t0 = time.perf_counter()
+    if before_pass:
+        before_pass()
     for i, (a_, b_) in enumerate(evs):
         a_.record(stream)
         if L:
@@ -750,7 +797,6 @@ def _time_steps(step, steps, warmup, stream, L=None, every=4):
             step()
         b_.record(stream)
     torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) / steps
     ev = float(np.mean([a_.elapsed_time(b_) for a_, b_ in evs])) / 1e3
     if not L:
         return wall, ev
@@ -759,24 +805,37 @@ def _time_steps(step, steps, warmup, stream, L=None, every=4):
 
 
 def _time_copies(pool, src, dst, reps, stream):
-    """HIP-event average seconds of one copy_blocks launch of the host pairs
-    (mkv_copy_blocks_host: validated, uploaded, launched)."""
+    """HIP-event average seconds of one copy_blocks launch of the pairs:
+    (the kernel alone, from device int32 pair arrays (mkv_copy_blocks);
+    the engine's host call: u32 pairs validated, uploaded and launched
+    (mkv_copy_blocks_host), its upload inside the bracket)."""
     import torch
 
     s_, d_ = np.ascontiguousarray(src, np.uint32), np.ascontiguousarray(dst, np.uint32)
-    pool.copy_blocks(s_, d_, stream=stream)
-    torch.cuda.synchronize()
-    evs = [(_event(), _event()) for _ in range(reps)]
-    for a_, b_ in evs:
-        a_.record(stream)
-        pool.copy_blocks(s_, d_, stream=stream)
-        b_.record(stream)
-    torch.cuda.synchronize()
-    pool.check()
-    return float(np.mean([a_.elapsed_time(b_) for a_, b_ in evs])) / 1e3
+    sd = torch.from_numpy(s_.astype(np.int32)).to(stream.device)
+    dd = torch.from_numpy(d_.astype(np.int32)).to(stream.device)
+    out = []
+    for host in (False, True):
+        call = (lambda: pool.copy_blocks(s_, d_, stream=stream)) if host else \
+            (lambda: pool.copy_blocks(sd, dd, stream=stream))
+        # One call per slot of the library's host staging ring first: a slot is
+        # allocated (or grown) at its first use at a size, as in an engine's
+        # first steps, not in its steady state.
+        for _ in range(9 if host else 1):
+            call()
+        torch.cuda.synchronize()
+        evs = [(_event(), _event()) for _ in range(reps)]
+        for a_, b_ in evs:
+            a_.record(stream)
+            call()
+            b_.record(stream)
+        torch.cuda.synchronize()
+        pool.check()
+        out.append(float(np.mean([a_.elapsed_time(b_) for a_, b_ in evs])) / 1e3)
+    return out[0], out[1]
 
 
-def bench_shared(steps, warmup, cpu=True):
+def bench_shared(steps, warmup, cpu=True, compare_whole=True, cpu_seconds=8.0):
     """The radix-sharing configuration, driven by the host block manager
     (wl.RadixSharingScenario) at Qwen2.5-7B shapes, all 28 layers: 256
     sequences share a 4,100-token prefix (255 copy-on-write copies of its
@@ -815,7 +874,7 @@ def bench_shared(steps, warmup, cpu=True):
         del view
         sc.prefill_prefix()
         cow_src, cow_dst, _ = sc.fork_and_suffixes()
-        cow_s = _time_copies(pool, cow_src, cow_dst, 10, stream)
+        cow_s, cow_host_s = _time_copies(pool, cow_src, cow_dst, 10, stream)
         # The 32 decode steps' metadata, from the block manager.
         metas = []
         for _ in range(sc.decode_steps):
@@ -851,8 +910,8 @@ def bench_shared(steps, warmup, cpu=True):
         for _ in range(warmup):  # the first step's metadata, rewritten by the timed first step
             cursor[0] = 0
             step()
-        cursor[0] = 0
-        wall, ev_step, layer_s = _time_steps(step, len(metas), 0, stream, L=L)
+        wall, ev_step, layer_s = _time_steps(step, len(metas), 0, stream, L=L,
+                                             before_pass=lambda: cursor.__setitem__(0, 0))
         pool.check()
         info = splan.info()
         splan.close()
@@ -863,7 +922,7 @@ def bench_shared(steps, warmup, cpu=True):
         logical = float(np.mean([L * (int(m["ctx"].sum()) * row + qo_meta + 4 * int(m["ids"].size) + app)
                                  for m in metas]))
         compare = None
-        if cpu:  # the same last step through mkv_decode_step over the whole tables
+        if compare_whole:  # the same last step through mkv_decode_step over the whole tables
             last = metas[-1]
             plan = pool.plan(last["ctx"], stream=stream, block_indptr=last["ip"].astype(np.uint32),
                              block_ids=last["ids"].astype(np.uint32))
@@ -881,7 +940,7 @@ def bench_shared(steps, warmup, cpu=True):
         # and the compaction's moves pack the pool.
         done, freed, live_before = sc.finish_and_evict()
         mv_src, mv_dst = sc.compaction()
-        mv_s = _time_copies(pool, mv_src, mv_dst, 10, stream)
+        mv_s, mv_host_s = _time_copies(pool, mv_src, mv_dst, 10, stream)
         bm.check_invariants()
     layer_unique = unique / L
     result = {
@@ -911,26 +970,32 @@ def bench_shared(steps, warmup, cpu=True):
         "entry": "mkv_decode_step_shared_prefix (prefix once on MFMA tiles, suffix plan, merge)",
         "cow_copies": {"pairs": int(cow_src.size), "bytes": int(cow_src.size) * per_pair,
                        "avg_launch_us": round(cow_s * 1e6, 2),
-                       "gbs": round(cow_src.size * per_pair / cow_s / 1e9, 2)},
+                       "gbs": round(cow_src.size * per_pair / cow_s / 1e9, 2),
+                       "host_call_us": round(cow_host_s * 1e6, 2),
+                       "timing": "avg_launch_us: the kernel from device pair arrays; host_call_us: "
+                                 "mkv_copy_blocks_host (u32 pairs checked, uploaded, launched)"},
         "compaction_moves": {"pairs": int(mv_src.size), "bytes": int(mv_src.size) * per_pair,
                              "finished_sequences": len(done), "blocks_freed_by_eviction": int(freed),
                              "live_blocks_before": int(live_before),
                              "avg_launch_us": round(mv_s * 1e6, 2),
-                             "gbs": round(mv_src.size * per_pair / mv_s / 1e9, 2)},
+                             "gbs": round(mv_src.size * per_pair / mv_s / 1e9, 2),
+                             "host_call_us": round(mv_host_s * 1e6, 2)},
         "cpu_baseline": None,
+        "timing": ("value and ms_per_step: the 32 steps, no event recorded inside them; roofline: a second "
+                   "pass of the 32 steps with per-layer events on every fourth"),
     }
     if compare:
         result.update(compare)
     if cpu:
         last = metas[-1]
         lb = wl.DecodeBatch(last["ctx"], last["ip"], last["ids"], np.zeros(B, np.int32), sc.num_blocks)
-        result["cpu_baseline"] = cpu_baseline(cfg, lb, logical, 1)
+        result["cpu_baseline"] = cpu_baseline(cfg, lb, logical, cpu_seconds)
         result["cpu_baseline"]["bytes"] = "logical (each sequence's whole context)"
     torch.cuda.empty_cache()
     return result
 
 
-def bench_pressure(steps, warmup, cpu=True):
+def bench_pressure(steps, warmup, cpu=True, cpu_seconds=8.0):
     """One step of a pool under pressure (the pool-pressure configuration):
     the 217,982-block pool of a 200 GB budget (all 28 layers, Qwen2.5-7B
     heads), 512 sequences with log-normal lengths (median 2,048, sigma 1,
@@ -995,7 +1060,10 @@ def bench_pressure(steps, warmup, cpu=True):
                    "tokens_attended": batch.total_tokens, "chunk_tokens": n_chunk, "plan": info,
                    "metadata": "host u32 chunk slots per append; host page tables held by the step's plan"},
         "pct_peak": round(100.0 * step_bytes / wall / 1e9 / PEAK_HBM_GBS, 2),
-        "step_bytes": step_bytes, "tokens_per_s": round((batch.num_seqs + n_chunk) / wall, 1),
+        "step_bytes": step_bytes, "tokens_per_s": round(batch.num_seqs / wall, 1),
+        "tokens_per_s_what": "decode tokens/s: the step's decoding sequences / step time (the chunks' tokens "
+                             "are appended, not decoded)",
+        "chunk_tokens_per_s": round(n_chunk / wall, 1),
         "step_us_hip_events": round(ev * 1e6, 1),
         "roofline": {"bound": "hbm", "achieved": round(step_bytes / L / layer_s / 1e9, 2), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(step_bytes / L / layer_s / 1e9 / PEAK_HBM_GBS, 4),
@@ -1004,9 +1072,11 @@ def bench_pressure(steps, warmup, cpu=True):
                      "kernel": "mkv_append_host (chunks) + mkv_decode_step (per layer)",
                      "bytes_per_launch": step_bytes // L, "avg_launch_us": round(layer_s * 1e6, 2)},
         "cpu_baseline": None,
+        "timing": ("value and ms_per_step: the K timed steps, no event recorded inside them; roofline: a "
+                   "second pass of K steps with per-layer events on every fourth"),
     }
     if cpu:
-        result["cpu_baseline"] = cpu_baseline(cfg, batch, step_bytes, 1, paged=False)
+        result["cpu_baseline"] = cpu_baseline(cfg, batch, step_bytes, cpu_seconds, paged=False)
     torch.cuda.empty_cache()
     return result
 
@@ -1113,9 +1183,9 @@ def decode_config(name: str, steps: int, warmup: int, mode: str = "step", pieces
     torch.cuda.synchronize()
     pool.check()
 
-    # Launch timing: an event chain around every layer's launch on every
-    # EVENT_EVERY-th timed step (events cost GPU time; sampling keeps the
-    # timed steps close to unperturbed).
+    # Launch timing, in a pass after the timed steps: an event chain around
+    # every layer's launch on every EVENT_EVERY-th step of that pass (events
+    # cost GPU time; sampling keeps those steps close to unperturbed).
     # The planned modes also time the attention kernel alone (the library
     # records a pair of events around it, before its merge) on every fourth
     # layer of the steps in between, a different quarter of the layers each
@@ -1133,13 +1203,21 @@ def decode_config(name: str, steps: int, warmup: int, mode: str = "step", pieces
                 pair[0].record(stream)
                 pair[1].record(stream)
     torch.cuda.synchronize()
+    # The timed steps record no event: `value` comes from unperturbed steps.
     t0 = time.perf_counter()
     for s_ in range(steps):
-        step(ev.get(s_), kev.get(s_))
+        step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     pool.check()
     elapsed = t1 - t0
+    # A second pass of as many steps carries the sampled events that time
+    # the layers and the attention kernel (the roofline's figures).
+    if ev or kev:
+        for s_ in range(steps):
+            step(ev.get(s_), kev.get(s_))
+        torch.cuda.synchronize()
+        pool.check()
     ms_step = elapsed / steps * 1e3
     attn_ms = [e[i].elapsed_time(e[i + 1]) for e in ev.values() for i in range(L)] or [float("nan")]
     attn_avg_s = float(np.mean(attn_ms)) / 1e3
@@ -1203,6 +1281,8 @@ def decode_config(name: str, steps: int, warmup: int, mode: str = "step", pieces
         "step_bytes": step_bytes,
         "roofline": roof,
         "cpu_baseline": None,
+        "timing": ("value and ms_per_step: the K timed steps, no event recorded inside them; roofline: a "
+                   "second pass of K steps with sampled launch events"),
     }
     plan.close()
     pool.close()
@@ -1213,9 +1293,10 @@ def decode_config(name: str, steps: int, warmup: int, mode: str = "step", pieces
 
 def _nested(r: dict) -> dict:
     """The fields of a configuration's result kept in the headline line."""
-    keep = ("metric", "value", "unit", "ms_per_step", "pct_peak", "tokens_per_s", "steps", "warmup", "dtype",
-            "config", "roofline", "effective_gbs_logical", "step_bytes", "unique_bytes_per_step",
-            "logical_bytes_per_step", "cow_copies", "compaction_moves")
+    keep = ("metric", "value", "unit", "ms_per_step", "pct_peak", "tokens_per_s", "tokens_per_s_what",
+            "chunk_tokens_per_s", "steps", "warmup", "dtype", "config", "roofline", "effective_gbs_logical",
+            "step_bytes", "unique_bytes_per_step", "logical_bytes_per_step", "cow_copies", "compaction_moves",
+            "cpu_baseline", "timing")
     return {k: r[k] for k in keep if k in r}
 
 
@@ -1241,10 +1322,12 @@ def main():
         bench_extend(args)
         return
     if args.op == "shared":
-        print(json.dumps(bench_shared(args.steps, args.warmup, cpu=not args.no_cpu_baseline)), flush=True)
+        print(json.dumps(bench_shared(args.steps, args.warmup, cpu=not args.no_cpu_baseline,
+                                      cpu_seconds=args.cpu_seconds)), flush=True)
         return
     if args.op == "pressure":
-        print(json.dumps(bench_pressure(args.steps, args.warmup, cpu=not args.no_cpu_baseline)), flush=True)
+        print(json.dumps(bench_pressure(args.steps, args.warmup, cpu=not args.no_cpu_baseline,
+                                        cpu_seconds=args.cpu_seconds)), flush=True)
         return
     from mitten_amd import workloads as wl
 
@@ -1252,17 +1335,22 @@ def main():
     result, batch, step_bytes = decode_config(args.config, args.steps, args.warmup, args.mode, args.pieces, kernel,
                                               args.split_tokens, not args.no_launch_events)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(wl.CONFIGS[args.config], batch, step_bytes, args.cpu_layers)
+        result["cpu_baseline"] = cpu_baseline(wl.CONFIGS[args.config], batch, step_bytes, args.cpu_seconds)
     if args.configs and args.config == "qwen2.5-7b" and args.mode == "step":
         # The other configurations of the measurement table, each on its own
         # pool at its full size, with fewer steps (their own lines come from
         # --config / --op).
         ks, kw = max(4, min(args.steps, 12)), max(1, min(args.warmup, 2))
+        cpu = not args.no_cpu_baseline
         nested = {}
         for name in ("qwen2.5-0.5b", "gemma-2b-mqa"):
-            nested[name] = _nested(decode_config(name, ks, kw)[0])
-        nested["radix-shared-prefix"] = _nested(bench_shared(ks, kw, cpu=False))
-        nested["pool-pressure"] = _nested(bench_pressure(ks, kw, cpu=False))
+            r, b, sb = decode_config(name, ks, kw)
+            if cpu:
+                r["cpu_baseline"] = cpu_baseline(wl.CONFIGS[name], b, sb, args.cpu_seconds, paged=False)
+            nested[name] = _nested(r)
+        nested["radix-shared-prefix"] = _nested(bench_shared(ks, kw, cpu=cpu, compare_whole=False,
+                                                             cpu_seconds=args.cpu_seconds))
+        nested["pool-pressure"] = _nested(bench_pressure(ks, kw, cpu=cpu, cpu_seconds=args.cpu_seconds))
         result["configs"] = nested
     print(json.dumps(result), flush=True)
 

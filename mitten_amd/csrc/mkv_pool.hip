@@ -229,8 +229,13 @@ int meta_acquire(Pool *p, size_t n, hipStream_t hs, MetaSlot **out) {
   }
   sl->gen++;
   n = std::max<size_t>(n, 1);
-  if (sl->cap < n) {  // grows by half again at least: a batch's tables grow step by step
-    const size_t cap = std::max<size_t>({n, 4096, sl->cap + sl->cap / 2});
+  // A slot starts at 64k values (256 KiB pinned, as much on the device): an
+  // engine step's slots, copy pairs and tables of a few thousand sequences fit
+  // from the first use. It grows by half again at least, since a batch's
+  // tables grow step by step, and each growth frees the old buffers, which
+  // synchronises the device.
+  if (sl->cap < n) {
+    const size_t cap = std::max<size_t>({n, (size_t)1 << 16, sl->cap + sl->cap / 2});
     if (sl->h) MKV_CHECK_HIP(hipHostFree(sl->h));
     if (sl->d) MKV_CHECK_HIP(hipFree(sl->d));
     sl->h = nullptr;

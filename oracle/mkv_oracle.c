@@ -526,6 +526,13 @@ ORC_API void orc_set_num_threads(int n) {
 #endif
 }
 
+/* Threads that fill orc_ref_faithful_batch's caches before its timed region
+ * (0: the current thread count). A one-thread timing of a large sample need
+ * not fill gigabytes of seeded values on one thread. */
+static int g_setup_threads = 0;
+
+ORC_API void orc_set_setup_threads(int n) { g_setup_threads = n > 0 ? n : 0; }
+
 /* Timed CPU baseline over a batch: for every sequence b (in parallel over
  * sequences with OpenMP), one decode step of one layer executed as
  * orc_ref_faithful_decode does, starting from a contiguous cache of
@@ -538,7 +545,10 @@ ORC_API double orc_ref_faithful_batch(const int32_t *ctx, int32_t num_seqs, int3
   float **vc = (float **)calloc(num_seqs, sizeof(float *));
   float **qn = (float **)calloc(num_seqs, sizeof(float *));
   float **on = (float **)calloc(num_seqs, sizeof(float *));
-#pragma omp parallel for schedule(dynamic)
+#ifdef _OPENMP
+  const int setup_threads = g_setup_threads > 0 ? g_setup_threads : omp_get_max_threads();
+#endif
+#pragma omp parallel for schedule(dynamic) num_threads(setup_threads)
   for (int b = 0; b < num_seqs; b++) {
     const int64_t T = ctx[b] - 1;
     kc[b] = (float *)malloc(sizeof(float) * Hkv * (T > 0 ? T : 1) * D);

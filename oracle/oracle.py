@@ -71,6 +71,7 @@ def lib():
             "orc_ref_faithful_decode_copy": (ctypes.c_int, [P, P, i64, i32, i32, i32, P, P, P, f32, P]),
             "orc_num_threads": (ctypes.c_int, []),
             "orc_set_num_threads": (None, [ctypes.c_int]),
+            "orc_set_setup_threads": (None, [ctypes.c_int]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -332,3 +333,9 @@ def num_threads() -> int:
 
 def set_num_threads(n: int) -> None:
     lib().orc_set_num_threads(n)
+
+
+def set_setup_threads(n: int) -> None:
+    """Threads that fill ref_faithful_batch's caches before its timed region
+    (0: the current thread count)."""
+    lib().orc_set_setup_threads(n)
