@@ -55,6 +55,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
+PREFILL_BUDGET = 4096  # prefill tokens per step of the pool-pressure configuration (max_prefill_tokens_per_iter)
 METRIC = "paged KV append+decode-attn achieved HBM GB/s (% peak); decode tokens/s"
 
 _HIP = None  # the HIP runtime torch loaded (ctypes), once a timing event is made
@@ -999,9 +1000,12 @@ def bench_pressure(steps, warmup, cpu=True, cpu_seconds=8.0):
     """One step of a pool under pressure (the pool-pressure configuration):
     the 217,982-block pool of a 200 GB budget (all 28 layers, Qwen2.5-7B
     heads), 512 sequences with log-normal lengths (median 2,048, sigma 1,
-    capped at 32,768) in blocks from a seeded permutation of the pool. Per
-    step and layer, 8 sequences append a 512-token chunk (mkv_append_host:
-    host u32 slots, the same for every layer, so uploaded once per step) and the other 504 run
+    capped at 32,768) in blocks from a seeded permutation of the pool. Eight
+    prefills in progress have a 512-token chunk of their prompt left; the
+    engine's budget rule (PrefillAdder, 4,096 prefill tokens per step) gives
+    each its chunk. Per step and layer, the 8 append their chunk
+    (mkv_append_host: host u32 slots, the same for every layer, so uploaded
+    once per step) and the other 504 run
     the fused append + decode attention from a plan holding the step's host
     tables; the chunks' prefill attention is left out, as the configuration
     states."""
@@ -1014,7 +1018,7 @@ def bench_pressure(steps, warmup, cpu=True, cpu_seconds=8.0):
     L, Hq, Hkv, D = cfg["num_layers"], cfg["num_q_heads"], cfg["num_kv_heads"], cfg["head_dim"]
     nblocks, seqs, chunk, chunk_seqs = 217_982, 512, 512, 8
     batch, chunk_slots, lengths = wl.pool_pressure_step(nblocks, seqs, chunk, chunk_seqs,
-                                                        wl.SplitMix64(wl.BASE_SEED + 4))
+                                                        wl.SplitMix64(wl.BASE_SEED + 4), budget=PREFILL_BUDGET)
     desc = PoolDesc(L, Hkv, Hq, D, nblocks, "bf16")
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream()

@@ -135,6 +135,38 @@ MKVH_API int mkvh_bm_fork(mkvh_block_manager *bm, uint64_t parent, uint64_t chil
  * of a shared block writes in place. */
 MKVH_API int mkvh_bm_append(mkvh_block_manager *bm, uint64_t seq, int32_t n_new, int32_t *out_slots,
                             int32_t *out_cow_src, int32_t *out_cow_dst, int32_t *out_n_cow);
+/* The chunking rule of PrefillAdder (inference-engine/src/prefill.rs:27-36,
+ * 99-114) over requests whose prefill is in progress, in order, with no
+ * pool involved: request i, with remaining[i] prompt tokens still to write,
+ * gets out_chunks[i] = min(remaining[i], budget - used) tokens; once the
+ * budget is used up the loop stops and the rest get 0, as does a request
+ * with nothing remaining. *out_used = tokens scheduled. budget is the
+ * engine's max_prefill_tokens_per_iter minus the step's decode tokens
+ * (scheduler.rs:14-18). */
+MKVH_API int mkvh_schedule_prefill_chunks(int64_t budget, const int64_t *remaining, int32_t n,
+                                          int64_t *out_chunks, int64_t *out_used);
+/* PrefillAdder::run (prefill.rs:21-114) on the block manager's books.
+ * 1. in_progress[0..n_in_progress): admitted sequences whose prompt is not
+ *    all written, in order; remaining = prompt length - tokens written; the
+ *    chunk rule above.
+ * 2. Then, while budget remains, waiting requests in order: request i's
+ *    prompt is waiting_tokens[waiting_indptr[i] .. waiting_indptr[i+1]); it
+ *    is admitted under sequence id waiting[i] as mkvh_bm_admit does (evict
+ *    the deficit once, radix match, allocate the rest), and gets its chunk by
+ *    the same rule from its cached length on. The first request the pool
+ *    cannot hold ends admission (the reference's `break`), as does the
+ *    budget.
+ * out_chunks[n_in_progress + n_waiting]: each request's chunk this step
+ * (0: none; an admitted request whose whole prompt was cached gets 0, as in
+ * the reference). *out_n_admitted: waiting requests admitted (a prefix of
+ * the list: the engine moves them to its prefilling list);
+ * out_cached_lens[i] (i < *out_n_admitted): their radix hits. Append each
+ * chunk with mkvh_bm_append. */
+MKVH_API int mkvh_bm_schedule_prefill(mkvh_block_manager *bm, int64_t budget, const uint64_t *in_progress,
+                                      int32_t n_in_progress, const uint64_t *waiting,
+                                      const int64_t *waiting_indptr, const uint32_t *waiting_tokens,
+                                      int32_t n_waiting, int64_t *out_chunks, int32_t *out_n_admitted,
+                                      int64_t *out_cached_lens);
 /* Prefill complete (scheduler.rs:117): full pages enter the tree; the tree
  * holds its own reference to each page it adopts. */
 MKVH_API int mkvh_bm_promote(mkvh_block_manager *bm, uint64_t seq, const uint32_t *tokens,

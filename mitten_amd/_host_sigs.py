@@ -39,6 +39,8 @@ HOST_SIGNATURES = {
     "mkvh_bm_admit": (c_int, [P, u64, U32P, i64, I64P]),
     "mkvh_bm_fork": (c_int, [P, u64, u64]),
     "mkvh_bm_append": (c_int, [P, u64, i32, I32P, I32P, I32P, I32P]),
+    "mkvh_schedule_prefill_chunks": (c_int, [i64, I64P, i32, I64P, I64P]),
+    "mkvh_bm_schedule_prefill": (c_int, [P, i64, U64P, i32, U64P, I64P, U32P, i32, I64P, ctypes.POINTER(i32), I64P]),
     "mkvh_bm_promote": (c_int, [P, u64, U32P, i64]),
     "mkvh_bm_release": (c_int, [P, u64]),
     "mkvh_bm_evict": (c_int, [P, i64, I64P]),

@@ -302,7 +302,8 @@ struct Radix {
 // ---------------------------------------------------------------------------
 struct Seq {
   std::vector<uint32_t> blocks;
-  int64_t len = 0;
+  int64_t len = 0;     // tokens written
+  int64_t prompt = 0;  // prompt length given at admission
   std::vector<size_t> locked;
 };
 
@@ -586,6 +587,7 @@ int mkvh_bm_admit(mkvh_block_manager *bm, uint64_t seq, const uint32_t *tokens, 
     s.blocks.push_back(b);
   }
   s.len = (int64_t)matched;
+  s.prompt = n_tokens;
   m->seqs.emplace(seq, std::move(s));
   if (out_cached_len) *out_cached_len = (int64_t)matched;
   return held;
@@ -656,6 +658,75 @@ int mkvh_bm_append(mkvh_block_manager *bm, uint64_t seq, int32_t n_new, int32_t 
     out_slots[p - s.len] = (int32_t)(s.blocks[p / ps] * ps + p % ps);
   }
   s.len = end;
+  return MKVH_OK;
+}
+
+// schedule_prefill_chunk (prefill.rs:99-114) for one request: min(remaining,
+// budget - used), nothing when the request has no prompt left.
+static int64_t prefill_chunk(int64_t remaining, int64_t budget, int64_t &used) {
+  if (remaining <= 0) return 0;
+  const int64_t chunk = std::min(remaining, budget - used);
+  if (chunk <= 0) return 0;
+  used += chunk;
+  return chunk;
+}
+
+int mkvh_schedule_prefill_chunks(int64_t budget, const int64_t *remaining, int32_t n, int64_t *out_chunks,
+                                 int64_t *out_used) {
+  if (budget < 0 || n < 0 || (n && (!remaining || !out_chunks)))
+    return fail(MKVH_ERR_INVALID_ARGUMENT, "bad chunk-schedule arguments");
+  for (int32_t i = 0; i < n; i++)
+    if (remaining[i] < 0) return fail(MKVH_ERR_INVALID_ARGUMENT, "remaining[%d] = %lld < 0", i, (long long)remaining[i]);
+  int64_t used = 0;
+  for (int32_t i = 0; i < n; i++) out_chunks[i] = 0;
+  // prefill.rs:27-36: in order, stopping once the budget is used up.
+  for (int32_t i = 0; i < n && used < budget; i++) out_chunks[i] = prefill_chunk(remaining[i], budget, used);
+  if (out_used) *out_used = used;
+  return MKVH_OK;
+}
+
+int mkvh_bm_schedule_prefill(mkvh_block_manager *bm, int64_t budget, const uint64_t *in_progress, int32_t n_in_progress,
+                             const uint64_t *waiting, const int64_t *waiting_indptr, const uint32_t *waiting_tokens,
+                             int32_t n_waiting, int64_t *out_chunks, int32_t *out_n_admitted,
+                             int64_t *out_cached_lens) {
+  H_CHECK(bm);
+  BlockMgr *m = reinterpret_cast<BlockMgr *>(bm);
+  if (budget < 0 || n_in_progress < 0 || n_waiting < 0 || !out_n_admitted ||
+      (n_in_progress && !in_progress) || (n_in_progress + n_waiting > 0 && !out_chunks) ||
+      (n_waiting && (!waiting || !waiting_indptr || !out_cached_lens)))
+    return fail(MKVH_ERR_INVALID_ARGUMENT, "bad prefill-schedule arguments");
+  // Every argument is checked before the books change.
+  for (int32_t i = 0; i < n_in_progress; i++)
+    if (!m->seqs.count(in_progress[i]))
+      return fail(MKVH_ERR_NOT_FOUND, "unknown sequence %llu", (unsigned long long)in_progress[i]);
+  if (n_waiting && waiting_indptr[0] != 0) return fail(MKVH_ERR_INVALID_ARGUMENT, "waiting_indptr[0] != 0");
+  for (int32_t i = 0; i < n_waiting; i++) {
+    if (waiting_indptr[i + 1] <= waiting_indptr[i])
+      return fail(MKVH_ERR_INVALID_ARGUMENT, "waiting request %d has no prompt tokens", i);
+    if (m->seqs.count(waiting[i]))
+      return fail(MKVH_ERR_INVALID_ARGUMENT, "sequence %llu already admitted", (unsigned long long)waiting[i]);
+  }
+  if (n_waiting && !waiting_tokens) return fail(MKVH_ERR_INVALID_ARGUMENT, "NULL waiting tokens");
+  for (int32_t i = 0; i < n_in_progress + n_waiting; i++) out_chunks[i] = 0;
+  *out_n_admitted = 0;
+  int64_t used = 0;
+  // 1. In-progress prefills first (prefill.rs:27-36).
+  for (int32_t i = 0; i < n_in_progress && used < budget; i++) {
+    const Seq &s = m->seqs.at(in_progress[i]);
+    out_chunks[i] = prefill_chunk(s.prompt - s.len, budget, used);
+  }
+  // 2. Admission from the waiting queue while budget remains (prefill.rs:39-93).
+  for (int32_t i = 0; i < n_waiting && used < budget; i++) {
+    int64_t cached = 0;
+    const uint32_t *tok = waiting_tokens + waiting_indptr[i];
+    const int64_t n_tok = waiting_indptr[i + 1] - waiting_indptr[i];
+    const int rc = mkvh_bm_admit(bm, waiting[i], tok, n_tok, &cached);
+    if (rc == MKVH_ERR_EXHAUSTED) break;  // cannot admit this request yet
+    if (rc != MKVH_OK) return rc;
+    out_cached_lens[i] = cached;
+    *out_n_admitted = i + 1;
+    out_chunks[n_in_progress + i] = prefill_chunk(n_tok - cached, budget, used);
+  }
   return MKVH_OK;
 }
 

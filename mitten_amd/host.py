@@ -238,6 +238,18 @@ class RadixCache(_Handle):
         return _lib_h().mkvh_radix_num_nodes(self._h)
 
 
+def schedule_prefill_chunks(budget: int, remaining) -> tuple[list[int], int]:
+    """The chunking rule of PrefillAdder (inference-engine/src/prefill.rs:27-36,
+    99-114) over in-progress prefills, in order: each gets min(remaining,
+    budget - used) tokens until the budget is used up. Returns (chunks,
+    tokens used)."""
+    r = np.ascontiguousarray(remaining, np.int64)
+    out, used = np.zeros(max(1, r.size), np.int64), ctypes.c_int64()
+    _check(_lib_h().mkvh_schedule_prefill_chunks(budget, _ptr(r, I64P), r.size, _ptr(out, I64P),
+                                                 ctypes.byref(used)))
+    return [int(c) for c in out[:r.size]], used.value
+
+
 class BlockManager(_Handle):
     """Block tables of live sequences over a pool of `num_blocks` device blocks,
     with the radix tree caching up to `max_cached_pages` full pages."""
@@ -269,6 +281,29 @@ class BlockManager(_Handle):
         _check(_lib_h().mkvh_bm_append(self._h, seq, n_new, _ptr(slots, I32P), _ptr(src, I32P), _ptr(dst, I32P),
                                        ctypes.byref(n)))
         return slots[:n_new], [(int(src[0]), int(dst[0]))] if n.value else []
+
+    def schedule_prefill(self, budget: int, in_progress, waiting):
+        """PrefillAdder::run (prefill.rs:21-114) on these books: in-progress
+        prefills (sequence ids, in order) first, then waiting requests
+        [(seq, prompt tokens), ...] admitted in order while budget remains,
+        each chunk min(remaining, budget - used). Returns (chunks of the
+        in-progress sequences, chunks of the waiting ones, number admitted
+        (a prefix of `waiting`), their cached lengths)."""
+        ip = np.ascontiguousarray(list(in_progress), np.uint64)
+        wseq = np.ascontiguousarray([s for s, _ in waiting], np.uint64)
+        toks = [_u32(t) for _, t in waiting]
+        windptr = np.zeros(len(toks) + 1, np.int64)
+        np.cumsum([t.size for t in toks], out=windptr[1:])
+        wtok = np.concatenate(toks) if toks else np.zeros(1, np.uint32)
+        chunks = np.zeros(max(1, ip.size + wseq.size), np.int64)
+        cached = np.zeros(max(1, wseq.size), np.int64)
+        n_adm = ctypes.c_int32()
+        _check(_lib_h().mkvh_bm_schedule_prefill(
+            self._h, budget, _ptr(ip, U64P), ip.size, _ptr(wseq, U64P), _ptr(windptr, I64P), _ptr(wtok, U32P),
+            wseq.size, _ptr(chunks, I64P), ctypes.byref(n_adm), _ptr(cached, I64P)))
+        k = n_adm.value
+        return ([int(c) for c in chunks[:ip.size]], [int(c) for c in chunks[ip.size:ip.size + wseq.size]], k,
+                [int(c) for c in cached[:k]])
 
     def promote(self, seq: int, tokens) -> None:
         t = _u32(tokens)

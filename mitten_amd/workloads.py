@@ -160,15 +160,25 @@ def shared_prefix_batch(num_seqs: int, prefix: int, suffix_lo: int, suffix_hi: i
 
 
 def pool_pressure_step(num_blocks: int, num_seqs: int, chunk: int, chunk_seqs: int,
-                       rng: SplitMix64) -> tuple[DecodeBatch, np.ndarray, np.ndarray]:
+                       rng: SplitMix64, budget: int | None = None) -> tuple[DecodeBatch, np.ndarray, np.ndarray]:
     """One step of a pool under pressure: `num_seqs` sequences with lengths
     ~LogNormal(ln 2048, 1) capped at 32,768 hold blocks drawn from a seeded
-    permutation of a `num_blocks` pool; the first `chunk_seqs` append a
-    `chunk`-token chunk, the others decode one token. Returns the decode
-    batch of the decoding sequences, the chunk tokens' slots and all
-    sequences' lengths before the step."""
+    permutation of a `num_blocks` pool. The first `chunk_seqs` are prefills
+    in progress with `chunk` tokens of their prompt left; the engine's
+    budget rule (PrefillAdder, inference-engine/src/prefill.rs:27-36,
+    99-114, in the host library) gives each its chunk under `budget` prefill
+    tokens (default chunk * chunk_seqs: every prefill finishes its prompt),
+    and the others decode one token. Returns the decode batch of the
+    decoding sequences, the chunk tokens' slots and all sequences' lengths
+    before the step."""
+    from .host import schedule_prefill_chunks
+
     lengths = np.asarray(lognormal_lengths(rng, num_seqs, 2048, 1.0, 32768), np.int64)
-    grow = np.where(np.arange(num_seqs) < chunk_seqs, chunk, 1)
+    chunks, _ = schedule_prefill_chunks(chunk * chunk_seqs if budget is None else budget, [chunk] * chunk_seqs)
+    if 0 in chunks:
+        raise ValueError("the budget leaves a prefill without a chunk this step")
+    grow = np.ones(num_seqs, np.int64)
+    grow[:chunk_seqs] = chunks
     nblk = (lengths + grow + PAGE - 1) // PAGE
     if int(nblk.sum()) > num_blocks:
         raise ValueError("the sequences need more blocks than the pool holds")
@@ -177,7 +187,7 @@ def pool_pressure_step(num_blocks: int, num_seqs: int, chunk: int, chunk_seqs: i
     tables = [perm[starts[b]:starts[b + 1]] for b in range(num_seqs)]
     chunk_slots = []
     for b in range(chunk_seqs):
-        pos = lengths[b] + np.arange(chunk)
+        pos = lengths[b] + np.arange(grow[b])
         chunk_slots.append(tables[b][pos // PAGE].astype(np.int64) * PAGE + pos % PAGE)
     dec = range(chunk_seqs, num_seqs)
     ctx = lengths[chunk_seqs:]

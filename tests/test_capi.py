@@ -95,3 +95,22 @@ def test_last_error_is_thread_local_and_descriptive():
     s = np.array([999], np.int32)
     assert lib.mkv_validate_slots(ctypes.byref(d), s.ctypes.data_as(_lib.I32P), 1) == 1
     assert b"slot[0] = 999" in lib.mkv_last_error()
+
+
+@pytest.mark.parametrize("bad,msg", [(np.array([3, 2**32 + 5], np.int64), "2^32"),
+                                     (np.array([2**32], np.uint64), "2^32"),
+                                     (np.array([4, -1], np.int32), "negative"),
+                                     (np.array([1.5]), "integers")])
+def test_host_u32_metadata_refuses_values_outside_u32(bad, msg):
+    """Engine ids and slots are u32: 2^32 + 5 must not wrap to slot 5 (a
+    valid slot of another sequence), and negative or fractional values are
+    not ids."""
+    from mitten_amd import device_pool as dp
+
+    for name in ("slot_mapping", "block_ids"):
+        with pytest.raises(BackendError) as ei:
+            dp._host_u32(bad, name)
+        assert ei.value.status == dp.MKV_ERR_INVALID_ARGUMENT
+        assert name in str(ei.value) and msg in str(ei.value)
+    assert dp._host_u32(np.array([0, 2**32 - 1], np.int64), "ids").tolist() == [0, 2**32 - 1]
+    assert dp._host_u32([], "ids").size == 0

@@ -118,6 +118,24 @@ def test_gather_host_matches_device_form_and_oracle(shape):
     pool.close()
 
 
+def test_host_ids_of_2_pow_32_or_more_are_refused_not_wrapped():
+    """A slot of 2^32 + 5 would wrap to slot 5 in a u32 cast (a valid slot of
+    the pool); a block id of 2^32 + 1 to block 1. Both are refused before
+    anything is launched, and the pool is untouched."""
+    desc, pool, host = _pool("qwen7b-bf16", 8, 14)
+    k = normal(15, (2, desc.num_kv_heads, desc.head_dim), desc.dtype)
+    v = normal(16, (2, desc.num_kv_heads, desc.head_dim), desc.dtype)
+    with pytest.raises(BackendError) as ei:
+        pool.append(0, to_device(k), to_device(v), np.array([3, 2**32 + 5], np.int64))
+    assert "2^32" in str(ei.value)
+    with pytest.raises(BackendError) as ei:
+        pool.plan([20], block_indptr=np.array([0, 2], np.int64), block_ids=np.array([0, 2**32 + 1], np.int64))
+    assert "2^32" in str(ei.value)
+    pool.check()
+    assert np.array_equal(bits(pool.read()), bits(host))
+    pool.close()
+
+
 def test_gather_host_rejects_short_table():
     desc, pool, host = _pool("qwen7b-bf16", 8, 14)
     with pytest.raises(BackendError) as ei:

@@ -244,10 +244,15 @@ def test_c4_radix_sharing_cow_decode_eviction_and_compaction():
 
 # --------------------------------------------------------------------- C5 ----
 
-C5_BLOCKS, C5_SEQS, C5_CHUNK, C5_CHUNK_SEQS = 217_982, 512, 512, 8
+C5_BLOCKS, C5_SEQS, C5_CHUNK, C5_CHUNK_SEQS, C5_BUDGET = 217_982, 512, 512, 8, 4096
 
 
 def test_c5_pool_pressure_chunked_append_and_decode():
+    """Sixteen prefills in progress, each with a 512-token chunk of its prompt
+    left; the block manager's budget rule (PrefillAdder, 4,096 prefill tokens
+    per step) gives the first eight their chunks in the first step and the
+    other eight in the second. Every sequence whose prefill is done decodes
+    one token per step."""
     import torch
 
     L, Hq, Hkv, D = 1, 28, 4, 128  # Qwen-7B heads, 1 of 28 layers
@@ -256,10 +261,12 @@ def test_c5_pool_pressure_chunked_append_and_decode():
     desc = PoolDesc(L, Hkv, Hq, D, C5_BLOCKS, "bf16")
     bm = BlockManager(C5_BLOCKS)
     seqs = list(range(C5_SEQS))
+    prefilling = seqs[:2 * C5_CHUNK_SEQS]
+    prompt = [n + (C5_CHUNK if s in prefilling else 0) for s, n in enumerate(lengths)]
     for s in seqs:
-        bm.admit(s, _tokens(10_000 + s, lengths[s]))
+        bm.admit(s, _tokens(10_000 + s, prompt[s]))
         bm.append(s, lengths[s])
-    assert bm.live_blocks() == sum((n + 15) // 16 for n in lengths)
+    assert bm.live_blocks() == sum((n + 15) // 16 for n in prompt)
     with DeviceKvPool(desc) as pool:
         view = pool.tensor()
         gen = torch.Generator(device="cuda")
@@ -273,7 +280,10 @@ def test_c5_pool_pressure_chunked_append_and_decode():
             return to_host(t.contiguous())
 
         for step in range(2):
-            chunk = seqs[step * C5_CHUNK_SEQS:(step + 1) * C5_CHUNK_SEQS]
+            got, _, _, _ = bm.schedule_prefill(C5_BUDGET, prefilling, [])
+            chunk = [s for s, c in zip(prefilling, got) if c]
+            assert chunk == seqs[step * C5_CHUNK_SEQS:(step + 1) * C5_CHUNK_SEQS]
+            assert [c for c in got if c] == [C5_CHUNK] * C5_CHUNK_SEQS
             slots = np.concatenate([bm.append(s, C5_CHUNK)[0] for s in chunk]).astype(np.int32)
             kc = normal(700 + step, (slots.size, Hkv, D), "bf16")
             vc = normal(800 + step, (slots.size, Hkv, D), "bf16")
@@ -299,7 +309,8 @@ def test_c5_pool_pressure_chunked_append_and_decode():
                 ref = orc.decode_attention(md, mini, 0, widen(qc[[r * C5_CHUNK + i for i in rows]]), vptr, vids,
                                            np.asarray([p + 1 for p in pos], np.int32))
                 assert_attention_close(oc[[r * C5_CHUNK + i for i in rows]], ref, "bf16")
-            dec = [s for s in seqs if s not in chunk]
+            dec = [s for s in seqs if s not in prefilling]  # prefill done: decoding
+            prefilling = [s for s in prefilling if s not in chunk]  # these chunks end their prompts
             new = np.concatenate([bm.append(s, 1)[0] for s in dec]).astype(np.int32)
             indptr, ids, ctx = bm.batch(dec)
             plan = pool.plan(ctx, block_indptr=_u32(indptr), block_ids=_u32(ids))

@@ -444,3 +444,112 @@ def test_block_manager_shared_prefix_after_fork():
     assert sl.tolist() == [100 + 5 - 96, 100 + 6 - 96, 100 + 7 - 96]
     own = [si[sp[b]:sp[b + 1]] for b in range(3)]
     assert len({int(o[0]) for o in own}) == 3  # each sequence's own copy of the partial page
+
+
+# ------------------------------ PrefillAdder's budget (prefill.rs:21-114) ----
+
+
+@pytest.mark.parametrize("budget,remaining,chunks,used", [
+    # In order, min(remaining, budget - used): the second request gets what is left.
+    (100, [30, 200, 5], [30, 70, 0], 100),
+    # The loop stops once the budget is used up (prefill.rs:28-30).
+    (10, [10, 4], [10, 0], 10),
+    # A request with nothing left gets no chunk and uses no budget (:101-104).
+    (64, [0, 40, 40], [0, 40, 24], 64),
+    # Budget 0: nothing is scheduled.
+    (0, [16, 16], [0, 0], 0),
+    # The pool-pressure step: 8 prefills with a 512-token chunk left each
+    # fill a budget of 4,096; a ninth waits.
+    (4096, [512] * 9, [512] * 8 + [0], 4096),
+])
+def test_prefill_chunk_rule_hand_worked(budget, remaining, chunks, used):
+    from mitten_amd.host import schedule_prefill_chunks
+
+    got, u = schedule_prefill_chunks(budget, remaining)
+    assert got == chunks and u == used
+
+
+def test_prefill_chunk_rule_matches_a_loop_restatement():
+    """Random cases against a plain restatement of prefill.rs:27-36 + 99-114."""
+    from mitten_amd.host import schedule_prefill_chunks
+
+    rng = np.random.default_rng(5)
+    for _ in range(200):
+        rem = rng.integers(0, 300, rng.integers(0, 12)).tolist()
+        budget = int(rng.integers(0, 1200))
+        want, used = [0] * len(rem), 0
+        for i, r in enumerate(rem):
+            if used >= budget:
+                break
+            c = min(r, budget - used)
+            if r > 0 and c > 0:
+                want[i] = c
+                used += c
+        assert schedule_prefill_chunks(budget, rem) == (want, used)
+
+
+def test_schedule_prefill_in_progress_first_then_admission():
+    """Two prefills in progress (prompts 100 and 300 tokens, 40 and 0 written)
+    and two waiting prompts. Budget 320: the in-progress ones get 60 and
+    min(300, 260) = 260 in order, and no waiting request is admitted, since
+    admission needs budget left (prefill.rs:39). Budget 400: 60 and 300, then
+    the first waiting request is admitted and gets the 40 tokens left; the
+    second is not admitted."""
+    bm = BlockManager(256, 16)
+    bm.admit(1, _tokens(1, 100))
+    bm.append(1, 40)
+    bm.admit(2, _tokens(2, 300))
+    waiting = [(3, _tokens(3, 200)), (4, _tokens(4, 50))]
+    ip, wc, n_adm, cached = bm.schedule_prefill(320, [1, 2], waiting)
+    assert ip == [60, 260] and n_adm == 0 and wc == [0, 0] and cached == []
+    ip, wc, n_adm, cached = bm.schedule_prefill(400, [1, 2], waiting)
+    assert ip == [60, 300] and n_adm == 1 and wc == [40, 0] and cached == [0]
+    assert bm.seq_len(3) == 0  # admitted: blocks reserved, nothing written yet
+    bm.append(3, 40)
+    bm.check_invariants()
+
+
+def test_schedule_prefill_admission_stops_at_the_first_that_does_not_fit():
+    """The reference breaks out of admission at the first request the pool
+    cannot hold (prefill.rs:51-54), even when a later, smaller one would fit."""
+    bm = BlockManager(10, 16)
+    waiting = [(1, _tokens(1, 64)), (2, _tokens(2, 200)), (3, _tokens(3, 16))]
+    ip, wc, n_adm, cached = bm.schedule_prefill(10_000, [], waiting)
+    assert n_adm == 1 and wc == [64, 0, 0] and ip == []
+    assert bm.free_blocks() == 6
+    bm.check_invariants()
+
+
+def test_schedule_prefill_radix_hit_starts_the_chunk_after_the_cached_prefix():
+    """A waiting prompt whose first 32 tokens are in the tree is admitted with
+    cached length 32 and chunked from there; a prompt cached in full gets no
+    chunk (the reference's remaining == 0 case)."""
+    bm = BlockManager(64, 16)
+    p = _tokens(7, 32)
+    bm.admit(1, p)
+    bm.append(1, 32)
+    bm.promote(1, p)
+    bm.release(1)
+    longer = np.concatenate([p, _tokens(8, 20)])
+    ip, wc, n_adm, cached = bm.schedule_prefill(15, [], [(2, longer), (3, p)])
+    assert n_adm == 1 and cached == [32] and wc == [15, 0]
+    bm.append(2, 15)  # the step writes the chunk
+    ip, wc, n_adm, cached = bm.schedule_prefill(100, [2], [(3, p)])
+    assert ip == [5] and n_adm == 1 and cached == [32] and wc == [0]
+    bm.check_invariants()
+
+
+def test_schedule_prefill_refuses_bad_arguments_before_changing_anything():
+    from mitten_amd.host import HostError
+
+    bm = BlockManager(32, 16)
+    bm.admit(1, _tokens(1, 20))
+    free = bm.free_blocks()
+    with pytest.raises(HostError):
+        bm.schedule_prefill(100, [9], [(2, _tokens(2, 20))])  # unknown in-progress sequence
+    with pytest.raises(HostError):
+        bm.schedule_prefill(100, [1], [(1, _tokens(2, 20))])  # waiting id already admitted
+    with pytest.raises(HostError):
+        bm.schedule_prefill(-1, [1], [])
+    assert bm.free_blocks() == free
+    bm.check_invariants()

@@ -4,6 +4,7 @@ state, each checked from the tables themselves."""
 from __future__ import annotations
 
 import numpy as np
+import pytest
 
 from mitten_amd import workloads as wl
 
@@ -61,3 +62,17 @@ def test_lognormal_lengths_median_and_cap():
     assert 1800 < np.median(x) < 2300  # median of LogNormal(ln 2048, 1)
     lx = np.log(x[(x > 1) & (x < 32768)])
     assert 0.9 < lx.std() < 1.1
+
+
+def test_pool_pressure_chunks_come_from_the_budget_rule():
+    """The chunks are the budget rule's: 8 prefills with 512 tokens left fill a
+    4,096-token budget; at 4,000 the eighth gets the 416 tokens left; a
+    budget that leaves a prefill without a chunk this step is refused (that
+    prefill would neither prefill nor decode)."""
+    batch, chunk_slots, _ = wl.pool_pressure_step(60_000, 64, 512, 8, wl.SplitMix64(12), budget=4096)
+    assert chunk_slots.size == 8 * 512
+    _, short, _ = wl.pool_pressure_step(60_000, 64, 512, 8, wl.SplitMix64(12), budget=4000)
+    assert short.size == 7 * 512 + 416
+    assert np.array_equal(short, chunk_slots[:short.size])  # the same slots, the last chunk cut short
+    with pytest.raises(ValueError):
+        wl.pool_pressure_step(60_000, 64, 512, 8, wl.SplitMix64(12), budget=7 * 512)
