@@ -52,7 +52,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleSlack = 8.0f;  // log2 units: p <= 2^8 between rescales
 constexpr int kQChunkMfma = 16;
-constexpr int kQChunkValu = 8;
+constexpr int kQChunkValu = 8;       // query heads per wave on the per-head (VALU) kernels
+constexpr int kQChunkValuSmall = 2;  // the same for launches too small to fill the device (see the plan)
 constexpr int kRing = 3;       // MFMA loop: blocks loaded ahead + 1
 constexpr int kBlockWeight = 8;    // plan: weight of one block in a piece ...
 constexpr int kSwitchWeight = 12;  // ... and of a sequence start inside it (about 1.5 blocks)
@@ -356,9 +357,9 @@ struct VTraits {
   static_assert(LPT >= 1 && LPT <= 64 && (64 % LPT) == 0, "unsupported head_dim");
 };
 
-template <int D, bool BF16>
+template <int D, bool BF16, int QC = kQChunkValu>
 struct VState {
-  float m[kQChunkValu], l[kQChunkValu], acc[kQChunkValu][VTraits<D, BF16>::VEC];
+  float m[QC], l[QC], acc[QC][VTraits<D, BF16>::VEC];
 };
 
 template <bool BF16, int VEC>
@@ -376,10 +377,10 @@ __device__ __forceinline__ void load_chunk(const uint8_t *p, float (&f)[VEC]) {
   }
 }
 
-template <int D, bool BF16>
-__device__ __forceinline__ void valu_segment(const KArgs &a, const Seg &sg, int lane, VState<D, BF16> &st) {
+template <int D, bool BF16, int QC>
+__device__ __forceinline__ void valu_segment(const KArgs &a, const Seg &sg, int lane, VState<D, BF16, QC> &st) {
   using T = VTraits<D, BF16>;
-  constexpr int ES = T::ES, VEC = T::VEC, LPT = T::LPT, TPI = T::TPI, QC = kQChunkValu;
+  constexpr int ES = T::ES, VEC = T::VEC, LPT = T::LPT, TPI = T::TPI;
   const int lt = lane / LPT, ld = lane % LPT;
   const int q0 = sg.qc * QC;
   const int nq = min(QC, a.G - q0);
@@ -503,11 +504,11 @@ __device__ __forceinline__ void valu_segment(const KArgs &a, const Seg &sg, int 
   }
 }
 
-template <int D, bool BF16>
-__device__ __forceinline__ void valu_store(const KArgs &a, const Seg &sg, int lane, const VState<D, BF16> &st,
+template <int D, bool BF16, int QC>
+__device__ __forceinline__ void valu_store(const KArgs &a, const Seg &sg, int lane, const VState<D, BF16, QC> &st,
                                            bool final, int64_t prow_base, int64_t prow_stride) {
   using T = VTraits<D, BF16>;
-  constexpr int ES = T::ES, VEC = T::VEC, LPT = T::LPT, QC = kQChunkValu;
+  constexpr int ES = T::ES, VEC = T::VEC, LPT = T::LPT;
   if (lane >= LPT) return;
   const int ld = lane;
   const int q0 = sg.qc * QC;
@@ -539,8 +540,9 @@ __device__ __forceinline__ void valu_store(const KArgs &a, const Seg &sg, int la
   }
 }
 
-// Processes one segment with the selected path and stores its result.
-template <int D, bool BF16, bool MFMA>
+// Processes one segment with the selected path and stores its result. QC:
+// query heads per wave on the VALU path (KArgs::nqc must be ceil(G / QC)).
+template <int D, bool BF16, bool MFMA, int QC = kQChunkValu>
 __device__ __forceinline__ void run_segment(const KArgs &a, const Seg &sg, int lane, bool final,
                                             int64_t prow_base, int64_t prow_stride) {
   if constexpr (MFMA) {
@@ -548,9 +550,9 @@ __device__ __forceinline__ void run_segment(const KArgs &a, const Seg &sg, int l
     mfma_segment<D>(a, sg, lane, st);
     mfma_store<D>(a, sg, lane, st, final, prow_base, prow_stride);
   } else {
-    VState<D, BF16> st;
-    valu_segment<D, BF16>(a, sg, lane, st);
-    valu_store<D, BF16>(a, sg, lane, st, final, prow_base, prow_stride);
+    VState<D, BF16, QC> st;
+    valu_segment<D, BF16, QC>(a, sg, lane, st);
+    valu_store<D, BF16, QC>(a, sg, lane, st, final, prow_base, prow_stride);
   }
 }
 
@@ -922,8 +924,9 @@ attn_stream_kernel(KArgs a, PlanDev pd) {
   if (a.new_k && qc == 0) store_new_rows<D>(a, lane, h, idv, seqv, metav, n, badv);
 }
 
-// One workgroup per (piece, group of <= 4 (KV head, query chunk) waves).
-template <int D, bool BF16, bool MFMA>
+// One workgroup per (piece, group of <= 4 (KV head, query chunk) waves). QC:
+// query heads per wave on the VALU path.
+template <int D, bool BF16, bool MFMA, int QC = kQChunkValu>
 __global__ void __launch_bounds__(256) attn_planned_kernel(KArgs a, PlanDev pd) {
   constexpr int ES = BF16 ? 2 : 4;
   const int lane = threadIdx.x & 63;
@@ -965,7 +968,7 @@ __global__ void __launch_bounds__(256) attn_planned_kernel(KArgs a, PlanDev pd) 
     }
     const bool single = pd.flat_meta[sb] & kMetaSingle;
     if (a.gk) sg.gtok = a.gtok0[b];
-    run_segment<D, BF16, MFMA>(a, sg, lane, single, (int64_t)(p + b) * a.Hq, 1);
+    run_segment<D, BF16, MFMA, QC>(a, sg, lane, single, (int64_t)(p + b) * a.Hq, 1);
   }
 }
 
@@ -1844,6 +1847,22 @@ static KArgs make_kargs(Pool *p, int32_t layer, const void *d_q, void *d_o, cons
     }                                                                                              \
   } while (0)
 
+// Launches VALU kernel `KERNEL<D, BF16, false, QC>` for the pool geometry.
+#define MKV_DISPATCH_VALU_QC(KERNEL, QC, GRID, BLOCK, STREAM, ...)                                      \
+  do {                                                                                                 \
+    const bool bf = g.dtype == MKV_DTYPE_BF16;                                                         \
+    switch (g.D) {                                                                                     \
+      case 32: if (bf) hipLaunchKernelGGL((KERNEL<32, true, false, QC>), GRID, BLOCK, 0, STREAM, __VA_ARGS__);  \
+               else hipLaunchKernelGGL((KERNEL<32, false, false, QC>), GRID, BLOCK, 0, STREAM, __VA_ARGS__); break; \
+      case 64: if (bf) hipLaunchKernelGGL((KERNEL<64, true, false, QC>), GRID, BLOCK, 0, STREAM, __VA_ARGS__);  \
+               else hipLaunchKernelGGL((KERNEL<64, false, false, QC>), GRID, BLOCK, 0, STREAM, __VA_ARGS__); break; \
+      case 128: if (bf) hipLaunchKernelGGL((KERNEL<128, true, false, QC>), GRID, BLOCK, 0, STREAM, __VA_ARGS__); \
+                else hipLaunchKernelGGL((KERNEL<128, false, false, QC>), GRID, BLOCK, 0, STREAM, __VA_ARGS__); break; \
+      default: if (bf) hipLaunchKernelGGL((KERNEL<256, true, false, QC>), GRID, BLOCK, 0, STREAM, __VA_ARGS__); \
+               else hipLaunchKernelGGL((KERNEL<256, false, false, QC>), GRID, BLOCK, 0, STREAM, __VA_ARGS__); break; \
+    }                                                                                                  \
+  } while (0)
+
 // Launches merge kernel `KERNEL<D, BF16>` for the pool geometry.
 #define MKV_DISPATCH_MERGE(KERNEL, GRID, BLOCK, STREAM, ...)                                 \
   do {                                                                                       \
@@ -1903,6 +1922,7 @@ struct Plan {
   int32_t n_prefix = 0;       // shared-prefix ids given at build time (0: none)
   bool all_partial = false;   // every sequence stores partials (built for a shared prefix's suffixes)
   bool beside = false;        // suffix pieces sized to run beside the prefix tiles (one per CU)
+  int32_t valu_qc = kQChunkValu;  // query heads per wave when the per-head (VALU) kernel runs the plan
   int64_t tokens = 0;         // sum of the context lengths
   int32_t max_ctx = 0;        // the longest context
 };
@@ -2297,6 +2317,14 @@ static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t 
     }
   }
   P = (int64_t)f0s.size() - 1;
+  // The per-head (VALU) kernel takes kQChunkValu query heads per wave. A
+  // launch with fewer (block, KV head) units than two per CU cannot fill the
+  // device and is latency-bound: there each wave takes kQChunkValuSmall
+  // heads, which divides a wave's arithmetic by four for the price of more
+  // waves reading the same (cache-resident) K/V. Larger launches keep the
+  // wide chunk, which reads each block once per KV head.
+  const int cus_now = device_cus(pl->pool);
+  const int32_t valu_qc = cus_now > 0 && total * g.Hkv <= 2 * (int64_t)cus_now ? kQChunkValuSmall : kQChunkValu;
   int64_t BP = 0;
   for (int64_t q = 0; q < P; q++) BP = std::max<int64_t>(BP, f0s[q + 1] - f0s[q]);
   DeviceGuard guard(pl->pool->device);
@@ -2416,6 +2444,7 @@ static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t 
   pl->n_merge = n_merge;
   pl->all_partial = all_partial;
   pl->beside = beside;
+  pl->valu_qc = valu_qc;
   pl->tokens = tokens;
   pl->max_ctx = max_ctx;
   return MKV_OK;
@@ -2513,6 +2542,8 @@ static int launch_planned(Pool *p, const Plan *pl, int32_t layer, const void *d_
     d_block_ids = pd.flat_id;
   }
   KArgs a = make_kargs(p, layer, d_q, d_o, d_block_indptr, d_block_ids, scale, flags, use_mfma);
+  const bool small_qc = !use_mfma && pl->valu_qc == kQChunkValuSmall;
+  if (small_qc) a.nqc = (a.G + kQChunkValuSmall - 1) / kQChunkValuSmall;
   a.new_k = reinterpret_cast<const uint8_t *>(d_k_new);
   a.new_v = reinterpret_cast<const uint8_t *>(d_v_new);
   a.ws_ml = reinterpret_cast<float *>(pl->d_ws);
@@ -2579,6 +2610,9 @@ static int launch_planned(Pool *p, const Plan *pl, int32_t layer, const void *d_
       }
       MKV_CHECK_LAUNCH("attn_stream_kernel");
     }
+  } else if (small_qc) {
+    MKV_DISPATCH_VALU_QC(attn_planned_kernel, kQChunkValuSmall, grid, block, hs, a, pd);
+    MKV_CHECK_LAUNCH("attn_planned_kernel");
   } else {
     MKV_DISPATCH(attn_planned_kernel, grid, block, hs, a, pd);
     MKV_CHECK_LAUNCH("attn_planned_kernel");

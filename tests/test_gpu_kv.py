@@ -316,6 +316,19 @@ def test_decode_step_fused_append(shape, kernel, pieces):
     assert_attention_close(got, ref, dt)
 
 
+@pytest.mark.parametrize("ctx", [PLAN_CTX, [480 + 7 * i for i in range(40)]])
+@pytest.mark.parametrize("shape,kernel", [("qwen0.5b-f32", None), ("qwen0.5b-bf16", "valu")])
+def test_per_head_kernel_small_and_wide_query_chunks(shape, kernel, ctx):
+    """The per-head kernel takes 2 query heads per wave for a launch with
+    fewer (block, KV head) units than two per CU (PLAN_CTX: 191 blocks x 2
+    heads) and 8 per wave otherwise (40 sequences of ~600 tokens: ~1,500 x 2).
+    Both, with G = 7 (chunks 2, 2, 2, 1 and 7), fused append included, against
+    the oracle."""
+    got, ref, dt, after, want, info = _planned_case(shape, ctx, 62, kernel=kernel, fused=True)
+    assert np.array_equal(bits(after), bits(want)), "fused append is not bit-exact"
+    assert_attention_close(got, ref, dt)
+
+
 @pytest.mark.parametrize("kernel", ["mfma", "mfma-per-head", "valu"])
 def test_planned_bad_block_id_reported(kernel):
     """An id outside the pool is reported and its block skipped; the other
