@@ -241,7 +241,7 @@ def cpu_baseline(cfg, batch, step_bytes, budget_s: float = 8.0, paged=True):
         per_tok = run(ncal, 1, nthreads, seed) / float(ctx[:ncal].sum())
         layer_s = per_tok * total_tok
         if layer_s <= budget:
-            nseq, passes = len(ctx), int(max(1, min(4 * L, budget // max(layer_s, 1e-9))))
+            nseq, passes = len(ctx), int(max(1, min(2000, budget // max(layer_s, 1e-9))))
         else:
             nseq, passes = _prefix_count(ctx, budget / per_tok), 1
         t = run(nseq, passes, nthreads, seed + 1)
