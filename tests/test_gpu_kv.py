@@ -24,6 +24,9 @@ SHAPES = {
     "g16-bf16": (1, 64, 4, 128, "bf16"),
     "d256-g4-bf16": (1, 16, 4, 256, "bf16"),  # head_dim 256, 2 Q loads per lane in the cooperative kernel
     "d256-g2-bf16": (1, 4, 2, 256, "bf16"),   # head_dim 256, 1 Q load per lane
+    "d32-f32": (1, 12, 2, 32, "f32"),         # the per-head kernel's other head dims, f32
+    "d128-f32": (1, 14, 2, 128, "f32"),
+    "d256-f32": (1, 8, 1, 256, "f32"),
 }
 
 
@@ -325,6 +328,20 @@ def test_per_head_kernel_small_and_wide_query_chunks(shape, kernel, ctx):
     Both, with G = 7 (chunks 2, 2, 2, 1 and 7), fused append included, against
     the oracle."""
     got, ref, dt, after, want, info = _planned_case(shape, ctx, 62, kernel=kernel, fused=True)
+    assert np.array_equal(bits(after), bits(want)), "fused append is not bit-exact"
+    assert_attention_close(got, ref, dt)
+
+
+@pytest.mark.parametrize("small", [True, False])
+@pytest.mark.parametrize("shape,kernel", [("d32-f32", None), ("d128-f32", None), ("d256-f32", None),
+                                          ("qwen7b-bf16", "valu"), ("gemma2b-bf16", "valu"), ("g16-bf16", "valu")])
+def test_per_head_kernel_query_chunks_every_head_dim(shape, kernel, small):
+    """Both query-chunk widths of the per-head kernel at head_dim 32, 128 and
+    256 (f32, and bf16 forced onto it): a few short sequences (under two
+    (block, KV head) units per CU: 2 heads per wave) and forty of ~600 tokens
+    (8 per wave), fused append included, against the oracle."""
+    ctx = [1, 17, 40, 100, 33] if small else [480 + 7 * i for i in range(40)]
+    got, ref, dt, after, want, info = _planned_case(shape, ctx, 63, kernel=kernel, fused=True)
     assert np.array_equal(bits(after), bits(want)), "fused append is not bit-exact"
     assert_attention_close(got, ref, dt)
 
