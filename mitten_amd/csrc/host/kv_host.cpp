@@ -16,6 +16,7 @@
 #include <queue>
 #include <string>
 #include <unordered_map>
+#include <unordered_set>
 #include <vector>
 
 #include "mitten_kv_host.h"
@@ -695,16 +696,23 @@ int mkvh_bm_schedule_prefill(mkvh_block_manager *bm, int64_t budget, const uint6
       (n_in_progress && !in_progress) || (n_in_progress + n_waiting > 0 && !out_chunks) ||
       (n_waiting && (!waiting || !waiting_indptr || !out_cached_lens)))
     return fail(MKVH_ERR_INVALID_ARGUMENT, "bad prefill-schedule arguments");
-  // Every argument is checked before the books change.
-  for (int32_t i = 0; i < n_in_progress; i++)
+  // Every argument is checked before the books change: each sequence id
+  // appears once in the two lists together.
+  std::unordered_set<uint64_t> seen;
+  for (int32_t i = 0; i < n_in_progress; i++) {
     if (!m->seqs.count(in_progress[i]))
       return fail(MKVH_ERR_NOT_FOUND, "unknown sequence %llu", (unsigned long long)in_progress[i]);
+    if (!seen.insert(in_progress[i]).second)
+      return fail(MKVH_ERR_INVALID_ARGUMENT, "sequence %llu listed twice", (unsigned long long)in_progress[i]);
+  }
   if (n_waiting && waiting_indptr[0] != 0) return fail(MKVH_ERR_INVALID_ARGUMENT, "waiting_indptr[0] != 0");
   for (int32_t i = 0; i < n_waiting; i++) {
     if (waiting_indptr[i + 1] <= waiting_indptr[i])
       return fail(MKVH_ERR_INVALID_ARGUMENT, "waiting request %d has no prompt tokens", i);
     if (m->seqs.count(waiting[i]))
       return fail(MKVH_ERR_INVALID_ARGUMENT, "sequence %llu already admitted", (unsigned long long)waiting[i]);
+    if (!seen.insert(waiting[i]).second)
+      return fail(MKVH_ERR_INVALID_ARGUMENT, "sequence %llu listed twice", (unsigned long long)waiting[i]);
   }
   if (n_waiting && !waiting_tokens) return fail(MKVH_ERR_INVALID_ARGUMENT, "NULL waiting tokens");
   for (int32_t i = 0; i < n_in_progress + n_waiting; i++) out_chunks[i] = 0;

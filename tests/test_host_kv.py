@@ -551,5 +551,9 @@ def test_schedule_prefill_refuses_bad_arguments_before_changing_anything():
         bm.schedule_prefill(100, [1], [(1, _tokens(2, 20))])  # waiting id already admitted
     with pytest.raises(HostError):
         bm.schedule_prefill(-1, [1], [])
+    with pytest.raises(HostError):
+        bm.schedule_prefill(100, [1, 1], [])  # an in-progress sequence listed twice
+    with pytest.raises(HostError):
+        bm.schedule_prefill(100, [], [(2, _tokens(2, 20)), (2, _tokens(3, 20))])  # a waiting id twice
     assert bm.free_blocks() == free
     bm.check_invariants()
