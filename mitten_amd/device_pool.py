@@ -158,28 +158,36 @@ def _host_u32(x, name: str) -> np.ndarray:
     return np.ascontiguousarray(a, np.uint32).reshape(-1)
 
 
-def _host_i32(x) -> np.ndarray:
+def _host_i32(x, name: str = "lengths") -> np.ndarray:
+    """Lengths, positions and the i32 metadata of the validators. Values
+    outside i32 are refused rather than wrapped by the cast (a context of
+    2^32 + 5 tokens would otherwise pass as 5)."""
     a = np.asarray(x.numpy() if hasattr(x, "numpy") else x)
+    if a.size:
+        if a.dtype.kind not in "iu":
+            raise BackendError(MKV_ERR_INVALID_ARGUMENT, f"{name} must hold integers, not {a.dtype}")
+        if int(a.max()) > 0x7FFFFFFF or (a.dtype.kind == "i" and int(a.min()) < -0x80000000):
+            raise BackendError(MKV_ERR_INVALID_ARGUMENT, f"{name} holds a value outside int32")
     return np.ascontiguousarray(a, np.int32).reshape(-1)
 
 
 def validate_slots(desc: PoolDesc, slots) -> None:
-    s = np.ascontiguousarray(slots, np.int32)
+    s = _host_i32(slots, "slots")
     _raise(_lib.device_lib().mkv_validate_slots(ctypes.byref(desc.c()), _i32p(s), s.size))
 
 
 def validate_block_tables(desc: PoolDesc, indptr, ids, ctx_lens, max_ctx_len: int) -> None:
-    ip = np.ascontiguousarray(indptr, np.int32)
-    ix = np.ascontiguousarray(ids, np.int32)
-    cl = None if ctx_lens is None else np.ascontiguousarray(ctx_lens, np.int32)
+    ip = _host_i32(indptr, "indptr")
+    ix = _host_i32(ids, "ids")
+    cl = None if ctx_lens is None else _host_i32(ctx_lens, "ctx_lens")
     _raise(_lib.device_lib().mkv_validate_block_tables(
         ctypes.byref(desc.c()), _i32p(ip), _i32p(ix) if ix.size else None,
         _i32p(cl) if cl is not None else None, ip.size - 1, max_ctx_len))
 
 
 def validate_copy_pairs(desc: PoolDesc, src, dst) -> None:
-    s = np.ascontiguousarray(src, np.int32)
-    d = np.ascontiguousarray(dst, np.int32)
+    s = _host_i32(src, "src")
+    d = _host_i32(dst, "dst")
     if s.size != d.size:
         raise BackendError(MKV_ERR_INVALID_ARGUMENT, "src and dst differ in length")
     _raise(_lib.device_lib().mkv_validate_copy_pairs(ctypes.byref(desc.c()), _i32p(s), _i32p(d), s.size))
@@ -357,7 +365,7 @@ class DeviceKvPool:
         torch = _torch()
         d = self.desc
         ip, ix = _host_u32(block_indptr, "block_indptr"), _host_u32(block_ids, "block_ids")
-        cl = _host_i32(ctx_lens)
+        cl = _host_i32(ctx_lens, "ctx_lens")
         B = cl.size
         if ip.size != B + 1:
             raise BackendError(MKV_ERR_INVALID_ARGUMENT, "block_indptr must have num_seqs + 1 entries")
@@ -490,7 +498,7 @@ class DeviceKvPool:
         sequence b's q_lens[b] query rows follow sequence b-1's in q."""
         torch = _torch()
         d = self.desc
-        ql, cl = _host_i32(q_lens), _host_i32(ctx_lens)
+        ql, cl = _host_i32(q_lens, "q_lens"), _host_i32(ctx_lens, "ctx_lens")
         ip, ix = _host_u32(block_indptr, "block_indptr"), _host_u32(block_ids, "block_ids")
         T = int(ql.astype(np.int64).sum())
         self._check_tensor(q, (T, d.num_q_heads, d.head_dim), "q")
@@ -521,7 +529,7 @@ class DeviceKvPool:
         if host != _is_host(positions):
             raise BackendError(MKV_ERR_INVALID_ARGUMENT, "positions and slot_mapping must both be host or device")
         if host:
-            slot_mapping, positions = _host_u32(slot_mapping, "slot_mapping"), _host_i32(positions)
+            slot_mapping, positions = _host_u32(slot_mapping, "slot_mapping"), _host_i32(positions, "positions")
         n = slot_mapping.shape[0]
         if host:
             if positions.size != n:
@@ -885,7 +893,7 @@ class DecodePlan:
         page tables (u32 CSR), held by the plan; prefix_ids: a shared prefix's
         host block ids (suffix plans only). The library copies them before
         returning."""
-        c = _host_i32(ctx_lens)
+        c = _host_i32(ctx_lens, "ctx_lens")
         sh = _stream_handle(stream)
         if (block_indptr is None) != (block_ids is None):
             raise BackendError(MKV_ERR_INVALID_ARGUMENT, "give both block_indptr and block_ids, or neither")

@@ -56,8 +56,16 @@ def _check(status: int) -> None:
     raise HostError(status, msg)
 
 
-def _u32(a) -> np.ndarray:
-    return np.ascontiguousarray(a, np.uint32)
+def _u32(a, name: str = "ids") -> np.ndarray:
+    """Token ids and page ids are u32: values outside [0, 2^32) are refused
+    rather than wrapped by the cast."""
+    x = np.asarray(a)
+    if x.size:
+        if x.dtype.kind not in "iu":
+            raise HostError(INVALID_ARGUMENT, f"{name} must hold integers, not {x.dtype}")
+        if (x.dtype.kind == "i" and int(x.min()) < 0) or int(x.max()) > 0xFFFFFFFF:
+            raise HostError(INVALID_ARGUMENT, f"{name} holds a value outside u32")
+    return np.ascontiguousarray(x, np.uint32)
 
 
 def _ptr(a: np.ndarray, t):
@@ -182,7 +190,7 @@ class RadixCache(_Handle):
 
     def match_prefix(self, tokens):
         """(matched_len, pages, locked_node_ids); locks every matched node."""
-        t = _u32(tokens)
+        t = _u32(tokens, "tokens")
         cap = max(1, t.size // self.page_size)
         pages = np.empty(cap, np.uint32)
         nodes = np.empty(cap, np.uint64)
@@ -192,7 +200,7 @@ class RadixCache(_Handle):
         return ml.value, pages[: npg.value].tolist(), nodes[: nnd.value].tolist()
 
     def insert_prefix(self, tokens, pages) -> None:
-        t, p = _u32(tokens), _u32(pages)
+        t, p = _u32(tokens, "tokens"), _u32(pages, "pages")
         _check(_lib_h().mkvh_radix_insert_prefix(self._h, _ptr(t, U32P), t.size, _ptr(p, U32P), p.size))
 
     def unlock_nodes(self, node_ids) -> None:
@@ -227,7 +235,7 @@ class RadixCache(_Handle):
 
     def promote_request(self, input_ids, device_len: int, kv_pages) -> None:
         """radix_cache.rs:287-294 (a Request's input_ids, device_len, kv_pages)."""
-        t, p = _u32(input_ids), _u32(kv_pages)
+        t, p = _u32(input_ids, "input_ids"), _u32(kv_pages, "kv_pages")
         _check(_lib_h().mkvh_radix_promote_request(self._h, _ptr(t, U32P), t.size, device_len, _ptr(p, U32P),
                                                    p.size))
 
@@ -266,7 +274,7 @@ class BlockManager(_Handle):
 
     def admit(self, seq: int, tokens) -> int:
         """Admission (prefill.rs:39-81); returns the cached prefix length."""
-        t = _u32(tokens)
+        t = _u32(tokens, "tokens")
         out = ctypes.c_int64()
         _check(_lib_h().mkvh_bm_admit(self._h, seq, _ptr(t, U32P), t.size, ctypes.byref(out)))
         return out.value
@@ -291,7 +299,7 @@ class BlockManager(_Handle):
         (a prefix of `waiting`), their cached lengths)."""
         ip = np.ascontiguousarray(list(in_progress), np.uint64)
         wseq = np.ascontiguousarray([s for s, _ in waiting], np.uint64)
-        toks = [_u32(t) for _, t in waiting]
+        toks = [_u32(t, "prompt tokens") for _, t in waiting]
         windptr = np.zeros(len(toks) + 1, np.int64)
         np.cumsum([t.size for t in toks], out=windptr[1:])
         wtok = np.concatenate(toks) if toks else np.zeros(1, np.uint32)
@@ -306,7 +314,7 @@ class BlockManager(_Handle):
                 [int(c) for c in cached[:k]])
 
     def promote(self, seq: int, tokens) -> None:
-        t = _u32(tokens)
+        t = _u32(tokens, "tokens")
         _check(_lib_h().mkvh_bm_promote(self._h, seq, _ptr(t, U32P), t.size))
 
     def release(self, seq: int) -> None:

@@ -17,7 +17,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import _lib
-from .device_pool import MKV_ERR_INVALID_ARGUMENT, BackendError, DeviceKvPool, _raise
+from .device_pool import MKV_ERR_INVALID_ARGUMENT, BackendError, DeviceKvPool, _host_i32, _raise
 
 HEADER_BYTES = 64
 
@@ -105,4 +105,4 @@ def _ids(block_ids):
 
     if isinstance(block_ids, torch.Tensor):
         return block_ids
-    return torch.from_numpy(np.ascontiguousarray(block_ids, np.int32)).cuda()
+    return torch.from_numpy(_host_i32(block_ids, "block_ids")).cuda()

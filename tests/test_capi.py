@@ -114,3 +114,42 @@ def test_host_u32_metadata_refuses_values_outside_u32(bad, msg):
         assert name in str(ei.value) and msg in str(ei.value)
     assert dp._host_u32(np.array([0, 2**32 - 1], np.int64), "ids").tolist() == [0, 2**32 - 1]
     assert dp._host_u32([], "ids").size == 0
+
+
+@pytest.mark.parametrize("bad,msg", [(np.array([7, 2**32 + 5], np.int64), "outside int32"),
+                                     (np.array([2**31], np.int64), "outside int32"),
+                                     (np.array([-2**31 - 1], np.int64), "outside int32"),
+                                     (np.array([2.0]), "integers")])
+def test_host_i32_metadata_refuses_values_outside_i32(bad, msg):
+    """Context lengths, positions and the validators' ids are i32: 2^32 + 5
+    must not wrap to 5, which would pass every later check."""
+    from mitten_amd import device_pool as dp
+
+    with pytest.raises(BackendError) as ei:
+        dp._host_i32(bad, "ctx_lens")
+    assert ei.value.status == dp.MKV_ERR_INVALID_ARGUMENT
+    assert "ctx_lens" in str(ei.value) and msg in str(ei.value)
+    desc = PoolDesc(2, 4, 28, 128, 10, "bf16")
+    with pytest.raises(BackendError):
+        dp.validate_slots(desc, bad)
+    with pytest.raises(BackendError):
+        dp.validate_copy_pairs(desc, bad, bad)
+    assert dp._host_i32(np.array([-2**31, 2**31 - 1], np.int64), "x").tolist() == [-2**31, 2**31 - 1]
+    assert dp._host_i32([], "x").size == 0
+
+
+@pytest.mark.parametrize("bad", [np.array([5, 2**32 + 1], np.int64), np.array([-1], np.int64), np.array([0.5])])
+def test_host_library_refuses_token_and_page_ids_outside_u32(bad):
+    """The radix tree's token ids and page ids are u32 (radix_cache.rs:37-62):
+    a value outside u32 is refused, not wrapped into another token or page."""
+    from mitten_amd.host import INVALID_ARGUMENT, HostError, RadixCache
+
+    rc = RadixCache(16, 8)
+    with pytest.raises(HostError) as ei:
+        rc.insert_prefix(bad, np.arange(1))
+    assert ei.value.status == INVALID_ARGUMENT and "tokens" in str(ei.value)
+    with pytest.raises(HostError) as ei:
+        rc.insert_prefix(np.arange(16 * bad.size), bad)
+    assert ei.value.status == INVALID_ARGUMENT and "pages" in str(ei.value)
+    with pytest.raises(HostError):
+        rc.match_prefix(bad)
