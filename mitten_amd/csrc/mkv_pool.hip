@@ -289,10 +289,14 @@ int check_host_tables(const Geom &g, const uint32_t *indptr, const uint32_t *ids
   if (indptr[num_seqs] > (uint32_t)INT32_MAX)
     return set_error(MKV_ERR_INVALID_ARGUMENT, "more than 2^31 - 1 block ids");
   if (indptr[num_seqs] > 0 && !ids) return set_error(MKV_ERR_INVALID_ARGUMENT, "NULL block ids");
-  int32_t mx = 0;
-  for (int32_t b = 0; b < num_seqs; b++) {
+  // Monotone over the whole array before any id is read: the ids array
+  // holds indptr[num_seqs] entries, and a later entry that falls back would
+  // otherwise let an earlier sequence's reads run past it.
+  for (int32_t b = 0; b < num_seqs; b++)
     if (indptr[b + 1] < indptr[b])
       return set_error(MKV_ERR_INVALID_ARGUMENT, "block_indptr not monotone at %d", b);
+  int32_t mx = 0;
+  for (int32_t b = 0; b < num_seqs; b++) {
     const int32_t n = lens[b];
     if (n < 1) return set_error(MKV_ERR_INVALID_ARGUMENT, "length[%d] = %d < 1", b, n);
     const uint32_t need = (uint32_t)((n + kPageSize - 1) / kPageSize);
@@ -681,9 +685,11 @@ extern "C" int mkv_validate_block_tables(const mkv_pool_desc *desc, const int32_
   if (rc) return rc;
   if (num_seqs < 0 || !indptr) return set_error(MKV_ERR_INVALID_ARGUMENT, "bad indptr");
   if (indptr[0] < 0) return set_error(MKV_ERR_INVALID_ARGUMENT, "indptr[0] < 0");
-  for (int32_t b = 0; b < num_seqs; b++) {
+  // The whole array first: ids holds indptr[num_seqs] entries.
+  for (int32_t b = 0; b < num_seqs; b++)
     if (indptr[b + 1] < indptr[b])
       return set_error(MKV_ERR_INVALID_ARGUMENT, "indptr not monotone at %d", b);
+  for (int32_t b = 0; b < num_seqs; b++) {
     for (int32_t i = indptr[b]; i < indptr[b + 1]; i++)
       if (!ids || ids[i] < 0 || ids[i] >= desc->num_blocks)
         return set_error(MKV_ERR_INVALID_ARGUMENT, "block id at %d (sequence %d) out of range", i, b);

@@ -69,6 +69,9 @@ def test_host_validators():
         validate_block_tables(d, [0, 1], [10], [5], 5)
     with pytest.raises(BackendError):  # context longer than max_ctx_len
         validate_block_tables(d, [0, 2], [1, 2], [20], 16)
+    with pytest.raises(BackendError) as ei:  # indptr falls back: refused before ids past the end are read
+        validate_block_tables(d, [0, 40, 2], [1, 2], [600, 20], 600)
+    assert "not monotone at 1" in str(ei.value)
     validate_copy_pairs(d, [1, 2], [3, 4])
     for src, dst in (([1, 2], [2, 3]), ([1, 2], [3, 3]), ([1], [10])):
         with pytest.raises(BackendError):

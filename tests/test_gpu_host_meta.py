@@ -229,6 +229,9 @@ def test_plan_with_host_tables_equals_device_tables(shape, kernel, pieces):
     ([0, 1], [1], [20], "cannot hold"),
     ([1, 2], [1, 2], [5], "block_indptr[0]"),
     ([0, 2], [1, 2], [0], "< 1"),
+    # An entry that falls back is refused before any id is read: sequence 0's
+    # 38 blocks would otherwise be read past the 2 ids given.
+    ([0, 40, 2], [1, 2], [600, 20], "not monotone at 1"),
 ])
 def test_plan_host_tables_rejected(ip, ids, ctx, msg):
     desc = PoolDesc(1, 4, 28, 128, 10, "bf16")
