@@ -446,6 +446,7 @@ int mkvh_page_table_remove_request(mkvh_page_table *pt, uint64_t req, uint32_t *
   auto lo = m.lower_bound({req, INT64_MIN}), hi = m.upper_bound({req, INT64_MAX});
   const int64_t n = std::distance(lo, hi);
   if (n > cap) return fail(MKVH_ERR_BUFFER_TOO_SMALL, "need room for %lld pages", (long long)n);
+  if (n && !out_pages) return fail(MKVH_ERR_INVALID_ARGUMENT, "NULL out_pages");
   int64_t i = 0;
   for (auto it = lo; it != hi; ++it) out_pages[i++] = it->second;
   m.erase(lo, hi);
@@ -472,6 +473,7 @@ int mkvh_radix_match_prefix(mkvh_radix *r, const uint32_t *tokens, int64_t n_tok
   const int64_t bound = n_tokens / x->page_size;
   if (pages_cap < bound || nodes_cap < bound)
     return fail(MKVH_ERR_BUFFER_TOO_SMALL, "capacities must be >= n_tokens / page_size = %lld", (long long)bound);
+  if (bound && (!out_pages || !out_nodes)) return fail(MKVH_ERR_INVALID_ARGUMENT, "NULL output arrays");
   size_t matched = 0;
   std::vector<uint32_t> pages;
   std::vector<size_t> nodes;
@@ -529,7 +531,7 @@ int mkvh_radix_promote_request(mkvh_radix *r, const uint32_t *input_ids, int64_t
   Radix *x = reinterpret_cast<Radix *>(r);
   const int64_t full = device_len / x->page_size;
   if (full == 0) return MKVH_OK;
-  if (device_len < 0 || n_input < full * x->page_size || n_pages < full)
+  if (device_len < 0 || n_input < full * x->page_size || n_pages < full || !input_ids || !kv_pages)
     return fail(MKVH_ERR_INVALID_ARGUMENT, "promote_request: input_ids or kv_pages shorter than device_len");
   std::vector<uint32_t> adopted;
   x->insert_prefix(input_ids, kv_pages, (size_t)full, x->evicted, adopted);
@@ -548,6 +550,10 @@ int64_t mkvh_radix_num_nodes(const mkvh_radix *r) {
 int mkvh_bm_create(int64_t num_blocks, int32_t page_size, int64_t max_cached_pages, mkvh_block_manager **out) {
   if (!out || num_blocks < 0 || num_blocks > UINT32_MAX || page_size < 1 || max_cached_pages < 0)
     return fail(MKVH_ERR_INVALID_ARGUMENT, "bad block manager arguments");
+  // Slots (block * page_size + offset) and the batch's block ids are int32.
+  if (num_blocks * (int64_t)page_size > INT32_MAX)
+    return fail(MKVH_ERR_INVALID_ARGUMENT, "%lld blocks of %d tokens: slots would not fit int32",
+                (long long)num_blocks, page_size);
   *out = reinterpret_cast<mkvh_block_manager *>(new (std::nothrow) BlockMgr(num_blocks, page_size, max_cached_pages));
   return *out ? MKVH_OK : fail(MKVH_ERR_EXHAUSTED, "host allocation failed");
 }

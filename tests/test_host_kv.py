@@ -190,6 +190,18 @@ def _tokens(seed, n):
     return np.random.default_rng(seed).integers(0, 50_000, n).astype(np.uint32)
 
 
+def test_block_manager_refuses_pools_whose_slots_overflow_int32():
+    """Slots are block * page_size + offset in int32 (the device pool's slot
+    type): 2^27 blocks of 16 tokens, or 2^20 of 2,048, would wrap them."""
+    from mitten_amd.host import INVALID_ARGUMENT, HostError
+
+    BlockManager(2**20 - 1, 2048, max_cached_pages=0).close()
+    for n, ps in ((2**27, 16), (2**20, 2048)):
+        with pytest.raises(HostError) as ei:
+            BlockManager(n, ps)
+        assert ei.value.status == INVALID_ARGUMENT and "int32" in str(ei.value)
+
+
 def test_admit_allocates_ceil_pages_and_decode_grows():
     bm = BlockManager(64, 16)
     assert bm.admit(1, _tokens(0, 40)) == 0
