@@ -18,7 +18,9 @@
 
 use crate::host::{CopyQueue, PagedLifecycle, PoolView};
 use crate::pool::{DeviceKvPool, KvDtype, PoolGeometry, Stream, Tables, PAGE_SIZE};
-use inference_backend::{BackendHandle, Batch, BoxFuture, EngineError, KvPool, Logits, ModelConfig, RequestState};
+// BoxFuture is not re-exported at the crate root (inference-backend/src/lib.rs:10).
+use inference_backend::backend::BoxFuture;
+use inference_backend::{BackendHandle, Batch, EngineError, KvPool, Logits, ModelConfig, RequestState};
 use mitten_kv_sys as sys;
 use parking_lot::Mutex;
 use std::ffi::c_void;
