@@ -222,7 +222,12 @@ copy_blocks_kernel(uint8_t *__restrict__ pool, const int32_t *__restrict__ src,
 int meta_acquire(Pool *p, size_t n, hipStream_t hs, MetaSlot **out) {
   MetaSlot *sl = &p->meta[p->meta_next];
   p->meta_next = (p->meta_next + 1) % kMetaSlots;
-  if (!sl->done) MKV_CHECK_HIP(hipEventCreateWithFlags(&sl->done, hipEventDisableTiming));
+  // The slot's event only tells the host that the launches reading the
+  // slot are done (the device never writes it), so it skips the
+  // system-scope cache fence: recorded after every host-form call, a fenced
+  // event held the next launch back by about 4.6 us.
+  if (!sl->done)
+    MKV_CHECK_HIP(hipEventCreateWithFlags(&sl->done, hipEventDisableTiming | hipEventDisableSystemFence));
   if (sl->pending) {  // the launches that read this slot last time are done
     MKV_CHECK_HIP(hipEventSynchronize(sl->done));
     sl->pending = false;
