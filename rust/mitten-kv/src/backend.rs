@@ -17,7 +17,7 @@
 //! MLP) belongs to the model; the model crates expose it through [`PagedModel`].
 
 use crate::host::{CopyQueue, PagedLifecycle, PoolView};
-use crate::pool::{DeviceKvPool, KvDtype, PoolGeometry, Stream, Tables, PAGE_SIZE};
+use crate::pool::{DeviceKvPool, KvDtype, PoolGeometry, SharedPrefix, Stream, Tables, PAGE_SIZE};
 // BoxFuture is not re-exported at the crate root (inference-backend/src/lib.rs:10).
 use inference_backend::backend::BoxFuture;
 use inference_backend::{BackendHandle, Batch, EngineError, KvPool, Logits, ModelConfig, RequestState};
@@ -155,7 +155,13 @@ pub struct PagedBackend<M: PagedModel> {
     copies: CopyQueue,
     scale: f32,
     flags: u32,
+    shared_prefix_min_bytes: u64,
 }
+
+/// K/V bytes per layer a shared prefix must save (its blocks read once
+/// instead of once per sequence) before a step takes the shared-prefix form,
+/// whose prefix tiles and merge cost about two extra launches per layer.
+pub const SHARED_PREFIX_MIN_BYTES: u64 = 128 << 20;
 
 impl<M: PagedModel> PagedBackend<M> {
     /// A pool on `device` for `model` with as many blocks as the scheduler's
@@ -173,7 +179,28 @@ impl<M: PagedModel> PagedBackend<M> {
             config,
             view: lifecycle.pool_view(),
             copies: lifecycle.copy_queue(),
+            shared_prefix_min_bytes: SHARED_PREFIX_MIN_BYTES,
         })
+    }
+
+    /// Bytes per layer a shared prefix must save before a step reads it
+    /// once for all its decode requests (`u64::MAX`: never).
+    pub fn with_shared_prefix_min_bytes(mut self, bytes: u64) -> Self {
+        self.shared_prefix_min_bytes = bytes;
+        self
+    }
+
+    /// The step's decode tables split at a prefix every request shares, when
+    /// the geometry takes the shared-prefix step and the prefix saves enough.
+    fn shared_prefix(&self, geom: &PoolGeometry, step: &StepLayout) -> Option<SharedPrefix> {
+        let b = step.decode_ctx.len();
+        if b < 2 || !geom.shared_prefix_supported() {
+            return None;
+        }
+        let split = SharedPrefix::split(&step.decode_tables, &step.decode_ctx)?;
+        let block_bytes = (2 * PAGE_SIZE * geom.kv_row_bytes()) as u64;
+        let saved = (b as u64 - 1) * split.prefix.len() as u64 * block_bytes;
+        (saved >= self.shared_prefix_min_bytes).then_some(split)
     }
 
     fn forward_now(&self, batch: &Batch) -> Result<Logits, EngineError> {
@@ -190,11 +217,19 @@ impl<M: PagedModel> PagedBackend<M> {
                 None => break,
             }
         }
-        if !step.decode_ctx.is_empty() {
-            inner.pool.begin_step(&step.decode_tables, &step.decode_ctx, stream)?;
+        let geom = *inner.pool.geometry();
+        // Decode requests that share a radix prefix read its blocks once for
+        // all of them (mkv_decode_step_shared_prefix); otherwise one plan of
+        // their whole tables.
+        let shared = self.shared_prefix(&geom, &step);
+        match &shared {
+            Some(split) => inner.pool.begin_shared_prefix_step(split, stream)?,
+            None if !step.decode_ctx.is_empty() => {
+                inner.pool.begin_step(&step.decode_tables, &step.decode_ctx, stream)?
+            }
+            None => {}
         }
         inner.model.begin(&batch.input_ids, &batch.position_ids, stream)?;
-        let geom = *inner.pool.geometry();
         let (kv_off, q_off) = (step.prefill_rows * geom.kv_row_bytes(), step.prefill_rows * geom.q_row_bytes());
         for layer in 0..geom.num_layers {
             let io = inner.model.attention_io(layer, stream)?;
@@ -209,8 +244,12 @@ impl<M: PagedModel> PagedBackend<M> {
                 if !step.decode_ctx.is_empty() {
                     let at = |p: *const c_void, off: usize| p.cast::<u8>().wrapping_add(off).cast::<c_void>();
                     let o = io.o.cast::<u8>().wrapping_add(q_off).cast::<c_void>();
-                    inner.pool.decode_step(layer, at(io.k, kv_off), at(io.v, kv_off), at(io.q, q_off), o,
-                                           self.scale, self.flags, stream)?;
+                    let (k, v, q) = (at(io.k, kv_off), at(io.v, kv_off), at(io.q, q_off));
+                    if shared.is_some() {
+                        inner.pool.decode_step_shared_prefix(layer, k, v, q, o, self.scale, self.flags, stream)?;
+                    } else {
+                        inner.pool.decode_step(layer, k, v, q, o, self.scale, self.flags, stream)?;
+                    }
                 }
             }
             inner.model.finish_layer(layer, stream)?;

@@ -26,9 +26,9 @@ mod error;
 mod host;
 mod pool;
 
-pub use backend::{AttentionIo, PagedBackend, PagedModel, StepLayout};
+pub use backend::{AttentionIo, PagedBackend, PagedModel, StepLayout, SHARED_PREFIX_MIN_BYTES};
 pub use error::check;
 pub use host::{
     schedule_prefill_chunks, Appended, CopyQueue, HostBlockManager, PagedLifecycle, PoolView, PrefillSchedule,
 };
-pub use pool::{DeviceKvPool, KvDtype, PoolGeometry, Stream, Tables, PAGE_SIZE};
+pub use pool::{DeviceKvPool, KvDtype, PoolGeometry, SharedPrefix, Stream, Tables, PAGE_SIZE};

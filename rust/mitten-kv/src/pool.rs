@@ -102,6 +102,15 @@ impl PoolGeometry {
     pub fn q_row_bytes(&self) -> usize {
         self.num_q_heads * self.head_dim * self.dtype.bytes()
     }
+
+    /// Whether `mkv_decode_step_shared_prefix` takes this geometry: bf16 KV
+    /// on the MFMA kernels (head_dim 64, 128 or 256, at most 16 query heads
+    /// per KV head).
+    pub fn shared_prefix_supported(&self) -> bool {
+        self.dtype == KvDtype::Bf16
+            && matches!(self.head_dim, 64 | 128 | 256)
+            && self.num_q_heads <= 16 * self.num_kv_heads
+    }
 }
 
 /// Page tables in the C ABI's CSR form (`Batch.page_table`, `batch.rs:24-26`,
@@ -125,6 +134,50 @@ impl Tables {
     }
     pub fn is_empty(&self) -> bool {
         self.len() == 0
+    }
+    /// Table `b`.
+    pub fn table(&self, b: usize) -> &[u32] {
+        &self.ids[self.indptr[b] as usize..self.indptr[b + 1] as usize]
+    }
+}
+
+/// A decode step's tables split at the leading block ids every table holds
+/// (the pages radix sharing handed to every request that matched a prefix,
+/// `inference-engine/src/radix_cache.rs:64-117`), limited to blocks that are
+/// full before each sequence's last token.
+#[derive(Clone, Debug, Default)]
+pub struct SharedPrefix {
+    /// The shared blocks, in order.
+    pub prefix: Vec<u32>,
+    /// Each sequence's blocks past the prefix.
+    pub suffix_tables: Tables,
+    /// Tokens past the prefix (the appended one included), per sequence.
+    pub suffix_lens: Vec<i32>,
+}
+
+impl SharedPrefix {
+    /// `None` when the tables share no leading block.
+    pub fn split(tables: &Tables, ctx_lens: &[i32]) -> Option<Self> {
+        let b = ctx_lens.len();
+        if b == 0 || tables.len() != b {
+            return None;
+        }
+        let mut limit = usize::MAX;
+        for (i, &ctx) in ctx_lens.iter().enumerate() {
+            let full_before_last = ((ctx.max(1) - 1) as usize) / PAGE_SIZE;
+            limit = limit.min(full_before_last).min(tables.table(i).len());
+        }
+        let first = tables.table(0);
+        let n = (0..limit).take_while(|&j| (1..b).all(|i| tables.table(i)[j] == first[j])).count();
+        if n == 0 {
+            return None;
+        }
+        let mut suffix_tables = Tables::new();
+        for i in 0..b {
+            suffix_tables.push(&tables.table(i)[n..]);
+        }
+        let suffix_lens = ctx_lens.iter().map(|&c| c - (n * PAGE_SIZE) as i32).collect();
+        Some(Self { prefix: first[..n].to_vec(), suffix_tables, suffix_lens })
     }
 }
 
@@ -194,6 +247,38 @@ impl DeviceKvPool {
                 stream,
             )
         })
+    }
+
+    /// Once per engine step whose decode requests share a prefix: the
+    /// plan of `mkv_decode_step_shared_prefix` (the prefix's blocks read once
+    /// for every sequence). Validated and copied before the call returns.
+    pub fn begin_shared_prefix_step(&mut self, split: &SharedPrefix, stream: Stream) -> Result<(), EngineError> {
+        check(unsafe {
+            sys::mkv_decode_plan_build_shared_prefix(
+                self.plan,
+                split.prefix.as_ptr(),
+                split.prefix.len() as i32,
+                split.suffix_lens.as_ptr(),
+                split.suffix_tables.indptr.as_ptr(),
+                split.suffix_tables.ids.as_ptr(),
+                split.suffix_lens.len() as i32,
+                0,
+                stream,
+            )
+        })
+    }
+
+    /// One layer of a step planned by `begin_shared_prefix_step`: the same
+    /// result as `decode_step` over the whole tables.
+    ///
+    /// # Safety
+    /// As for `decode_step`.
+    #[allow(clippy::too_many_arguments)]
+    pub unsafe fn decode_step_shared_prefix(&mut self, layer: usize, k_new: *const c_void, v_new: *const c_void,
+                                            q: *const c_void, o: *mut c_void, scale: f32, flags: u32,
+                                            stream: Stream) -> Result<(), EngineError> {
+        check(sys::mkv_decode_step_shared_prefix(self.raw, self.plan, layer as i32, k_new, v_new, q, o, ptr::null(),
+                                                 0, ptr::null(), ptr::null(), scale, flags, stream))
     }
 
     /// One layer of the decode step (`inference-model-qwen/src/model.rs:390-416`):
