@@ -211,8 +211,8 @@ impl DeviceKvPool {
     }
 
     /// The library handle, for the entry points this type does not wrap
-    /// (fused prep, wire export/import, the shared-prefix step). The pool
-    /// keeps ownership.
+    /// (wire export/import, gathers, device-table forms). The pool keeps
+    /// ownership.
     pub fn as_raw(&self) -> *mut sys::mkv_pool {
         self.raw
     }
@@ -323,6 +323,32 @@ impl DeviceKvPool {
         check(sys::mkv_extend_attention_host(self.raw, layer as i32, q, o, q_lens.as_ptr(), ctx_lens.as_ptr(),
                                              tables.indptr.as_ptr(), tables.ids.as_ptr(), q_lens.len() as i32,
                                              scale, flags, stream))
+    }
+
+    /// The fused step before attention (`inference-model-qwen/src/model.rs:371-392`):
+    /// RMSNorm(1 + w) of every q and k head (`model.rs:104-108`), NeoX RoPE
+    /// on their first `rotary_dim` dims at `positions` (`inv_freq` holds
+    /// `rotary_dim / 2` frequencies), k and v appended at `slots`; the
+    /// prepared q goes to `q_out` `[n][Hq][D]`. `q` is the gated q_proj
+    /// output `[n][Hq][2][D]` unless `flags` has `MKV_PREP_PLAIN_Q`. The
+    /// positions and slots are validated and copied before the call returns.
+    ///
+    /// # Safety
+    /// `q`, `k`, `v`, `q_out` are device buffers of the pool's dtype; the
+    /// weights and frequencies are f32 device buffers (the weights may be
+    /// null with `MKV_PREP_NO_NORM`).
+    #[allow(clippy::too_many_arguments)]
+    pub unsafe fn norm_rope_append_host(&mut self, layer: usize, q: *const c_void, k: *const c_void,
+                                        v: *const c_void, q_norm_w: *const f32, k_norm_w: *const f32,
+                                        inv_freq: *const f32, rotary_dim: usize, eps: f32, positions: &[i32],
+                                        slots: &[u32], q_out: *mut c_void, flags: u32,
+                                        stream: Stream) -> Result<(), EngineError> {
+        if positions.len() != slots.len() {
+            return Err(EngineError::Backend("positions and slots differ in length".into()));
+        }
+        check(sys::mkv_qk_norm_rope_append_host(self.raw, layer as i32, q, k, v, q_norm_w, k_norm_w, inv_freq,
+                                                rotary_dim as i32, eps, positions.as_ptr(), slots.as_ptr(),
+                                                slots.len() as i32, q_out, flags, stream))
     }
 
     /// Copy-on-write copies or compaction moves, every layer, K and V. The
