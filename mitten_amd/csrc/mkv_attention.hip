@@ -58,6 +58,7 @@ constexpr int kRing = 3;       // MFMA loop: blocks loaded ahead + 1
 constexpr int kBlockWeight = 8;    // plan: weight of one block in a piece ...
 constexpr int kSwitchWeight = 12;  // ... and of a sequence start inside it (about 1.5 blocks)
 constexpr int kFirstRoundWeight = 116;  // plan: cap of the first-dispatched pieces, percent
+constexpr int kOddXcdWeight = 96;       // plan: cap of pieces dealt to odd-numbered XCDs, percent
 constexpr int kCoopRing = 3;   // register stages of the cooperative kernel (one less when
                                // its slots carry four Q loads per lane, or at head_dim 256,
                                // where three stages spilled registers)
@@ -2284,6 +2285,14 @@ static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t 
   // workgroup of their CU.
   const int64_t first = (!pieces && resident > 0 && device_cus(pl->pool) > 0 &&
                          resident == 2 * (int64_t)device_cus(pl->pool)) ? device_cus(pl->pool) : 0;
+  // Workgroup L runs on XCD L mod 8, and in a launch of one round of
+  // resident pieces the odd-numbered XCDs finish last: per-workgroup stamps
+  // on every box measured put their last workgroups about 5 us (6%) after
+  // the even XCDs'. Pieces with an odd index, dealt to those XCDs, get
+  // kOddXcdWeight percent of the cap (C2 72.7 -> 73.4% of peak, Gemma-2B
+  // MQA 72.3 -> 73.3%). Launches of several rounds, whose freed slots take
+  // the next piece whatever its XCD, keep equal caps.
+  const bool odd_light = !pieces && resident > 0 && P == resident;
   auto cut = [&](int64_t cap) {
     f0s.clear();
     int64_t w = 0;
@@ -2293,7 +2302,9 @@ static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t 
     for (int64_t f = 0; f < total; f++) {
       while (blk0v[b + 1] <= f) b++;
       int64_t wi = kBlockWeight + ((f == blk0v[b] && cnt > 0) ? kSwitchWeight : 0);
-      const int64_t cq = (int64_t)f0s.size() - 1 < first ? cap_first : cap;
+      const int64_t idx = (int64_t)f0s.size() - 1;  // the piece being filled
+      const int64_t cq0 = idx < first ? cap_first : cap;
+      const int64_t cq = odd_light && (idx & 1) ? cq0 * kOddXcdWeight / 100 : cq0;
       if (cnt > 0 && (cnt == 64 || w + wi > cq)) {
         cnt = 0;
         w = 0;
