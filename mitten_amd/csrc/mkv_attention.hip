@@ -973,6 +973,99 @@ __global__ void __launch_bounds__(256) attn_planned_kernel(KArgs a, PlanDev pd) 
   }
 }
 
+// A latency-bound step on the per-head kernel (few blocks for the device:
+// the plan's small query chunks) without split-K partials: one workgroup of
+// kSeqWaves waves per (sequence, KV head, query chunk); wave w takes the
+// w-th contiguous share of the sequence's blocks, and the waves' softmax
+// states merge through LDS into the final rows. No merge launch follows.
+// 16 waves for f32 pools; 8 for bf16, whose per-lane state and loads need
+// more than the 128 registers of a 16-wave workgroup.
+constexpr int seq_waves(bool bf16) { return bf16 ? 8 : 16; }
+
+template <int D, bool BF16, bool MFMA, int QC>
+__global__ void __launch_bounds__(64 * seq_waves(BF16)) attn_seq_kernel(KArgs a, PlanDev pd) {
+  static_assert(!MFMA, "per-head path only");
+  using T = VTraits<D, BF16>;
+  constexpr int ES = T::ES, VEC = T::VEC, LPT = T::LPT;
+  constexpr int kSeqWaves = seq_waves(BF16);
+  __shared__ float part[kSeqWaves][QC][2 + D];  // per wave and query head: m, l, unnormalised row
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int b = blockIdx.x;
+  Seg sg;
+  sg.b = b;
+  sg.h = (int)blockIdx.y / a.nqc;
+  sg.qc = (int)blockIdx.y % a.nqc;
+  sg.ctx = pd.ctx[b];
+  const int sb = pd.seq_blk0[b], nb = pd.seq_blk0[b + 1] - sb;
+  const int tab0 = a.indptr[b];
+  if (tab0 < 0 || a.indptr[b + 1] - tab0 < nb) {  // uniform over the workgroup
+    if (threadIdx.x == 0 && sg.qc == 0) record_error(a.d_err, MKV_DEVERR_TABLE);
+    return;
+  }
+  sg.table = a.ids + tab0;
+  sg.j0 = (int)((int64_t)nb * wave / kSeqWaves);
+  sg.j1 = (int)((int64_t)nb * (wave + 1) / kSeqWaves);
+  sg.nk = sg.nv = nullptr;
+  if (a.new_k && sg.j0 < sg.j1 && sg.j1 == nb) {
+    // This wave holds the sequence's last block: the step's new row.
+    const int32_t blk = sg.table[nb - 1];
+    if (blk < 0 || blk >= a.nblocks) {
+      if (lane == 0) record_error(a.d_err, MKV_DEVERR_BLOCK);
+    } else {
+      const int64_t src = ((int64_t)b * a.Hkv + sg.h) * D * ES;
+      sg.nk = a.new_k + src;
+      sg.nv = a.new_v + src;
+      if (sg.qc == 0) store_new_row<D, ES>(a, lane, b, sg.h, blk, (sg.ctx - 1) % kPageSize);
+    }
+  }
+  if (a.gk) sg.gtok = a.gtok0[b];
+  VState<D, BF16, QC> st;
+  valu_segment<D, BF16, QC>(a, sg, lane, st);  // an empty share leaves m = -inf, l = 0, row 0
+  const int q0 = sg.qc * QC;
+  const int nq = min(QC, a.G - q0);
+  if (lane < LPT) {
+#pragma unroll
+    for (int g = 0; g < QC; g++) {
+      if (g >= nq) break;
+      part[wave][g][0] = st.m[g];
+      part[wave][g][1] = st.l[g];
+#pragma unroll
+      for (int e = 0; e < VEC; e++) part[wave][g][2 + lane * VEC + e] = st.acc[g][e];
+    }
+  }
+  __syncthreads();
+  // Wave g merges query head q0 + g: lane ld the dims ld*VEC .. +VEC.
+  if (wave >= nq || lane >= LPT) return;
+  const int g = wave;
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kSeqWaves; w++) M = fmaxf(M, part[w][g][0]);
+  float L = 0.0f, acc[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; e++) acc[e] = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kSeqWaves; w++) {
+    const float mw = part[w][g][0];
+    const float f = mw == -INFINITY ? 0.0f : fast_exp2(mw - M);
+    L = fmaf(part[w][g][1], f, L);
+#pragma unroll
+    for (int e = 0; e < VEC; e++) acc[e] = fmaf(part[w][g][2 + lane * VEC + e], f, acc[e]);
+  }
+  const float f = final_scale(M, L, a.zero_sink);
+  const int hq = sg.h * a.G + q0 + g;
+  uint8_t *op = reinterpret_cast<uint8_t *>(a.o) + ((int64_t)(b * a.Hq + hq) * D + lane * VEC) * ES;
+  u32x4 wv;
+  if constexpr (BF16) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) wv[e] = pack_bf16x2(acc[2 * e] * f, acc[2 * e + 1] * f);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; e++) wv[e] = __float_as_uint(acc[e] * f);
+  }
+  *reinterpret_cast<u32x4 *>(op) = wv;
+}
+
 // ---- LDS-fed MFMA block (cooperative kernel) -------------------------------
 //
 // Same online-softmax step as mfma_block, but V^T comes straight from the
@@ -2574,6 +2667,7 @@ static int launch_planned(Pool *p, const Plan *pl, int32_t layer, const void *d_
   hipEvent_t ev_start = p->ev_start, ev_end = p->ev_end;
   p->ev_start = p->ev_end = nullptr;
   if (ev_start) MKV_CHECK_HIP(hipEventRecord(ev_start, hs));
+  bool merged = false;  // the attention kernel wrote the final rows of every sequence
   if (use_mfma) {
     // Cooperative kernel: Q rows of one sequence (Hq * D * 2 bytes) must fit
     // the QL loads per lane its ring slots carry.
@@ -2621,6 +2715,13 @@ static int launch_planned(Pool *p, const Plan *pl, int32_t layer, const void *d_
       }
       MKV_CHECK_LAUNCH("attn_stream_kernel");
     }
+  } else if (small_qc && merge && !pl->all_partial) {
+    // Latency-bound: one workgroup per (sequence, KV head, query chunk),
+    // the waves' states merged in LDS; no partials, no merge launch.
+    const dim3 sgrid((unsigned)pl->B, (unsigned)(g.Hkv * a.nqc)), sblock(64 * seq_waves(g.dtype == MKV_DTYPE_BF16));
+    MKV_DISPATCH_VALU_QC(attn_seq_kernel, kQChunkValuSmall, sgrid, sblock, hs, a, pd);
+    MKV_CHECK_LAUNCH("attn_seq_kernel");
+    merged = true;
   } else if (small_qc) {
     MKV_DISPATCH_VALU_QC(attn_planned_kernel, kQChunkValuSmall, grid, block, hs, a, pd);
     MKV_CHECK_LAUNCH("attn_planned_kernel");
@@ -2629,7 +2730,7 @@ static int launch_planned(Pool *p, const Plan *pl, int32_t layer, const void *d_
     MKV_CHECK_LAUNCH("attn_planned_kernel");
   }
   if (ev_end) MKV_CHECK_HIP(hipEventRecord(ev_end, hs));
-  if (pl->n_merge && merge) {
+  if (pl->n_merge && merge && !merged) {
     const int64_t mwgs = ((int64_t)pl->n_merge * g.Hq + 3) / 4;
     MKV_DISPATCH_MERGE(merge_planned_kernel, dim3((unsigned)mwgs), dim3(256), hs, a, pd);
     MKV_CHECK_LAUNCH("merge_planned_kernel");
