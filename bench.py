@@ -134,7 +134,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=8.0,
                     help="about how long the CPU baseline's one-thread sample runs, per configuration")
     ap.add_argument("--op", choices=["decode", "prep", "wire", "gather", "copy", "append", "extend", "shared",
-                                     "pressure"],
+                                     "pressure", "small"],
                     default="decode",
                     help="decode: the decode step (headline); prep: the fused q/k-norm + RoPE + "
                          "append kernel on a prefill chunk; wire: KV block export + import of a "
@@ -143,7 +143,8 @@ def parse():
                          "prefill attention of --extend-seqs chunks of --tokens-per-chunk after "
                          "--prefix tokens; shared: decode step of 256 sequences over a radix-shared "
                          "prefix, with its copy-on-write copies and compaction moves; pressure: "
-                         "chunk appends + decode step over a 200 GB pool")
+                         "chunk appends + decode step over a 200 GB pool; small: latency-bound decode "
+                         "steps of 1-8 sequences at Qwen2.5-7B heads")
     ap.add_argument("--extend-seqs", type=int, default=8, help="--op extend: sequences")
     ap.add_argument("--tokens-per-chunk", type=int, default=512, help="--op extend: chunk length")
     ap.add_argument("--prefix", type=int, default=4096, help="--op extend: cached tokens before the chunk")
@@ -1338,6 +1339,66 @@ def _nested(r: dict) -> dict:
     return {k: r[k] for k in keep if k in r}
 
 
+SMALL_BATCHES = [[4096], [8192], [4096] * 4, [2048] * 8, [8192] * 4]
+
+
+def bench_small(args):
+    """Decode steps of batches too small to fill the device (1-8 sequences
+    at Qwen2.5-7B heads, bf16): the fused append + attention per layer from a
+    plan holding the host tables, as in the headline step. Latency-bound, so
+    the figure is microseconds per layer; each batch also reports its K/V
+    bytes at that time."""
+    import torch
+
+    from mitten_amd import DeviceKvPool, PoolDesc
+    from mitten_amd import workloads as wl
+
+    cfg = wl.CONFIGS["qwen2.5-7b"]
+    L, Hq, Hkv, D = 4, cfg["num_q_heads"], cfg["num_kv_heads"], cfg["head_dim"]
+    dev = torch.device("cuda:0")
+    rows = []
+    for ctxs in SMALL_BATCHES:
+        batch = wl.decode_batch_from_contexts([c - 1 for c in ctxs], wl.SplitMix64(wl.BASE_SEED + 31),
+                                              extra_blocks=2)
+        desc = PoolDesc(L, Hkv, Hq, D, batch.num_blocks, "bf16")
+        B = len(ctxs)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(wl.BASE_SEED + 31)
+        q = torch.randn((B, Hq, D), generator=gen, device=dev).to(torch.bfloat16)
+        kn = torch.randn((B, Hkv, D), generator=gen, device=dev).to(torch.bfloat16)
+        vn = torch.randn((B, Hkv, D), generator=gen, device=dev).to(torch.bfloat16)
+        out = torch.empty_like(q)
+        ip = np.ascontiguousarray(batch.block_indptr, np.uint32)
+        ids = np.ascontiguousarray(batch.block_ids, np.uint32)
+        with DeviceKvPool(desc) as pool:
+            plan = pool.plan(batch.ctx_lens, block_indptr=ip, block_ids=ids)
+            info = plan.info()
+            for _ in range(args.warmup):
+                for layer in range(L):
+                    pool.decode_step(layer, plan, kn, vn, q, None, None, out=out)
+            torch.cuda.synchronize()
+            n = max(args.steps, 1) * 5
+            t0 = time.perf_counter()
+            for _ in range(n):
+                for layer in range(L):
+                    pool.decode_step(layer, plan, kn, vn, q, None, None, out=out)
+            torch.cuda.synchronize()
+            us = (time.perf_counter() - t0) / (n * L) * 1e6
+            pool.check()
+            plan.close()
+        kv = int(np.sum(batch.ctx_lens)) * desc.num_kv_heads * desc.head_dim * desc.elem_bytes * 2
+        rows.append({"sequences": B, "context": ctxs[0], "plan": info, "us_per_layer": round(us, 2),
+                     "kv_bytes_per_layer": kv, "kv_gbs": round(kv / us / 1e3, 1)})
+    print(json.dumps({
+        "metric": "latency-bound decode step: microseconds per layer", "unit": "us", "higher_is_better": False,
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "dtype": "bf16",
+        "data": "synthetic: N(0,1) K/V from a seed in the pool (uninitialised blocks), q and new rows from a seed",
+        "config": {"workload": "decode step (fused append + paged attention + merge) of 1-8 sequences, "
+                               "Qwen2.5-7B heads", "layers_timed": 4, "q_heads": Hq, "kv_heads": Hkv,
+                   "head_dim": D},
+        "batches": rows}), flush=True)
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -1366,6 +1427,9 @@ def main():
     if args.op == "pressure":
         print(json.dumps(bench_pressure(args.steps, args.warmup, cpu=not args.no_cpu_baseline,
                                         cpu_seconds=args.cpu_seconds)), flush=True)
+        return
+    if args.op == "small":
+        bench_small(args)
         return
     from mitten_amd import workloads as wl
 

@@ -59,6 +59,7 @@ constexpr int kBlockWeight = 8;    // plan: weight of one block in a piece ...
 constexpr int kSwitchWeight = 12;  // ... and of a sequence start inside it (about 1.5 blocks)
 constexpr int kFirstRoundWeight = 116;  // plan: cap of the first-dispatched pieces, percent
 constexpr int kOddXcdWeight = 96;       // plan: cap of pieces dealt to odd-numbered XCDs, percent
+constexpr int kMinPieceBlocks = 8;      // plan: fewest blocks per piece of a cooperative plan
 constexpr int kCoopRing = 3;   // register stages of the cooperative kernel (one less when
                                // its slots carry four Q loads per lane, or at head_dim 256,
                                // where three stages spilled registers)
@@ -2354,6 +2355,11 @@ static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t 
   const bool beside = !pieces && all_partial && prefix_beside(pl->pool);
   const int64_t resident = pieces ? 0 : beside ? device_cus(pl->pool) : coop_resident(pl->pool);
   int64_t P = pieces ? pieces : resident ? resident : std::max<int64_t>(1, 2048 / std::max(1, g.Hkv * nqc));
+  // A batch too small to fill the resident workgroups with long pieces is
+  // latency-bound: pieces of one or two blocks would only add partials for
+  // the merge to read back (up to hundreds per sequence, 16 per round).
+  // Cooperative plans keep at least kMinPieceBlocks blocks per piece there.
+  if (!pieces && resident > 0) P = std::min<int64_t>(P, std::max<int64_t>(1, (total + kMinPieceBlocks - 1) / kMinPieceBlocks));
   P = std::max<int64_t>(P, (total + 63) / 64);  // a piece is at most 64 blocks (one per lane)
   P = std::min<int64_t>(P, total);
   std::vector<int32_t> blk0v(num_seqs + 1);
