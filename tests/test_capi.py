@@ -40,6 +40,12 @@ def test_python_bindings_cover_the_header():
     assert set(_declared("mitten_kv_host.h", "mkvh")) == set(_host_sigs.HOST_SIGNATURES)
 
 
+def test_version_through_the_abi():
+    from mitten_amd import _lib
+
+    assert _lib.device_lib().mkv_version() == 100  # 0.1.0 as MAJOR*10000 + MINOR*100 + PATCH
+
+
 def test_required_bytes_reference_kat_through_the_abi():
     # kv_pool.rs:130-136
     assert required_bytes(PoolDesc(28, 4, 28, 128, 512, "bf16")) == 469_762_048

@@ -576,3 +576,42 @@ def test_decode_step_gather_rejects_small_outputs():
         with pytest.raises(BackendError):
             pool.decode_step(0, plan, z, z, q, _i32([0, 2, 4]), _i32([0, 1, 2, 3]), gather_out=(small, small))
         plan.close()
+
+
+def test_device_buffers_and_pool_descriptor_through_the_abi():
+    """The backend's device-buffer entry points (mkv_buffer_alloc / free,
+    memcpy both ways) round-trip bytes; mkv_pool_get_desc returns the
+    descriptor the pool was made from and mkv_pool_buffer its size; NULL
+    outputs and a device that does not exist are refused with a status."""
+    import ctypes
+
+    from mitten_amd import _lib, required_bytes
+
+    lib = _lib.device_lib()
+    n = 3 * 4096 + 48
+    src = np.random.default_rng(41).integers(0, 256, n, dtype=np.uint8)
+    back = np.zeros(n, np.uint8)
+    ptr = ctypes.c_void_p()
+    assert lib.mkv_buffer_alloc(0, n, ctypes.byref(ptr)) == 0 and ptr.value
+    try:
+        assert lib.mkv_memcpy_h2d(ptr, src.ctypes.data_as(ctypes.c_void_p), n, None) == 0
+        assert lib.mkv_memcpy_d2h(back.ctypes.data_as(ctypes.c_void_p), ptr, n, None) == 0
+        assert np.array_equal(back, src)
+    finally:
+        assert lib.mkv_buffer_free(ptr) == 0
+    assert lib.mkv_buffer_free(None) == 0
+    assert lib.mkv_buffer_alloc(0, 16, None) == dp.MKV_ERR_INVALID_ARGUMENT
+    bad = ctypes.c_void_p()
+    assert lib.mkv_buffer_alloc(4096, 16, ctypes.byref(bad)) == dp.MKV_ERR_NO_DEVICE and not bad.value
+
+    desc = PoolDesc(3, 4, 28, 128, 37, "bf16")
+    with DeviceKvPool(desc) as pool:
+        got = _lib.PoolDescC()
+        assert lib.mkv_pool_get_desc(pool._h, ctypes.byref(got)) == 0
+        want = desc.c()
+        assert [getattr(got, f) for f, _ in got._fields_] == [getattr(want, f) for f, _ in want._fields_]
+        assert lib.mkv_pool_get_desc(pool._h, None) == dp.MKV_ERR_INVALID_ARGUMENT
+        size = ctypes.c_uint64()
+        base = ctypes.c_void_p()
+        assert lib.mkv_pool_buffer(pool._h, ctypes.byref(base), ctypes.byref(size)) == 0
+        assert size.value == required_bytes(desc) and base.value == pool.data_ptr
