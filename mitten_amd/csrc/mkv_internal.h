@@ -117,6 +117,7 @@ struct DeviceGuard {
   explicit DeviceGuard(int dev) {
     if (hipGetDevice(&prev) != hipSuccess) prev = -1;
     if (prev != dev) ok = hipSetDevice(dev) == hipSuccess;
+    if (!ok) (void)hipGetLastError();  // reported by the caller's status, not left for the next HIP check
   }
   ~DeviceGuard() {
     int cur = -1;

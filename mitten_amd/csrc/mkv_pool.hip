@@ -29,6 +29,10 @@ int set_error(int code, const char *fmt, ...) {
 }
 
 int hip_fail(hipError_t e, const char *what) {
+  // The failure is the call's status: clear the thread's last HIP error so
+  // that the caller's own next error check (torch's, after its next launch)
+  // does not report it a second time.
+  (void)hipGetLastError();
   int code = (e == hipErrorOutOfMemory) ? MKV_ERR_OUT_OF_MEMORY : MKV_ERR_HIP;
   return set_error(code, "%s failed: %s (%d)", what, hipGetErrorString(e), (int)e);
 }
@@ -339,8 +343,10 @@ extern "C" int mkv_pool_create(const mkv_pool_desc *desc, int device, mkv_pool *
   if (!out_pool) return set_error(MKV_ERR_INVALID_ARGUMENT, "out_pool is NULL");
   *out_pool = nullptr;
   int ndev = 0;
-  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0)
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0) {
+    (void)hipGetLastError();
     return set_error(MKV_ERR_NO_DEVICE, "no HIP device available");
+  }
   if (device < 0 || device >= ndev)
     return set_error(MKV_ERR_INVALID_ARGUMENT, "device %d out of range (%d devices)", device, ndev);
   DeviceGuard guard(device);
@@ -737,6 +743,13 @@ extern "C" int mkv_validate_copy_pairs(const mkv_pool_desc *desc, const int32_t 
 extern "C" int mkv_buffer_alloc(int device, uint64_t bytes, void **out_dev_ptr) {
   if (!out_dev_ptr) return set_error(MKV_ERR_INVALID_ARGUMENT, "out pointer is NULL");
   *out_dev_ptr = nullptr;
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0) {
+    (void)hipGetLastError();
+    return set_error(MKV_ERR_NO_DEVICE, "no HIP device available");
+  }
+  if (device < 0 || device >= ndev)
+    return set_error(MKV_ERR_INVALID_ARGUMENT, "device %d out of range (%d devices)", device, ndev);
   DeviceGuard guard(device);
   if (!guard.ok) return set_error(MKV_ERR_NO_DEVICE, "cannot select device %d", device);
   MKV_CHECK_HIP(hipMalloc(out_dev_ptr, bytes ? bytes : 1));

@@ -582,7 +582,8 @@ def test_device_buffers_and_pool_descriptor_through_the_abi():
     """The backend's device-buffer entry points (mkv_buffer_alloc / free,
     memcpy both ways) round-trip bytes; mkv_pool_get_desc returns the
     descriptor the pool was made from and mkv_pool_buffer its size; NULL
-    outputs and a device that does not exist are refused with a status."""
+    outputs and a device that does not exist are refused with a status, and
+    leave no HIP error for the caller's next check."""
     import ctypes
 
     from mitten_amd import _lib, required_bytes
@@ -602,7 +603,12 @@ def test_device_buffers_and_pool_descriptor_through_the_abi():
     assert lib.mkv_buffer_free(None) == 0
     assert lib.mkv_buffer_alloc(0, 16, None) == dp.MKV_ERR_INVALID_ARGUMENT
     bad = ctypes.c_void_p()
-    assert lib.mkv_buffer_alloc(4096, 16, ctypes.byref(bad)) == dp.MKV_ERR_NO_DEVICE and not bad.value
+    assert lib.mkv_buffer_alloc(4096, 16, ctypes.byref(bad)) == dp.MKV_ERR_INVALID_ARGUMENT and not bad.value
+    assert b"out of range" in lib.mkv_last_error()
+    # A refused call leaves no HIP error behind for the caller's next check.
+    import torch
+
+    assert torch.zeros(4, device="cuda").sum().item() == 0.0
 
     desc = PoolDesc(3, 4, 28, 128, 37, "bf16")
     with DeviceKvPool(desc) as pool:

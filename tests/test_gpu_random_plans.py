@@ -1,7 +1,8 @@
 """Seeded random decode steps through the plan: random head shapes and
 kernels, batch sizes, context lengths (block edges and single tokens
 included), piece counts (0 = the device's choice, one piece, more pieces
-than blocks), the zero sink, and host or device page tables. Each case runs
+than blocks), the zero sink, host or device page tables, and K/V loads
+through the caches or not (MKV_ATTN_CACHED_LOADS). Each case runs
 the fused append + attention step (`mkv_decode_step`) on one layer and checks
 the pool bit for bit and the attention output against the oracle, as the
 engine's decode step (inference-model-qwen/src/model.rs:390-416) computes
@@ -56,15 +57,17 @@ def _case(i: int):
     ctx = _contexts(rng, B)
     total = sum((c + 15) // 16 for c in ctx)
     pieces = [0, 1, int(rng.integers(1, total + 6))][int(rng.integers(3))]
-    return dict(Hq=Hq, Hkv=Hkv, D=D, dt=dt, kernel=kernel, ctx=ctx, pieces=pieces,
-                zero_sink=bool(rng.integers(2)), host_tables=bool(rng.integers(2)), seed=9100 + 10 * i)
+    zero_sink, host_tables = bool(rng.integers(2)), bool(rng.integers(2))
+    return dict(Hq=Hq, Hkv=Hkv, D=D, dt=dt, kernel=kernel, ctx=ctx, pieces=pieces, zero_sink=zero_sink,
+                host_tables=host_tables, cached=bool(rng.integers(2)), seed=9100 + 10 * i)
 
 
 @pytest.mark.parametrize("i", range(N_CASES))
 def test_random_decode_step_matches_the_oracle(i):
     c = _case(i)
     print(f"case {i}: Hq {c['Hq']} Hkv {c['Hkv']} D {c['D']} {c['dt']} kernel {c['kernel']} B {len(c['ctx'])} "
-          f"pieces {c['pieces']} zero_sink {c['zero_sink']} host tables {c['host_tables']}", flush=True)
+          f"pieces {c['pieces']} zero_sink {c['zero_sink']} host tables {c['host_tables']} cached {c['cached']}",
+          flush=True)
     seed, dt = c["seed"], c["dt"]
     batch = wl.decode_batch_from_contexts([x - 1 for x in c["ctx"]], wl.SplitMix64(seed), extra_blocks=2)
     desc = PoolDesc(1, c["Hkv"], c["Hq"], c["D"], batch.num_blocks, dt)
@@ -86,7 +89,7 @@ def test_random_decode_step_matches_the_oracle(i):
             plan = pool.plan(batch.ctx_lens, pieces=c["pieces"])
             tables = tuple(torch.from_numpy(a.astype(np.int32)).cuda() for a in (ip, ids))
         o = pool.decode_step(0, plan, to_device(kn), to_device(vn), to_device(q), *tables,
-                             zero_sink=c["zero_sink"], kernel=c["kernel"])
+                             zero_sink=c["zero_sink"], kernel=c["kernel"], cached_loads=c["cached"])
         pool.check()
         got, after = to_host(o), pool.read()
         plan.close()
