@@ -519,6 +519,11 @@ MKV_API int mkv_validate_copy_pairs(const mkv_pool_desc *desc, const int32_t *sr
 
 /* ---- device buffers (the backend's device-buffer type) ------------------- */
 
+/* hipMalloc on `device` (the backend's device-buffer allocation).
+ * MKV_ERR_NO_DEVICE without a HIP device, MKV_ERR_INVALID_ARGUMENT for a
+ * device index out of range or a NULL out pointer, MKV_ERR_OUT_OF_MEMORY. A
+ * HIP failure returned as a status leaves no HIP error behind for the
+ * caller's next check (true of every entry point). */
 MKV_API int mkv_buffer_alloc(int device, uint64_t bytes, void **out_dev_ptr);
 MKV_API int mkv_buffer_free(void *dev_ptr);
 /* Host -> device on `stream`; the host buffer must stay valid until the
