@@ -144,7 +144,7 @@ def parse():
                          "--prefix tokens; shared: decode step of 256 sequences over a radix-shared "
                          "prefix, with its copy-on-write copies and compaction moves; pressure: "
                          "chunk appends + decode step over a 200 GB pool; small: latency-bound decode "
-                         "steps of 1-8 sequences at Qwen2.5-7B heads")
+                         "steps of 1-12 sequences at Qwen2.5-7B heads")
     ap.add_argument("--extend-seqs", type=int, default=8, help="--op extend: sequences")
     ap.add_argument("--tokens-per-chunk", type=int, default=512, help="--op extend: chunk length")
     ap.add_argument("--prefix", type=int, default=4096, help="--op extend: cached tokens before the chunk")
@@ -1339,12 +1339,12 @@ def _nested(r: dict) -> dict:
     return {k: r[k] for k in keep if k in r}
 
 
-SMALL_BATCHES = [[4096], [8192], [4096] * 4, [2048] * 8, [8192] * 4]
+SMALL_BATCHES = [[4096], [8192], [4096] * 4, [2048] * 8, [8192] * 4, [4096] * 12, [8192] * 8]
 
 
 def bench_small(args):
-    """Decode steps of batches too small to fill the device (1-8 sequences
-    at Qwen2.5-7B heads, bf16): the fused append + attention per layer from a
+    """Decode steps of batches too small to fill the device (1-12 sequences
+    at Qwen2.5-7B heads, bf16; 8 x 8k is the first that fills it): the fused append + attention per layer from a
     plan holding the host tables, as in the headline step. Latency-bound, so
     the figure is microseconds per layer; each batch also reports its K/V
     bytes at that time."""
@@ -1393,7 +1393,7 @@ def bench_small(args):
         "metric": "latency-bound decode step: microseconds per layer", "unit": "us", "higher_is_better": False,
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "dtype": "bf16",
         "data": "synthetic: N(0,1) K/V from a seed in the pool (uninitialised blocks), q and new rows from a seed",
-        "config": {"workload": "decode step (fused append + paged attention + merge) of 1-8 sequences, "
+        "config": {"workload": "decode step (fused append + paged attention + merge) of 1-12 sequences, "
                                "Qwen2.5-7B heads", "layers_timed": 4, "q_heads": Hq, "kv_heads": Hkv,
                    "head_dim": D},
         "batches": rows}), flush=True)

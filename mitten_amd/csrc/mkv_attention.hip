@@ -59,7 +59,8 @@ constexpr int kBlockWeight = 8;    // plan: weight of one block in a piece ...
 constexpr int kSwitchWeight = 12;  // ... and of a sequence start inside it (about 1.5 blocks)
 constexpr int kFirstRoundWeight = 116;  // plan: cap of the first-dispatched pieces, percent
 constexpr int kOddXcdWeight = 96;       // plan: cap of pieces dealt to odd-numbered XCDs, percent
-constexpr int kMinPieceBlocks = 8;      // plan: fewest blocks per piece of a cooperative plan
+constexpr int kMinPieceBlocks = 4;      // plan: fewest blocks per piece of a small cooperative plan ...
+constexpr int kSmallPlanBlocks = 8;     // ... one with fewer blocks than this per resident workgroup
 constexpr int kCoopRing = 3;   // register stages of the cooperative kernel (one less when
                                // its slots carry four Q loads per lane, or at head_dim 256,
                                // where three stages spilled registers)
@@ -558,24 +559,30 @@ __device__ __forceinline__ void run_segment(const KArgs &a, const Seg &sg, int l
   }
 }
 
-// Log-sum-exp merge of n partial rows into row out_row of o: partial s has
-// (m, l) at ml_at(s) and its D floats at o_at(s). Lane s holds partial s's
-// (m, l); lane d holds dims d + 64k of every partial. Up to 16 partials
-// merge in one memory round trip: all their loads are issued before the
-// first use; weights exp2(m_s - M) are broadcast with readlane. More
-// partials take further rounds of 16.
-template <int D, bool BF16, class MlAt, class OAt>
-__device__ __forceinline__ void merge_partials(const KArgs &a, int lane, int n, MlAt ml_at, OAt o_at,
-                                               int64_t out_row) {
-  // Lane owns DPL contiguous dims (one vector load per partial row); all
-  // loads of up to SB partials are issued before their first use.
-  constexpr int DPL = (D + 63) / 64;
+// Log-sum-exp merge of n partial rows: partial s has (m, l) at ml_at(s) and
+// its D floats at o_at(s). Lane s holds partial s's (m, l); lane d holds dims
+// d * DPL .. +DPL of every partial. Up to 16 partials merge in one memory
+// round trip: all their loads are issued before the first use; weights
+// exp2(m_s - M) are broadcast with readlane. More partials take further
+// rounds of 16. Leaves the merged (M, L) (wave-uniform) and the lane's dims
+// of the unnormalised row in acc; n = 0 leaves (-inf, 0, 0).
+template <int D>
+struct MergeVec {
+  static constexpr int DPL = (D + 63) / 64;  // dims per lane (one vector load per partial row)
+  typedef float type __attribute__((ext_vector_type(DPL)));
+};
+
+template <int D, class MlAt, class OAt>
+__device__ __forceinline__ void merge_partials_state(int lane, int n, MlAt ml_at, OAt o_at, float &M, float &L,
+                                                     typename MergeVec<D>::type &acc) {
+  constexpr int DPL = MergeVec<D>::DPL;
   constexpr int SB = 16;
-  typedef float fvec __attribute__((ext_vector_type(DPL)));
+  typedef typename MergeVec<D>::type fvec;
   const int d0 = lane * DPL;
   const bool has = d0 < D;  // D = 32 leaves half the lanes idle
-  fvec acc = {};
-  float M = -INFINITY, L = 0.0f;
+  acc = fvec{};
+  M = -INFINITY;
+  L = 0.0f;
   for (int s0 = 0; s0 < n; s0 += SB) {
     const int cnt = min(SB, n - s0);
     float2 ml = make_float2(-INFINITY, 0.0f);
@@ -603,7 +610,16 @@ __device__ __forceinline__ void merge_partials(const KArgs &a, int lane, int n, 
     }
     M = Mn;
   }
-  if (!has) return;
+}
+
+// Row out_row of o from a merged (M, L, acc): the lane's DPL dims.
+template <int D, bool BF16>
+__device__ __forceinline__ void store_merged_row(const KArgs &a, int lane, float M, float L,
+                                                 const typename MergeVec<D>::type &acc, int64_t out_row) {
+  constexpr int DPL = MergeVec<D>::DPL;
+  typedef typename MergeVec<D>::type fvec;
+  const int d0 = lane * DPL;
+  if (d0 >= D) return;
   const float f = final_scale(M, L, a.zero_sink);
   if constexpr (BF16) {
     uint16_t *op = reinterpret_cast<uint16_t *>(a.o) + out_row * D + d0;
@@ -619,6 +635,15 @@ __device__ __forceinline__ void merge_partials(const KArgs &a, int lane, int n, 
   } else {
     *reinterpret_cast<fvec *>(reinterpret_cast<float *>(a.o) + out_row * D + d0) = acc * f;
   }
+}
+
+template <int D, bool BF16, class MlAt, class OAt>
+__device__ __forceinline__ void merge_partials(const KArgs &a, int lane, int n, MlAt ml_at, OAt o_at,
+                                               int64_t out_row) {
+  float M, L;
+  typename MergeVec<D>::type acc;
+  merge_partials_state<D>(lane, n, ml_at, o_at, M, L, acc);
+  store_merged_row<D, BF16>(a, lane, M, L, acc, out_row);
 }
 
 // Partials ws[base + s*stride], s < n, of the kernel's workspace.
@@ -1842,6 +1867,57 @@ __global__ void __launch_bounds__(256) merge_planned_kernel(KArgs a, PlanDev pd)
                       (int64_t)b * a.Hq + hq);
 }
 
+// A sequence cut into many pieces (a batch too small to fill the device with
+// long pieces): one workgroup per (sequence, query head) row, wave w merging
+// the w-th share of the row's partials (one round of loads each), the waves'
+// states combined in LDS by wave 0. The grid is n_merge * Hq.
+constexpr int kWideMergeWaves = 8;
+constexpr int kWideMergeMin = 16;  // partials per row above which the wide merge runs (one round of merge_rows)
+
+template <int D, bool BF16>
+__global__ void __launch_bounds__(64 * kWideMergeWaves) merge_wide_kernel(KArgs a, PlanDev pd) {
+  constexpr int DPL = MergeVec<D>::DPL;
+  typedef typename MergeVec<D>::type fvec;
+  __shared__ float part[kWideMergeWaves][2 + 64 * DPL];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t row = blockIdx.x;
+  const int b = pd.merge_seqs[row / a.Hq];
+  const int hq = (int)(row % a.Hq);
+  const int n = pd.seq_npiece[b];
+  const int s0 = (int)((int64_t)n * wave / kWideMergeWaves);
+  const int s1 = (int)((int64_t)n * (wave + 1) / kWideMergeWaves);
+  // Partial s of the row at workspace row (seq_piece0[b] + b + s) * Hq + hq.
+  const int64_t base = ((int64_t)pd.seq_piece0[b] + b + s0) * a.Hq + hq;
+  float M, L;
+  fvec acc;
+  merge_partials_state<D>(
+      lane, s1 - s0, [&](int s) { return a.ws_ml + 2 * (base + (int64_t)s * a.Hq); },
+      [&](int s) { return a.ws_o + (base + (int64_t)s * a.Hq) * D; }, M, L, acc);
+  if (lane == 0) {
+    part[wave][0] = M;
+    part[wave][1] = L;
+  }
+#pragma unroll
+  for (int k = 0; k < DPL; k++) part[wave][2 + lane * DPL + k] = acc[k];
+  __syncthreads();
+  if (wave != 0) return;
+  float Mx = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kWideMergeWaves; w++) Mx = fmaxf(Mx, part[w][0]);
+  float Lx = 0.0f;
+  fvec ax = fvec{};
+#pragma unroll
+  for (int w = 0; w < kWideMergeWaves; w++) {
+    const float mw = part[w][0];
+    const float f = mw == -INFINITY ? 0.0f : fast_exp2(mw - Mx);  // an empty share adds nothing
+    Lx = fmaf(part[w][1], f, Lx);
+#pragma unroll
+    for (int k = 0; k < DPL; k++) ax[k] = fmaf(part[w][2 + lane * DPL + k], f, ax[k]);
+  }
+  store_merged_row<D, BF16>(a, lane, Mx, Lx, ax, (int64_t)b * a.Hq + hq);
+}
+
 // Decode over a shared prefix: row (sequence b, query head hq) merges b's
 // suffix partials (one per piece, in the plan's workspace, as
 // merge_planned_kernel reads them) with the prefix's S key-range partials
@@ -2016,6 +2092,7 @@ struct Plan {
   int32_t n_prefix = 0;       // shared-prefix ids given at build time (0: none)
   bool all_partial = false;   // every sequence stores partials (built for a shared prefix's suffixes)
   bool beside = false;        // suffix pieces sized to run beside the prefix tiles (one per CU)
+  int32_t max_npiece = 0;     // most pieces any merged sequence spans
   int32_t valu_qc = kQChunkValu;  // query heads per wave when the per-head (VALU) kernel runs the plan
   int64_t tokens = 0;         // sum of the context lengths
   int32_t max_ctx = 0;        // the longest context
@@ -2355,11 +2432,18 @@ static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t 
   const bool beside = !pieces && all_partial && prefix_beside(pl->pool);
   const int64_t resident = pieces ? 0 : beside ? device_cus(pl->pool) : coop_resident(pl->pool);
   int64_t P = pieces ? pieces : resident ? resident : std::max<int64_t>(1, 2048 / std::max(1, g.Hkv * nqc));
-  // A batch too small to fill the resident workgroups with long pieces is
-  // latency-bound: pieces of one or two blocks would only add partials for
-  // the merge to read back (up to hundreds per sequence, 16 per round).
-  // Cooperative plans keep at least kMinPieceBlocks blocks per piece there.
-  if (!pieces && resident > 0) P = std::min<int64_t>(P, std::max<int64_t>(1, (total + kMinPieceBlocks - 1) / kMinPieceBlocks));
+  // A batch too small to give every resident workgroup kSmallPlanBlocks
+  // blocks is latency-bound. Its cooperative plan takes at most one piece per
+  // CU (a second workgroup on a CU only competes for it) and at least
+  // kMinPieceBlocks blocks per piece (shorter ones only add partials for the
+  // merge to read back). Batches of 1-8 sequences at Qwen2.5-7B heads,
+  // us per layer: 1 x 4k 17.3 -> 14.6, 1 x 8k 19.5 -> 14.7, 8 x 2k 17.1 ->
+  // 15.1 (with the wide merge for rows of many partials).
+  if (!pieces && resident > 0 && total < resident * kSmallPlanBlocks) {
+    const int cus = device_cus(pl->pool);
+    if (cus > 0) P = std::min<int64_t>(P, cus);
+    P = std::min<int64_t>(P, std::max<int64_t>(1, (total + kMinPieceBlocks - 1) / kMinPieceBlocks));
+  }
   P = std::max<int64_t>(P, (total + 63) / 64);  // a piece is at most 64 blocks (one per lane)
   P = std::min<int64_t>(P, total);
   std::vector<int32_t> blk0v(num_seqs + 1);
@@ -2387,8 +2471,8 @@ static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t 
   // resident pieces the odd-numbered XCDs finish last: per-workgroup stamps
   // on every box measured put their last workgroups about 5 us (6%) after
   // the even XCDs'. Pieces with an odd index, dealt to those XCDs, get
-  // kOddXcdWeight percent of the cap (C2 72.7 -> 73.4% of peak, Gemma-2B
-  // MQA 72.3 -> 73.3%). Launches of several rounds, whose freed slots take
+  // kOddXcdWeight percent of the cap (the 28-layer Qwen2.5-7B step of 64
+  // sequences 72.7 -> 73.4% of peak, Gemma-2B MQA 72.3 -> 73.3%). Launches of several rounds, whose freed slots take
   // the next piece whatever its XCD, keep equal caps.
   const bool odd_light = !pieces && resident > 0 && P == resident;
   auto cut = [&](int64_t cap) {
@@ -2475,9 +2559,12 @@ static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t 
     spiece0[b] = q;
     snpiece[b] = last - q + 1;
   }
-  int n_merge = 0;
+  int n_merge = 0, max_npiece = 0;
   for (int32_t b = 0; b < num_seqs; b++)
-    if (snpiece[b] > 1 || all_partial) mseq[n_merge++] = b;
+    if (snpiece[b] > 1 || all_partial) {
+      mseq[n_merge++] = b;
+      max_npiece = std::max(max_npiece, snpiece[b]);
+    }
   int32_t *tok0 = mseq + n_merge, *fseq = tok0 + num_seqs + 1, *fmeta = fseq + total;
   // Gather rows: sequence b's tokens start after the earlier contexts
   // (clamped where they pass 2^31 - 1: the fused gather then refuses the plan).
@@ -2551,6 +2638,7 @@ static int plan_build(mkv_decode_plan *plan, const int32_t *h_ctx_lens, int32_t 
   pl->BP = (int32_t)BP;
   pl->total = (int32_t)total;
   pl->n_merge = n_merge;
+  pl->max_npiece = max_npiece;
   pl->all_partial = all_partial;
   pl->beside = beside;
   pl->valu_qc = valu_qc;
@@ -2736,9 +2824,20 @@ static int launch_planned(Pool *p, const Plan *pl, int32_t layer, const void *d_
   }
   if (ev_end) MKV_CHECK_HIP(hipEventRecord(ev_end, hs));
   if (pl->n_merge && merge && !merged) {
-    const int64_t mwgs = ((int64_t)pl->n_merge * g.Hq + 3) / 4;
-    MKV_DISPATCH_MERGE(merge_planned_kernel, dim3((unsigned)mwgs), dim3(256), hs, a, pd);
-    MKV_CHECK_LAUNCH("merge_planned_kernel");
+    // Rows of many partials spread over 8 waves, where the rows are few (at
+    // most two per CU): with thousands of rows (64 sequences at Qwen2.5-7B
+    // heads have 1,792, 446 cut sequences 12,488) the eightfold waves cost
+    // more than the rounds they save (2.80 -> 2.97 ms per 28-layer step).
+    const int64_t rows = (int64_t)pl->n_merge * g.Hq;
+    const int cus = device_cus(p);
+    if (pl->max_npiece > kWideMergeMin && cus > 0 && rows <= 2 * (int64_t)cus) {
+      MKV_DISPATCH_MERGE(merge_wide_kernel, dim3((unsigned)rows), dim3(64 * kWideMergeWaves), hs, a, pd);
+      MKV_CHECK_LAUNCH("merge_wide_kernel");
+    } else {
+      const int64_t mwgs = ((int64_t)pl->n_merge * g.Hq + 3) / 4;
+      MKV_DISPATCH_MERGE(merge_planned_kernel, dim3((unsigned)mwgs), dim3(256), hs, a, pd);
+      MKV_CHECK_LAUNCH("merge_planned_kernel");
+    }
   }
   if (gather && !fused_gather)
     return mkv_gather(reinterpret_cast<mkv_pool *>(p), layer, d_block_indptr, d_block_ids, pd.tok0, pl->B,

@@ -621,3 +621,39 @@ def test_device_buffers_and_pool_descriptor_through_the_abi():
         base = ctypes.c_void_p()
         assert lib.mkv_pool_buffer(pool._h, ctypes.byref(base), ctypes.byref(size)) == 0
         assert size.value == required_bytes(desc) and base.value == pool.data_ptr
+
+
+@pytest.mark.parametrize("ctx,pieces,zero_sink", [([4096], 0, False), ([4096], 0, True), ([700, 1900, 64], 0, False),
+                                                  ([700, 1900, 64], 166, True), ([1024] * 4, 256, False)])
+def test_rows_of_many_partials_merge_over_waves(ctx, pieces, zero_sink):
+    """A small batch cut into many short pieces (the device's choice: pieces of
+    4 blocks, at most one per CU; or an explicit count) leaves rows of more
+    than 16 partials, which the merge spreads over 8 waves and combines in
+    LDS. Fused step vs the oracle at Qwen2.5-7B heads."""
+    import torch
+
+    Hq, Hkv, D = 28, 4, 128
+    seed = 71 + len(ctx) + pieces
+    batch = wl.decode_batch_from_contexts([c - 1 for c in ctx], wl.SplitMix64(seed), extra_blocks=2)
+    desc = PoolDesc(1, Hkv, Hq, D, batch.num_blocks, "bf16")
+    host = normal(seed + 1, desc.shape, "bf16")
+    B = len(ctx)
+    q = normal(seed + 2, (B, Hq, D), "bf16")
+    kn, vn = normal(seed + 3, (B, Hkv, D), "bf16"), normal(seed + 4, (B, Hkv, D), "bf16")
+    with DeviceKvPool(desc) as pool:
+        pool.write(host)
+        plan = pool.plan(batch.ctx_lens, pieces=pieces)
+        info = plan.info()
+        most = max(-(-c // 16) for c in ctx) / max(info["blocks_per_piece"], 1)
+        assert most > 16, info  # some row has more partials than one round of the narrow merge
+        o = pool.decode_step(0, plan, to_device(kn), to_device(vn), to_device(q), _i32(batch.block_indptr),
+                             _i32(batch.block_ids), zero_sink=zero_sink)
+        pool.check()
+        got, after = to_host(o), pool.read()
+        plan.close()
+    want = host.copy()
+    assert orc.append(odesc(desc), want, 0, kn, vn, batch.slot_mapping) == -1
+    assert np.array_equal(bits(after), bits(want))
+    ref = orc.decode_attention(odesc(desc), want, 0, widen(q), batch.block_indptr, batch.block_ids, batch.ctx_lens,
+                               zero_sink=zero_sink)
+    assert_attention_close(got, ref, "bf16")
