@@ -380,7 +380,10 @@ __device__ __forceinline__ void load_chunk(const uint8_t *p, float (&f)[VEC]) {
   }
 }
 
-template <int D, bool BF16, int QC>
+// BATCHED: the U tokens of a lane's batch are scored first and enter the
+// online softmax together (one rescale and U + 1 exponentials per query head,
+// not 2U of each), at the cost of holding their V rows.
+template <int D, bool BF16, int QC, bool BATCHED = false>
 __device__ __forceinline__ void valu_segment(const KArgs &a, const Seg &sg, int lane, VState<D, BF16, QC> &st) {
   using T = VTraits<D, BF16>;
   constexpr int ES = T::ES, VEC = T::VEC, LPT = T::LPT, TPI = T::TPI;
@@ -438,6 +441,65 @@ __device__ __forceinline__ void valu_segment(const KArgs &a, const Seg &sg, int 
   auto consume = [&](const u32x4 (&kd)[U], const u32x4 (&vd)[U], bool okb, int bi) {
     if (!okb && lane == 0) record_error(a.d_err, MKV_DEVERR_BLOCK);
     const int tb = t_begin + bi * BT;
+    if constexpr (BATCHED) {
+      float vfu[U][VEC], su[U][QC];
+      bool vu[U];
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const int t = tb + u * TPI + lt;
+        vu[u] = okb && t < t_end;
+        if (a.gk && sg.qc == 0 && vu[u]) {  // fused gather: the row as read (the new row from its input)
+          const int64_t go = ((sg.gtok * a.Hkv + (int64_t)sg.h * sg.ctx + t) * D) * ES + ld * 16;
+          *reinterpret_cast<u32x4 *>(a.gk + go) = kd[u];
+          *reinterpret_cast<u32x4 *>(a.gv + go) = vd[u];
+        }
+        float kf[VEC];
+        if constexpr (BF16) {
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            kf[2 * e] = bf16_lo(kd[u][e]), kf[2 * e + 1] = bf16_hi(kd[u][e]);
+            vfu[u][2 * e] = bf16_lo(vd[u][e]), vfu[u][2 * e + 1] = bf16_hi(vd[u][e]);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; e++) kf[e] = __uint_as_float(kd[u][e]), vfu[u][e] = __uint_as_float(vd[u][e]);
+        }
+#pragma unroll
+        for (int g = 0; g < QC; g++) {
+          if (g >= nq) break;
+          float sc = 0.0f;
+#pragma unroll
+          for (int e = 0; e < VEC; e++) sc = fmaf(qv[g][e], kf[e], sc);
+          su[u][g] = row_sum<LPT>(sc);  // DPP steps within the token's lanes (no LDS round trips)
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < QC; g++) {
+        if (g >= nq) break;
+        float mx = st.m[g];
+#pragma unroll
+        for (int u = 0; u < U; u++)
+          if (vu[u]) mx = fmaxf(mx, su[u][g]);
+        if (mx == -INFINITY) continue;  // nothing visible yet
+        const float al = st.m[g] == -INFINITY ? 0.0f : fast_exp2(st.m[g] - mx);
+        float pu[U], lsum = 0.0f;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+          pu[u] = vu[u] ? fast_exp2(su[u][g] - mx) : 0.0f;
+          lsum += pu[u];
+        }
+        st.l[g] = fmaf(st.l[g], al, lsum);
+#pragma unroll
+        for (int e = 0; e < VEC; e++) {
+          float acc = st.acc[g][e] * al;
+#pragma unroll
+          for (int u = 0; u < U; u++) acc = fmaf(pu[u], vfu[u][e], acc);
+          st.acc[g][e] = acc;
+        }
+        st.m[g] = mx;
+      }
+      return;
+    }
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int t = tb + u * TPI + lt;
@@ -1046,7 +1108,7 @@ __global__ void __launch_bounds__(64 * kSeqWaves) attn_seq_kernel(KArgs a, PlanD
   }
   if (a.gk) sg.gtok = a.gtok0[b];
   VState<D, BF16, QC> st;
-  valu_segment<D, BF16, QC>(a, sg, lane, st);  // an empty share leaves m = -inf, l = 0, row 0
+  valu_segment<D, BF16, QC, true>(a, sg, lane, st);  // an empty share leaves m = -inf, l = 0, row 0
   const int q0 = sg.qc * QC;
   const int nq = min(QC, a.G - q0);
   if (lane < LPT) {
