@@ -322,11 +322,11 @@ def test_decode_step_fused_append(shape, kernel, pieces):
 @pytest.mark.parametrize("ctx", [PLAN_CTX, [480 + 7 * i for i in range(40)]])
 @pytest.mark.parametrize("shape,kernel", [("qwen0.5b-f32", None), ("qwen0.5b-bf16", "valu")])
 def test_per_head_kernel_small_and_wide_query_chunks(shape, kernel, ctx):
-    """The per-head kernel takes 2 query heads per wave for a launch with
+    """The per-head kernel takes 1 query head per wave for a launch with
     fewer (block, KV head) units than two per CU (PLAN_CTX: 191 blocks x 2
     heads) and 8 per wave otherwise (40 sequences of ~600 tokens: ~1,500 x 2).
-    Both, with G = 7 (chunks 2, 2, 2, 1 and 7), fused append included, against
-    the oracle."""
+    Both, with G = 7 (seven chunks of 1, and one of 7), fused append
+    included, against the oracle."""
     got, ref, dt, after, want, info = _planned_case(shape, ctx, 62, kernel=kernel, fused=True)
     assert np.array_equal(bits(after), bits(want)), "fused append is not bit-exact"
     assert_attention_close(got, ref, dt)
@@ -338,7 +338,7 @@ def test_per_head_kernel_small_and_wide_query_chunks(shape, kernel, ctx):
 def test_per_head_kernel_query_chunks_every_head_dim(shape, kernel, small):
     """Both query-chunk widths of the per-head kernel at head_dim 32, 128 and
     256 (f32, and bf16 forced onto it): a few short sequences (under two
-    (block, KV head) units per CU: 2 heads per wave) and forty of ~600 tokens
+    (block, KV head) units per CU: 1 head per wave) and forty of ~600 tokens
     (8 per wave), fused append included, against the oracle."""
     ctx = [1, 17, 40, 100, 33] if small else [480 + 7 * i for i in range(40)]
     got, ref, dt, after, want, info = _planned_case(shape, ctx, 63, kernel=kernel, fused=True)

@@ -1,7 +1,7 @@
 """Seeded random decode steps small enough to take the per-sequence kernel:
 the per-head (VALU) path (f32 pools, or bf16 with kernel "valu") on fewer
 (block, KV head) units than two per CU, where one workgroup per (sequence, KV
-head, query-head pair) merges its waves' states in LDS and no merge launch
+head, query head) merges its waves' states in LDS and no merge launch
 follows. Random head shapes, 1-8 sequences, contexts from one token to the
 size limit, piece counts, the zero sink, host or device tables, and the
 fused block-table gather (the engine's small-model step,
